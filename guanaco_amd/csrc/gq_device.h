@@ -1,0 +1,78 @@
+/*
+ * gq_device.h — gfx950 device helpers shared by the decode kernels.
+ *
+ * Wave64 reductions use DPP row operations (a 16-lane row reduces with
+ * row_ror:8, row_ror:4 and two quad permutes, all folded into the VALU add)
+ * and two cross-row exchanges.  Block loads are 16-byte vector loads where
+ * the K-quant layout is 16-byte aligned (Q4_K) and dword loads funnel-shifted
+ * with v_alignbyte where it is only 2-byte aligned (Q6_K: 210-byte blocks,
+ * Q8_0: 34-byte blocks).
+ */
+#ifndef GQ_DEVICE_H
+#define GQ_DEVICE_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define GQ_WAVE 64
+
+typedef uint32_t gq_u32x3 __attribute__((ext_vector_type(3), aligned(4)));
+
+__device__ __forceinline__ float gq_h2f(uint32_t h16) {
+  return (float)__builtin_bit_cast(_Float16, (unsigned short)(h16 & 0xffffu));
+}
+
+/* DPP move helpers: compile-time control words (gfx9 encoding). */
+template <int CTRL>
+__device__ __forceinline__ float gq_dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                0xf, 0xf, false));
+}
+
+/* Sum over each 16-lane row; every lane of the row receives the row sum. */
+__device__ __forceinline__ float gq_row16_sum(float v) {
+  v += gq_dpp<0x128>(v); /* row_ror:8 */
+  v += gq_dpp<0x124>(v); /* row_ror:4 */
+  v += gq_dpp<0x4e>(v);  /* quad_perm [2,3,0,1] */
+  v += gq_dpp<0xb1>(v);  /* quad_perm [1,0,3,2] */
+  return v;
+}
+
+/* Sum over groups of 8 lanes (lanes 8k..8k+7); every lane receives it. */
+__device__ __forceinline__ float gq_row8_sum(float v) {
+  v += gq_dpp<0x141>(v); /* row_half_mirror: lane i <-> 7-i within 8 */
+  v += gq_dpp<0x4e>(v);
+  v += gq_dpp<0xb1>(v);
+  return v;
+}
+
+/* Full wave64 sum; every lane receives it. */
+__device__ __forceinline__ float gq_wave_sum(float v) {
+  v = gq_row16_sum(v);
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+__device__ __forceinline__ float gq_wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+/* Two dwords starting at a 2-byte-aligned address: one 12-byte dword-aligned
+ * load and two v_alignbyte funnel shifts.  Reads at most 4 bytes past the
+ * 8 requested (callers keep that inside the block). */
+__device__ __forceinline__ uint2 gq_load8_a2(const uint8_t *p) {
+  const uintptr_t a = (uintptr_t)p;
+  const gq_u32x3 w = *(const gq_u32x3 *)(a & ~(uintptr_t)3);
+  const uint32_t sh = (uint32_t)(a & 3u);
+  uint2 r;
+  r.x = __builtin_amdgcn_alignbyte(w.y, w.x, sh);
+  r.y = __builtin_amdgcn_alignbyte(w.z, w.y, sh);
+  return r;
+}
+
+__device__ __forceinline__ uint32_t gq_byte(uint32_t w, int k) { return (w >> (8 * k)) & 0xffu; }
+
+#endif

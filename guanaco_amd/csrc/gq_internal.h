@@ -1,0 +1,88 @@
+/*
+ * gq_internal.h — launchers shared between the translation units of
+ * libgq_hip.so (not part of the C ABI).
+ */
+#ifndef GQ_INTERNAL_H
+#define GQ_INTERNAL_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/gq_hip.h"
+
+/* ---- quantised matvec ----------------------------------------------------
+ * One launch computes up to three row segments of the same dtype and shared
+ * input x (e.g. the q and k projections), with optional fused prologue and
+ * epilogue:
+ *   prologue: x <- RMSNorm(x) * norm_w (when norm_w != NULL)
+ *   MV_STORE:  y = W x
+ *   MV_RESID:  y = r + W x            (r may alias y)
+ *   MV_SWIGLU: seg[0] = gate, seg[1] = up (same rows);
+ *              seg[0].y = silu(W_g x) * (W_u x)
+ */
+enum { MV_STORE = 0, MV_RESID = 1, MV_SWIGLU = 2 };
+
+struct MvSeg {
+  const uint8_t *w;
+  float *y;
+  const float *r;
+  int rows;
+};
+
+struct MvArgs {
+  MvSeg seg[3];
+  int nseg;
+  int cols;
+  const float *x;
+  const float *norm_w;
+  float eps;
+};
+
+int gq_launch_matvec(int dtype, int mode, const MvArgs &a, hipStream_t s);
+
+/* ---- attention -------------------------------------------------------- */
+struct AttnArgs {
+  const float *q;   /* n_heads x hd (already rotated) */
+  const float *k;   /* layer K slab [n_kv][max_seq][hd] */
+  const float *v;
+  float *part_o;    /* [n_heads][nch][hd] */
+  float *part_ml;   /* [n_heads][nch][2] */
+  float *out;       /* n_heads x hd */
+  const int *pos_dev; /* position read on the device when not NULL */
+  int pos;
+  int n_heads, n_kv, hd, max_seq, nch, s_max;
+  float scale;
+};
+int gq_attn_nch(int n_kv, int max_seq);
+int gq_attn_smax(int max_seq, int nch);
+int gq_launch_attention(const AttnArgs &a, hipStream_t s, hipEvent_t mid);
+
+struct RopeArgs {
+  float *q;
+  const float *k, *v;
+  float *kc, *vc;      /* layer slabs */
+  const float2 *cs;    /* rope table [max_seq][hd/2] (cos, sin) */
+  const int *pos_dev;
+  int pos;
+  int n_heads, n_kv, hd, max_seq;
+};
+int gq_launch_rope_append(const RopeArgs &a, hipStream_t s);
+
+/* ---- misc -------------------------------------------------------------- */
+int gq_launch_rmsnorm(const float *x, const float *w, float *out, int dim, float eps,
+                      hipStream_t s);
+int gq_launch_embed(int dtype, const void *table, int hidden, const int *token_dev, int token,
+                    float *out, hipStream_t s);
+/* argmax of x[n] (ties -> lowest index) -> *out_index; when step_dev != NULL
+ * also stores the index at tokens[*step_dev], then ++*step_dev and
+ * ++*pos_dev (the decode-loop bookkeeping of one graph replay). */
+int gq_launch_argmax(const float *x, int n, float *scratch, int nblk, int *out_index,
+                     int *tokens, int *step_dev, int *pos_dev, hipStream_t s);
+int gq_argmax_blocks(int n);
+int gq_launch_silu_mul(float *gate, const float *up, int n, hipStream_t s);
+int gq_launch_synth_quant(void *dev, int dtype, int rows, int cols, uint64_t seed, hipStream_t s);
+int gq_launch_synth_normal(float *dev, size_t n, uint64_t seed, int norm_weight, hipStream_t s);
+int gq_launch_synth_kv(float *slab, int n_layers, int n_kv, int hd, int max_seq, int n_pos,
+                       uint64_t seed, hipStream_t s);
+
+#endif

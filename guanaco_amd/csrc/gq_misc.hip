@@ -1,0 +1,224 @@
+/*
+ * gq_misc.hip — small decode-step kernels: RMSNorm, embedding-row dequant,
+ * greedy argmax (with the decode loop's device-side bookkeeping), SiLU*up,
+ * and the device fills of the synthetic-input generator (gq_synth.h).
+ */
+#include "gq_device.h"
+#include "gq_internal.h"
+#include "gq_synth.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+/* out = w * (x * 1/sqrt(mean(x^2) + eps)) (kernels_cpu.c:199-265); one
+ * workgroup, sum of squares in a fixed tree order. */
+__global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *x, const float *w, float *out,
+                                                          int dim, float eps) {
+  __shared__ float red[kThreads / GQ_WAVE];
+  const int tid = threadIdx.x;
+  float ss = 0.f;
+  for (int i = tid; i < dim; i += kThreads) ss = __builtin_fmaf(x[i], x[i], ss);
+  ss = gq_wave_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  float tot = (red[0] + red[1]) + (red[2] + red[3]);
+  tot = tot / (float)dim;
+  tot = tot + eps;
+  const float r = 1.0f / sqrtf(tot);
+  for (int i = tid; i < dim; i += kThreads) out[i] = (w ? w[i] : 1.0f) * (x[i] * r);
+}
+
+/* Embedding row of `token` (engine.c:214-283): F32 copy, Q8_0 q*scale,
+ * Q4_K (d*sc)*q - dmin*m with separate roundings. */
+__global__ __launch_bounds__(kThreads) void embed_kernel(int dtype, const uint8_t *table, int hidden,
+                                                        const int *token_dev, int token, float *out) {
+#pragma clang fp contract(off)
+  const int tok = token_dev ? *token_dev : token;
+  for (int e = threadIdx.x; e < hidden; e += kThreads) {
+    float v;
+    if (dtype == GQ_F32) {
+      v = ((const float *)table)[(size_t)tok * hidden + e];
+    } else if (dtype == GQ_Q8_0) {
+      const uint8_t *blk = table + ((size_t)tok * (hidden / 32) + e / 32) * 34;
+      v = (float)(int8_t)blk[2 + (e & 31)] * gq_h2f(blk[0] | (blk[1] << 8));
+    } else {
+      const uint8_t *blk = table + ((size_t)tok * (hidden / 256) + e / 256) * 144;
+      const int u = e & 255, cc = u >> 6, o = u & 63;
+      const int j = 2 * cc + (o >= 32);
+      const uint8_t *s = blk + 4;
+      int sc, m;
+      if (j < 4) {
+        sc = s[j] & 63, m = s[j + 4] & 63;
+      } else {
+        sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
+        m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+      }
+      const uint8_t qb = blk[16 + 32 * cc + (o & 31)];
+      const int q = o < 32 ? (qb & 15) : (qb >> 4);
+      const float d = gq_h2f(blk[0] | (blk[1] << 8)), dm = gq_h2f(blk[2] | (blk[3] << 8));
+      const float d1 = d * (float)sc, m1 = dm * (float)m;
+      v = d1 * (float)q - m1;
+    }
+    out[e] = v;
+  }
+}
+
+/* (value, index) reduction, ties to the lower index (tokenizer.c:175-185). */
+__device__ __forceinline__ void better(float &v, int &i, float v2, int i2) {
+  if (v2 > v || (v2 == v && i2 < i)) v = v2, i = i2;
+}
+
+__device__ __forceinline__ void block_argmax(float &v, int &i) {
+  __shared__ float sv[kThreads / GQ_WAVE];
+  __shared__ int si[kThreads / GQ_WAVE];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float v2 = __shfl_xor(v, o, 64);
+    const int i2 = __shfl_xor(i, o, 64);
+    better(v, i, v2, i2);
+  }
+  const int tid = threadIdx.x;
+  if ((tid & 63) == 0) sv[tid >> 6] = v, si[tid >> 6] = i;
+  __syncthreads();
+  v = sv[0], i = si[0];
+  for (int w = 1; w < kThreads / GQ_WAVE; w++) better(v, i, sv[w], si[w]);
+}
+
+constexpr int kArgmaxPerBlock = 4096;
+
+__global__ __launch_bounds__(kThreads) void argmax_stage1(const float *x, int n, float *scratch) {
+  const int base = blockIdx.x * kArgmaxPerBlock;
+  const int end = min(n, base + kArgmaxPerBlock);
+  float v = -INFINITY;
+  int i = 0x7fffffff;
+  for (int e = base + threadIdx.x; e < end; e += kThreads) better(v, i, x[e], e);
+  block_argmax(v, i);
+  if (threadIdx.x == 0) {
+    scratch[2 * blockIdx.x] = v;
+    scratch[2 * blockIdx.x + 1] = __int_as_float(i);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void argmax_stage2(const float *scratch, int nblk, int *out,
+                                                         int *tokens, int *step_dev, int *pos_dev) {
+  float v = -INFINITY;
+  int i = 0x7fffffff;
+  for (int b = threadIdx.x; b < nblk; b += kThreads)
+    better(v, i, scratch[2 * b], __float_as_int(scratch[2 * b + 1]));
+  block_argmax(v, i);
+  if (threadIdx.x == 0) {
+    if (i == 0x7fffffff) i = 0; /* all NaN: the reference keeps index 0 */
+    *out = i;
+    if (step_dev) {
+      tokens[*step_dev] = i;
+      *step_dev += 1;
+      *pos_dev += 1;
+    }
+  }
+}
+
+__global__ void silu_mul_kernel(float *gate, const float *up, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) {
+    const float g = gate[i];
+    const float sig = 1.0f / (1.0f + expf(0.0f - g));
+    gate[i] = (g * sig) * up[i];
+  }
+}
+
+/* ---- synthetic fills: one thread per 4 output bytes / one float ---- */
+__global__ void synth_quant_kernel(uint8_t *out, int dtype, size_t nbytes, int bb, uint64_t seed) {
+  const size_t i4 = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i4 >= nbytes) return;
+  uint32_t word = 0;
+  for (int k = 0; k < 4 && i4 + k < nbytes; k++) {
+    const size_t i = i4 + k;
+    const uint64_t b = i / (size_t)bb;
+    const uint32_t o = (uint32_t)(i - b * bb);
+    const uint8_t v = dtype == GQ_Q4_K ? gq_q4k_byte(seed, b, o)
+                      : dtype == GQ_Q6_K ? gq_q6k_byte(seed, b, o)
+                                         : gq_q8_0_byte(seed, b, o);
+    word |= (uint32_t)v << (8 * k);
+  }
+  if (i4 + 4 <= nbytes) {
+    *(uint32_t *)(out + i4) = word;
+  } else {
+    for (int k = 0; i4 + k < nbytes; k++) out[i4 + k] = (uint8_t)(word >> (8 * k));
+  }
+}
+
+__global__ void synth_normal_kernel(float *out, size_t n, uint64_t seed, int norm_weight) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = norm_weight ? gq_norm_weight(seed, i) : gq_normal(seed, i);
+}
+
+__global__ void synth_kv_kernel(float *slab, int n_kv, int hd, int max_seq, int n_pos, uint64_t seed) {
+  /* blockIdx.y = layer * n_kv + head; x covers n_pos * hd elements */
+  const int lh = blockIdx.y;
+  const int layer = lh / n_kv, h = lh - layer * n_kv;
+  const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= (size_t)n_pos * hd) return;
+  const int p = (int)(e / hd), d = (int)(e - (size_t)p * hd);
+  slab[((size_t)lh * max_seq + p) * hd + d] = gq_normal(seed, gq_kv_index(layer, n_kv, h, p, hd, d));
+}
+
+} // namespace
+
+int gq_launch_rmsnorm(const float *x, const float *w, float *out, int dim, float eps, hipStream_t s) {
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(kThreads), 0, s, x, w, out, dim, eps);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+int gq_launch_embed(int dtype, const void *table, int hidden, const int *token_dev, int token,
+                    float *out, hipStream_t s) {
+  if (dtype != GQ_F32 && dtype != GQ_Q8_0 && dtype != GQ_Q4_K) return -1;
+  hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(kThreads), 0, s, dtype, (const uint8_t *)table,
+                     hidden, token_dev, token, out);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+int gq_argmax_blocks(int n) { return (n + kArgmaxPerBlock - 1) / kArgmaxPerBlock; }
+
+int gq_launch_argmax(const float *x, int n, float *scratch, int nblk, int *out_index, int *tokens,
+                     int *step_dev, int *pos_dev, hipStream_t s) {
+  if (n <= 0 || nblk != gq_argmax_blocks(n)) return -1;
+  hipLaunchKernelGGL(argmax_stage1, dim3(nblk), dim3(kThreads), 0, s, x, n, scratch);
+  hipLaunchKernelGGL(argmax_stage2, dim3(1), dim3(kThreads), 0, s, scratch, nblk, out_index, tokens,
+                     step_dev, pos_dev);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+int gq_launch_silu_mul(float *gate, const float *up, int n, hipStream_t s) {
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((n + 255) / 256), dim3(256), 0, s, gate, up, n);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+int gq_launch_synth_quant(void *dev, int dtype, int rows, int cols, uint64_t seed, hipStream_t s) {
+  int qk, bb;
+  if (dtype == GQ_Q4_K) qk = 256, bb = 144;
+  else if (dtype == GQ_Q6_K) qk = 256, bb = 210;
+  else if (dtype == GQ_Q8_0) qk = 32, bb = 34;
+  else return -1;
+  if (cols % qk) return -2;
+  const size_t nbytes = (size_t)rows * (cols / qk) * bb;
+  const size_t threads = (nbytes + 3) / 4;
+  hipLaunchKernelGGL(synth_quant_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
+                     (uint8_t *)dev, dtype, nbytes, bb, seed);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+int gq_launch_synth_normal(float *dev, size_t n, uint64_t seed, int norm_weight, hipStream_t s) {
+  hipLaunchKernelGGL(synth_normal_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, dev, n,
+                     seed, norm_weight);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+int gq_launch_synth_kv(float *slab, int n_layers, int n_kv, int hd, int max_seq, int n_pos,
+                       uint64_t seed, hipStream_t s) {
+  if (n_pos <= 0) return 0;
+  const size_t per = (size_t)n_pos * hd;
+  hipLaunchKernelGGL(synth_kv_kernel, dim3((unsigned)((per + 255) / 256), n_layers * n_kv), dim3(256),
+                     0, s, slab, n_kv, hd, max_seq, n_pos, seed);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}

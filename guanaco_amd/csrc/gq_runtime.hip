@@ -1,0 +1,983 @@
+/*
+ * gq_runtime.hip — the C ABI of libgq_hip.so (include/gq_hip.h): device
+ * context and stream, memory, the device KV cache and .lctx sessions, model
+ * binding, the per-token decode step (eager or replayed from a captured HIP
+ * graph) and event-based measurement.
+ *
+ * Device memory plan for one context (sized for 288 GB of HBM):
+ *   weights     as uploaded, reference block layout, 256 B tail padding;
+ *   K, V slabs  [layer][kv_head][max_seq][head_dim] fp32, one allocation each
+ *               (8B shape at max_seq 8320: 2 x 1.09 GB);
+ *   RoPE table  [max_seq][head_dim/2] (cos, sin) fp32 pairs;
+ *   workspace   hidden, q|k|v, attention output, SwiGLU activation, logits,
+ *               split-K partials, argmax partials, device token/pos/step.
+ */
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "gq_internal.h"
+
+namespace {
+
+constexpr size_t kPad = 256;
+
+struct Workspace {
+  float *hidden = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *act2 = nullptr;
+  float *logits = nullptr, *part_o = nullptr, *part_ml = nullptr, *amax = nullptr;
+  int *d_token = nullptr, *d_pos = nullptr, *d_step = nullptr, *d_tokens = nullptr;
+  int tokens_cap = 0, nch = 0, s_max = 0, amax_blocks = 0;
+  size_t part_cap = 0, part_ml_cap = 0; /* floats in part_o / part_ml */
+};
+
+} // namespace
+
+struct gq_ctx {
+  int dev = 0;
+  hipStream_t stream = nullptr;
+  char err[512] = {0};
+  int n_cu = 0;
+  char name[128] = {0};
+  std::vector<void *> allocs;
+  /* host-pointer op staging */
+  float *sx = nullptr, *sy = nullptr;
+  size_t sx_cap = 0, sy_cap = 0;
+  /* KV cache */
+  int kv_layers = 0, kv_heads = 0, kv_hd = 0, kv_max_seq = 0;
+  float theta = 0.f;
+  float *kslab = nullptr, *vslab = nullptr;
+  float2 *rope = nullptr;
+  /* model */
+  bool bound = false;
+  gq_model m{};
+  std::vector<gq_layer> layers;
+  Workspace ws;
+  /* graph */
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t gexec = nullptr;
+  /* measurement hooks for eager steps */
+  bool prof = false;
+  std::vector<hipEvent_t> ev;
+  std::vector<int> ev_class;
+  std::vector<double> ev_bytes;
+};
+
+static int fail(gq_ctx *c, int code, const char *fmt, ...) __attribute__((format(printf, 3, 4)));
+static int fail(gq_ctx *c, int code, const char *fmt, ...) {
+  if (c) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(c->err, sizeof c->err, fmt, ap);
+    va_end(ap);
+  }
+  return code;
+}
+
+#define HIPCHK(c, call)                                                                         \
+  do {                                                                                          \
+    hipError_t e_ = (call);                                                                     \
+    if (e_ != hipSuccess) return fail((c), -4, "%s: %s", #call, hipGetErrorString(e_));         \
+  } while (0)
+
+static size_t block_bytes(int dtype, int *qk) {
+  switch (dtype) {
+  case GQ_Q4_K: *qk = 256; return 144;
+  case GQ_Q6_K: *qk = 256; return 210;
+  case GQ_Q8_0: *qk = 32; return 34;
+  default: *qk = 0; return 0;
+  }
+}
+
+static int mv_class(int dtype) { return dtype == GQ_Q4_K ? 0 : dtype == GQ_Q6_K ? 1 : 2; }
+
+/* ------------------------------------------------------------ lifecycle */
+extern "C" int gq_hip_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+  return n;
+}
+
+extern "C" gq_ctx *gq_hip_create(int device_id) {
+  int n = gq_hip_device_count();
+  if (device_id < 0 || device_id >= n) return nullptr;
+  if (hipSetDevice(device_id) != hipSuccess) return nullptr;
+  gq_ctx *c = new gq_ctx();
+  c->dev = device_id;
+  if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+    delete c;
+    return nullptr;
+  }
+  hipDeviceProp_t p;
+  if (hipGetDeviceProperties(&p, device_id) == hipSuccess) {
+    c->n_cu = p.multiProcessorCount;
+    snprintf(c->name, sizeof c->name, "%s", p.gcnArchName);
+  }
+  return c;
+}
+
+static void free_graph(gq_ctx *c) {
+  if (c->gexec) (void)hipGraphExecDestroy(c->gexec);
+  if (c->graph) (void)hipGraphDestroy(c->graph);
+  c->gexec = nullptr;
+  c->graph = nullptr;
+}
+
+extern "C" void gq_hip_destroy(gq_ctx *c) {
+  if (!c) return;
+  (void)hipSetDevice(c->dev);
+  (void)hipStreamSynchronize(c->stream);
+  free_graph(c);
+  for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
+  for (void *p : c->allocs) (void)hipFree(p);
+  (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+
+extern "C" const char *gq_hip_last_error(const gq_ctx *c) { return c ? c->err : "no context"; }
+
+extern "C" int gq_hip_sync(gq_ctx *c) {
+  if (!c) return -1;
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return 0;
+}
+
+extern "C" int gq_hip_device_info(gq_ctx *c, int *n_cu, char *name, int name_len) {
+  if (!c) return -1;
+  if (n_cu) *n_cu = c->n_cu;
+  if (name && name_len > 0) snprintf(name, (size_t)name_len, "%s", c->name);
+  return 0;
+}
+
+/* ------------------------------------------------------------ memory */
+static void *dev_alloc(gq_ctx *c, size_t bytes) {
+  void *p = nullptr;
+  if (hipMalloc(&p, bytes + kPad) != hipSuccess) {
+    fail(c, -4, "hipMalloc(%zu) failed", bytes + kPad);
+    return nullptr;
+  }
+  c->allocs.push_back(p);
+  return p;
+}
+
+extern "C" void *gq_hip_malloc(gq_ctx *c, size_t bytes) {
+  if (!c) return nullptr;
+  (void)hipSetDevice(c->dev);
+  return dev_alloc(c, bytes);
+}
+
+extern "C" void gq_hip_free(gq_ctx *c, void *p) {
+  if (!c || !p) return;
+  auto it = std::find(c->allocs.begin(), c->allocs.end(), p);
+  if (it == c->allocs.end()) return;
+  (void)hipStreamSynchronize(c->stream);
+  (void)hipFree(p);
+  c->allocs.erase(it);
+}
+
+extern "C" int gq_hip_h2d(gq_ctx *c, void *dev, const void *host, size_t bytes) {
+  if (!c || !dev || !host) return -1;
+  HIPCHK(c, hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return 0;
+}
+
+extern "C" int gq_hip_d2h(gq_ctx *c, void *host, const void *dev, size_t bytes) {
+  if (!c || !dev || !host) return -1;
+  HIPCHK(c, hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return 0;
+}
+
+extern "C" void *gq_hip_upload_weight(gq_ctx *c, const void *host, size_t bytes) {
+  if (!c || !host || !bytes) return nullptr;
+  (void)hipSetDevice(c->dev);
+  void *d = dev_alloc(c, bytes);
+  if (!d) return nullptr;
+  /* staged by the runtime from pageable memory: no DMA straight out of a
+   * private file mapping (matvec_q4k_cuda.cu:119-121) */
+  if (hipMemcpy(d, host, bytes, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemset((char *)d + bytes, 0, kPad) != hipSuccess) {
+    gq_hip_free(c, d);
+    fail(c, -4, "weight upload of %zu bytes failed", bytes);
+    return nullptr;
+  }
+  return d;
+}
+
+extern "C" void *gq_hip_host_alloc_pinned(size_t bytes) {
+  void *p = nullptr;
+  if (hipHostMalloc(&p, bytes, hipHostMallocDefault) != hipSuccess) return nullptr;
+  return p;
+}
+
+extern "C" void gq_hip_host_free_pinned(void *p) {
+  if (p) (void)hipHostFree(p);
+}
+
+/* ------------------------------------------------------------ synthetic */
+extern "C" int gq_hip_synth_quant(gq_ctx *c, void *dev, int dtype, int rows, int cols, uint64_t seed) {
+  if (!c || !dev || rows <= 0 || cols <= 0) return -1;
+  int rc = gq_launch_synth_quant(dev, dtype, rows, cols, seed, c->stream);
+  if (rc) return fail(c, rc, "synth_quant: bad dtype/shape");
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return 0;
+}
+
+extern "C" int gq_hip_synth_normal(gq_ctx *c, float *dev, size_t n, uint64_t seed) {
+  if (!c || !dev) return -1;
+  if (gq_launch_synth_normal(dev, n, seed, 0, c->stream)) return fail(c, -4, "synth_normal");
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return 0;
+}
+
+extern "C" int gq_hip_synth_norm_weight(gq_ctx *c, float *dev, size_t n, uint64_t seed) {
+  if (!c || !dev) return -1;
+  if (gq_launch_synth_normal(dev, n, seed, 1, c->stream)) return fail(c, -4, "synth_norm_weight");
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return 0;
+}
+
+/* ------------------------------------------------------------ matvec */
+static int check_mv(gq_ctx *c, int dtype, const void *w, int rows, int cols, size_t byte_size,
+                    const void *x, const void *y) {
+  int qk;
+  const size_t bb = block_bytes(dtype, &qk);
+  if (!w || !x || !y || !bb || rows <= 0 || cols <= 0) return fail(c, -1, "matvec: bad argument");
+  if (cols % qk) return fail(c, -2, "matvec: cols %d not a multiple of %d", cols, qk);
+  if (byte_size && (size_t)rows * (size_t)(cols / qk) * bb > byte_size)
+    return fail(c, -3, "matvec: byte_size %zu too small", byte_size);
+  if (cols > 16384) return fail(c, -1, "matvec: cols %d above 16384", cols);
+  return 0;
+}
+
+static int launch_one_mv(gq_ctx *c, int dtype, const void *w, int rows, int cols, const float *x,
+                         float *y) {
+  MvArgs a{};
+  a.seg[0] = MvSeg{(const uint8_t *)w, y, nullptr, rows};
+  a.nseg = 1;
+  a.cols = cols;
+  a.x = x;
+  return gq_launch_matvec(dtype, MV_STORE, a, c->stream);
+}
+
+extern "C" int gq_hip_matvec(gq_ctx *c, int dtype, const void *w, int rows, int cols,
+                             size_t byte_size, const float *x, float *y) {
+  if (!c) return -1;
+  int rc = check_mv(c, dtype, w, rows, cols, byte_size, x, y);
+  if (rc) return rc;
+  if (c->sx_cap < (size_t)cols) {
+    float *p = (float *)dev_alloc(c, sizeof(float) * cols);
+    if (!p) return -4;
+    if (c->sx) gq_hip_free(c, c->sx);
+    c->sx = p, c->sx_cap = cols;
+  }
+  if (c->sy_cap < (size_t)rows) {
+    float *p = (float *)dev_alloc(c, sizeof(float) * rows);
+    if (!p) return -4;
+    if (c->sy) gq_hip_free(c, c->sy);
+    c->sy = p, c->sy_cap = rows;
+  }
+  HIPCHK(c, hipMemcpyAsync(c->sx, x, sizeof(float) * cols, hipMemcpyHostToDevice, c->stream));
+  rc = launch_one_mv(c, dtype, w, rows, cols, c->sx, c->sy);
+  if (rc) return fail(c, rc, "matvec launch failed");
+  HIPCHK(c, hipMemcpyAsync(y, c->sy, sizeof(float) * rows, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return 0;
+}
+
+extern "C" int gq_hip_matvec_dev(gq_ctx *c, int dtype, const void *w, int rows, int cols,
+                                 const float *x, float *y) {
+  if (!c) return -1;
+  int rc = check_mv(c, dtype, w, rows, cols, 0, x, y);
+  if (rc) return rc;
+  rc = launch_one_mv(c, dtype, w, rows, cols, x, y);
+  return rc ? fail(c, rc, "matvec launch failed") : 0;
+}
+
+/* ------------------------------------------------------------ KV cache */
+static size_t layer_floats(const gq_ctx *c) {
+  return (size_t)c->kv_heads * c->kv_max_seq * c->kv_hd;
+}
+
+extern "C" int gq_hip_kv_init(gq_ctx *c, int n_layers, int n_kv_heads, int head_dim, int max_seq,
+                              float rope_theta) {
+  if (!c || n_layers <= 0 || n_kv_heads <= 0 || head_dim <= 0 || (head_dim & 1) || max_seq <= 0)
+    return fail(c, -1, "kv_init: bad geometry");
+  (void)hipSetDevice(c->dev);
+  if (c->kslab) {
+    gq_hip_free(c, c->kslab);
+    gq_hip_free(c, c->vslab);
+    gq_hip_free(c, c->rope);
+    c->kslab = c->vslab = nullptr;
+    c->rope = nullptr;
+  }
+  free_graph(c);
+  c->bound = false;
+  c->kv_layers = n_layers, c->kv_heads = n_kv_heads, c->kv_hd = head_dim, c->kv_max_seq = max_seq;
+  c->theta = rope_theta;
+  const size_t bytes = sizeof(float) * layer_floats(c) * n_layers;
+  c->kslab = (float *)dev_alloc(c, bytes);
+  c->vslab = (float *)dev_alloc(c, bytes);
+  const size_t half = (size_t)head_dim / 2;
+  c->rope = (float2 *)dev_alloc(c, sizeof(float2) * half * max_seq);
+  if (!c->kslab || !c->vslab || !c->rope) return -4;
+  /* zeroed like kv_cache_create (kv_cache.c:73-75) */
+  HIPCHK(c, hipMemsetAsync(c->kslab, 0, bytes, c->stream));
+  HIPCHK(c, hipMemsetAsync(c->vslab, 0, bytes, c->stream));
+  /* RoPE table with the reference's fp32 expressions (kernels_cpu.c:409-413) */
+  std::vector<float2> tab(half * max_seq);
+  std::vector<float> freq(half);
+  for (size_t i = 0; i < half; i++)
+    freq[i] = 1.0f / powf(rope_theta, (float)(2 * i) / (float)head_dim);
+  for (int p = 0; p < max_seq; p++)
+    for (size_t i = 0; i < half; i++) {
+      const float a = (float)p * freq[i];
+      tab[(size_t)p * half + i] = make_float2(cosf(a), sinf(a));
+    }
+  HIPCHK(c, hipMemcpyAsync(c->rope, tab.data(), sizeof(float2) * tab.size(), hipMemcpyHostToDevice,
+                           c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return 0;
+}
+
+extern "C" float *gq_hip_kv_k(gq_ctx *c, int layer) {
+  if (!c || !c->kslab || layer < 0 || layer >= c->kv_layers) return nullptr;
+  return c->kslab + layer_floats(c) * layer;
+}
+
+extern "C" float *gq_hip_kv_v(gq_ctx *c, int layer) {
+  if (!c || !c->vslab || layer < 0 || layer >= c->kv_layers) return nullptr;
+  return c->vslab + layer_floats(c) * layer;
+}
+
+extern "C" int gq_hip_kv_append(gq_ctx *c, int layer, int pos, const float *k, const float *v) {
+  if (!c || !c->kslab || !k || !v) return fail(c, -1, "kv_append: not initialised / NULL");
+  if (layer < 0 || layer >= c->kv_layers) return fail(c, -1, "kv_append: bad layer %d", layer);
+  if (pos < 0) return fail(c, -5, "kv_append: negative position %d", pos);
+  const int p = pos % c->kv_max_seq; /* ring wrap of kv_cache.c:101 */
+  const size_t hd = c->kv_hd, row = sizeof(float) * hd, pitch = row * c->kv_max_seq;
+  float *kd = gq_hip_kv_k(c, layer) + (size_t)p * hd, *vd = gq_hip_kv_v(c, layer) + (size_t)p * hd;
+  HIPCHK(c, hipMemcpy2DAsync(kd, pitch, k, row, row, c->kv_heads, hipMemcpyHostToDevice, c->stream));
+  HIPCHK(c, hipMemcpy2DAsync(vd, pitch, v, row, row, c->kv_heads, hipMemcpyHostToDevice, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return 0;
+}
+
+extern "C" int gq_hip_kv_read_layer(gq_ctx *c, int layer, float *k, float *v) {
+  if (!c || !c->kslab || layer < 0 || layer >= c->kv_layers) return fail(c, -1, "kv_read_layer");
+  const size_t bytes = sizeof(float) * layer_floats(c);
+  if (k) HIPCHK(c, hipMemcpyAsync(k, gq_hip_kv_k(c, layer), bytes, hipMemcpyDeviceToHost, c->stream));
+  if (v) HIPCHK(c, hipMemcpyAsync(v, gq_hip_kv_v(c, layer), bytes, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return 0;
+}
+
+extern "C" int gq_hip_kv_write_layer(gq_ctx *c, int layer, const float *k, const float *v) {
+  if (!c || !c->kslab || layer < 0 || layer >= c->kv_layers) return fail(c, -1, "kv_write_layer");
+  const size_t bytes = sizeof(float) * layer_floats(c);
+  if (k) HIPCHK(c, hipMemcpyAsync(gq_hip_kv_k(c, layer), k, bytes, hipMemcpyHostToDevice, c->stream));
+  if (v) HIPCHK(c, hipMemcpyAsync(gq_hip_kv_v(c, layer), v, bytes, hipMemcpyHostToDevice, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return 0;
+}
+
+extern "C" int gq_hip_kv_sync(gq_ctx *c, int layer, int pos, int T, const float *h_k,
+                              const float *h_v, int head_stride, int max_seq) {
+  if (!c || !c->kslab || !h_k || !h_v || T <= 0) return fail(c, -1, "kv_sync: bad argument");
+  if (layer < 0 || layer >= c->kv_layers || max_seq != c->kv_max_seq)
+    return fail(c, -1, "kv_sync: layer/max_seq mismatch");
+  if (pos < 0 || pos + T > c->kv_max_seq) return fail(c, -5, "kv_sync: rows outside the cache");
+  const size_t hd = c->kv_hd, w = sizeof(float) * hd * T;
+  const size_t dpitch = sizeof(float) * hd * c->kv_max_seq, spitch = sizeof(float) * head_stride;
+  HIPCHK(c, hipMemcpy2DAsync(gq_hip_kv_k(c, layer) + pos * hd, dpitch, h_k + pos * hd, spitch, w,
+                             c->kv_heads, hipMemcpyHostToDevice, c->stream));
+  HIPCHK(c, hipMemcpy2DAsync(gq_hip_kv_v(c, layer) + pos * hd, dpitch, h_v + pos * hd, spitch, w,
+                             c->kv_heads, hipMemcpyHostToDevice, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return 0;
+}
+
+extern "C" int gq_hip_kv_prefill_synth(gq_ctx *c, uint64_t seed_k, uint64_t seed_v, int n_pos) {
+  if (!c || !c->kslab) return fail(c, -1, "kv_prefill_synth: no cache");
+  if (n_pos < 0 || n_pos > c->kv_max_seq) return fail(c, -5, "kv_prefill_synth: n_pos");
+  if (gq_launch_synth_kv(c->kslab, c->kv_layers, c->kv_heads, c->kv_hd, c->kv_max_seq, n_pos, seed_k,
+                         c->stream) ||
+      gq_launch_synth_kv(c->vslab, c->kv_layers, c->kv_heads, c->kv_hd, c->kv_max_seq, n_pos, seed_v,
+                         c->stream))
+    return fail(c, -4, "kv_prefill_synth launch");
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return 0;
+}
+
+/* ------------------------------------------------------------ .lctx */
+namespace {
+#pragma pack(push, 1)
+struct LctxHeader { /* session.c:36-48 */
+  uint32_t magic, version;
+  int32_t n_layers, n_kv_heads, head_dim, max_seq, current_pos, n_tokens;
+  uint8_t reserved[32];
+};
+#pragma pack(pop)
+static_assert(sizeof(LctxHeader) == 64, "lctx header is 64 bytes");
+constexpr uint32_t kLctxMagic = 0x5843544Cu, kLctxVersion = 1;
+} // namespace
+
+static int check_header(gq_ctx *c, const LctxHeader &h) {
+  if (h.magic != kLctxMagic) return fail(c, -1, "lctx: bad magic");
+  if (h.version != kLctxVersion) return fail(c, -1, "lctx: unsupported version %u", h.version);
+  if (h.n_layers != c->kv_layers || h.n_kv_heads != c->kv_heads || h.head_dim != c->kv_hd)
+    return fail(c, -1, "lctx: model geometry mismatch");
+  if (h.max_seq != c->kv_max_seq) return fail(c, -1, "lctx: max_seq mismatch");
+  if (h.n_tokens < 0) return fail(c, -1, "lctx: negative token count");
+  return 0;
+}
+
+extern "C" int gq_hip_lctx_save(gq_ctx *c, const char *path, int current_pos, const int32_t *tokens,
+                                int n_tokens) {
+  if (!c || !c->kslab || !path) return fail(c, -1, "lctx_save: bad argument");
+  FILE *f = fopen(path, "wb");
+  if (!f) return fail(c, -1, "lctx_save: cannot open %s", path);
+  LctxHeader h;
+  memset(&h, 0, sizeof h);
+  h.magic = kLctxMagic, h.version = kLctxVersion;
+  h.n_layers = c->kv_layers, h.n_kv_heads = c->kv_heads, h.head_dim = c->kv_hd;
+  h.max_seq = c->kv_max_seq, h.current_pos = current_pos, h.n_tokens = n_tokens;
+  const size_t lb = sizeof(float) * layer_floats(c);
+  void *buf = gq_hip_host_alloc_pinned(lb);
+  int rc = 0;
+  if (!buf) rc = fail(c, -4, "lctx_save: pinned buffer");
+  if (!rc && fwrite(&h, sizeof h, 1, f) != 1) rc = fail(c, -1, "lctx_save: write");
+  if (!rc && n_tokens > 0 && tokens &&
+      fwrite(tokens, sizeof(int32_t), (size_t)n_tokens, f) != (size_t)n_tokens)
+    rc = fail(c, -1, "lctx_save: write");
+  for (int which = 0; which < 2 && !rc; which++)
+    for (int l = 0; l < c->kv_layers && !rc; l++) {
+      const float *src = which ? gq_hip_kv_v(c, l) : gq_hip_kv_k(c, l);
+      if (hipMemcpyAsync(buf, src, lb, hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
+          hipStreamSynchronize(c->stream) != hipSuccess)
+        rc = fail(c, -4, "lctx_save: device gather");
+      else if (fwrite(buf, 1, lb, f) != lb)
+        rc = fail(c, -1, "lctx_save: write");
+    }
+  gq_hip_host_free_pinned(buf);
+  fclose(f);
+  return rc;
+}
+
+extern "C" int gq_hip_lctx_load(gq_ctx *c, const char *path, int *current_pos, int32_t **tokens,
+                                int *n_tokens) {
+  if (!c || !c->kslab || !path) return fail(c, -1, "lctx_load: bad argument");
+  FILE *f = fopen(path, "rb");
+  if (!f) return fail(c, -1, "lctx_load: cannot open %s", path);
+  LctxHeader h;
+  int rc = fread(&h, sizeof h, 1, f) == 1 ? check_header(c, h) : fail(c, -1, "lctx_load: short header");
+  int32_t *tok = nullptr;
+  if (!rc && h.n_tokens > 0) {
+    tok = (int32_t *)malloc(sizeof(int32_t) * h.n_tokens);
+    if (!tok || fread(tok, sizeof(int32_t), (size_t)h.n_tokens, f) != (size_t)h.n_tokens)
+      rc = fail(c, -1, "lctx_load: short token block");
+  }
+  const size_t lb = sizeof(float) * layer_floats(c);
+  void *buf = rc ? nullptr : gq_hip_host_alloc_pinned(lb);
+  if (!rc && !buf) rc = fail(c, -4, "lctx_load: pinned buffer");
+  for (int which = 0; which < 2 && !rc; which++)
+    for (int l = 0; l < c->kv_layers && !rc; l++) {
+      float *dst = which ? gq_hip_kv_v(c, l) : gq_hip_kv_k(c, l);
+      if (fread(buf, 1, lb, f) != lb)
+        rc = fail(c, -1, "lctx_load: short K/V block");
+      else if (hipMemcpyAsync(dst, buf, lb, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+               hipStreamSynchronize(c->stream) != hipSuccess)
+        rc = fail(c, -4, "lctx_load: device restore");
+    }
+  gq_hip_host_free_pinned(buf);
+  fclose(f);
+  if (rc) {
+    free(tok);
+    return rc;
+  }
+  if (current_pos) *current_pos = h.current_pos;
+  if (n_tokens) *n_tokens = h.n_tokens;
+  if (tokens) *tokens = tok;
+  else free(tok);
+  return 0;
+}
+
+extern "C" int gq_hip_lctx_restore_image(gq_ctx *c, const void *image, size_t size, int *current_pos,
+                                         float *ms) {
+  if (!c || !c->kslab || !image || size < sizeof(LctxHeader)) return fail(c, -1, "lctx_restore");
+  LctxHeader h;
+  memcpy(&h, image, sizeof h);
+  int rc = check_header(c, h);
+  if (rc) return rc;
+  const size_t slab = sizeof(float) * layer_floats(c) * c->kv_layers;
+  const size_t off = sizeof h + sizeof(int32_t) * (size_t)h.n_tokens;
+  if (size < off + 2 * slab) return fail(c, -1, "lctx_restore: short image");
+  /* the image's K and V regions are laid out exactly like the device slabs */
+  hipEvent_t e0, e1;
+  HIPCHK(c, hipEventCreate(&e0));
+  HIPCHK(c, hipEventCreate(&e1));
+  HIPCHK(c, hipEventRecord(e0, c->stream));
+  HIPCHK(c, hipMemcpyAsync(c->kslab, (const char *)image + off, slab, hipMemcpyHostToDevice, c->stream));
+  HIPCHK(c, hipMemcpyAsync(c->vslab, (const char *)image + off + slab, slab, hipMemcpyHostToDevice,
+                           c->stream));
+  HIPCHK(c, hipEventRecord(e1, c->stream));
+  HIPCHK(c, hipEventSynchronize(e1));
+  float t = 0.f;
+  (void)hipEventElapsedTime(&t, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (ms) *ms = t;
+  if (current_pos) *current_pos = h.current_pos;
+  return 0;
+}
+
+/* ------------------------------------------------------------ model */
+static int check_weight(gq_ctx *c, const gq_weight &w, int rows, int cols, const char *what) {
+  int qk;
+  if (!w.data || !block_bytes(w.dtype, &qk)) return fail(c, -1, "%s: missing or bad dtype", what);
+  if (w.rows != rows || w.cols != cols) return fail(c, -1, "%s: shape %dx%d, expected %dx%d", what, w.rows, w.cols, rows, cols);
+  if (cols % qk) return fail(c, -2, "%s: cols %% block", what);
+  return 0;
+}
+
+extern "C" int gq_hip_model_bind(gq_ctx *c, const gq_model *m) {
+  if (!c || !m || !m->layers) return fail(c, -1, "model_bind: NULL");
+  if (!c->kslab) return fail(c, -1, "model_bind: call gq_hip_kv_init first");
+  if (m->n_layers != c->kv_layers || m->n_kv_heads != c->kv_heads || m->head_dim != c->kv_hd)
+    return fail(c, -1, "model_bind: model and KV geometry differ");
+  if (m->n_heads % m->n_kv_heads || m->hidden != m->n_heads * m->head_dim)
+    return fail(c, -1, "model_bind: head geometry");
+  if (m->hidden > 16384 || m->ff > 16384 || (m->hidden & 255) || (m->ff & 255))
+    return fail(c, -1, "model_bind: hidden/ff must be multiples of 256 up to 16384");
+  const int H = m->hidden, F = m->ff, kvd = m->n_kv_heads * m->head_dim;
+  for (int l = 0; l < m->n_layers; l++) {
+    const gq_layer &L = m->layers[l];
+    int rc = check_weight(c, L.wq, H, H, "wq") || check_weight(c, L.wk, kvd, H, "wk") ||
+             check_weight(c, L.wv, kvd, H, "wv") || check_weight(c, L.wo, H, H, "wo") ||
+             check_weight(c, L.w_gate, F, H, "w_gate") || check_weight(c, L.w_up, F, H, "w_up") ||
+             check_weight(c, L.w_down, H, F, "w_down");
+    if (rc) return -1;
+    if (!L.rms_att || !L.rms_ffn) return fail(c, -1, "layer %d: norm weights", l);
+  }
+  if (check_weight(c, m->lm_head, m->vocab, H, "lm_head")) return -1;
+  if (!m->embed.data || m->embed.rows != m->vocab || m->embed.cols != H ||
+      (m->embed.dtype != GQ_F32 && m->embed.dtype != GQ_Q8_0 && m->embed.dtype != GQ_Q4_K))
+    return fail(c, -1, "embed: F32, Q8_0 or Q4_K (vocab x hidden)");
+  if (!m->rms_final) return fail(c, -1, "rms_final");
+  free_graph(c);
+  c->m = *m;
+  c->layers.assign(m->layers, m->layers + m->n_layers);
+  c->m.layers = c->layers.data();
+  Workspace &w = c->ws;
+  w.nch = gq_attn_nch(m->n_kv_heads, c->kv_max_seq);
+  w.s_max = gq_attn_smax(c->kv_max_seq, w.nch);
+  w.amax_blocks = gq_argmax_blocks(m->vocab);
+  auto need = [&](float *&p, size_t n) -> bool {
+    if (p) gq_hip_free(c, p);
+    p = (float *)dev_alloc(c, sizeof(float) * n);
+    return p != nullptr;
+  };
+  if (!need(w.hidden, H) || !need(w.qkv, H + 2 * kvd) || !need(w.attn, H) || !need(w.act, F) ||
+      !need(w.act2, F) || !need(w.logits, m->vocab) ||
+      !need(w.part_o, (size_t)m->n_heads * w.nch * m->head_dim) ||
+      !need(w.part_ml, (size_t)m->n_heads * w.nch * 2) || !need(w.amax, 2 * (size_t)w.amax_blocks))
+    return -4;
+  w.part_cap = (size_t)m->n_heads * w.nch * m->head_dim;
+  w.part_ml_cap = (size_t)m->n_heads * w.nch * 2;
+  if (!w.d_token) {
+    w.d_token = (int *)dev_alloc(c, 4 * sizeof(int));
+    if (!w.d_token) return -4;
+    w.d_pos = w.d_token + 1;
+    w.d_step = w.d_token + 2;
+  }
+  c->bound = true;
+  return 0;
+}
+
+/* ---- eager-step measurement hooks ---- */
+static hipEvent_t next_event(gq_ctx *c) {
+  hipEvent_t e;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  c->ev.push_back(e);
+  return e;
+}
+
+static void mark(gq_ctx *c, int cls, double bytes) {
+  if (!c->prof) return;
+  hipEvent_t e = next_event(c);
+  if (!e) return;
+  (void)hipEventRecord(e, c->stream);
+  c->ev_class.push_back(cls);
+  c->ev_bytes.push_back(bytes);
+}
+
+static double mv_bytes(const gq_weight &w, int extra_vectors) {
+  int qk;
+  const size_t bb = block_bytes(w.dtype, &qk);
+  return (double)w.rows * (w.cols / qk) * bb + 4.0 * w.cols + 4.0 * w.rows * (1 + extra_vectors);
+}
+
+/* One decode layer; positions come from pos_dev when not NULL. */
+static int run_layer(gq_ctx *c, int l, int pos, const int *pos_dev, float *hidden) {
+  const gq_model &m = c->m;
+  const gq_layer &L = c->layers[l];
+  Workspace &w = c->ws;
+  const int H = m.hidden, kvd = m.n_kv_heads * m.head_dim;
+  float *q = w.qkv, *k = w.qkv + H, *v = w.qkv + H + kvd;
+  int rc;
+  /* q, k, v: one launch per distinct dtype, RMSNorm fused into each */
+  const gq_weight *W[3] = {&L.wq, &L.wk, &L.wv};
+  float *Y[3] = {q, k, v};
+  bool done[3] = {false, false, false};
+  for (int i = 0; i < 3; i++) {
+    if (done[i]) continue;
+    MvArgs a{};
+    a.cols = H, a.x = hidden, a.norm_w = L.rms_att, a.eps = m.rms_eps;
+    double bytes = 4.0 * H;
+    for (int j = i; j < 3; j++)
+      if (!done[j] && W[j]->dtype == W[i]->dtype) {
+        a.seg[a.nseg++] = MvSeg{(const uint8_t *)W[j]->data, Y[j], nullptr, W[j]->rows};
+        bytes += mv_bytes(*W[j], 0) - 4.0 * H;
+        done[j] = true;
+      }
+    if ((rc = gq_launch_matvec(W[i]->dtype, MV_STORE, a, c->stream))) return rc;
+    mark(c, mv_class(W[i]->dtype), bytes);
+  }
+  RopeArgs ra{q, k, v, gq_hip_kv_k(c, l), gq_hip_kv_v(c, l), c->rope, pos_dev, pos,
+              m.n_heads, m.n_kv_heads, m.head_dim, c->kv_max_seq};
+  if ((rc = gq_launch_rope_append(ra, c->stream))) return rc;
+  mark(c, 4, 4.0 * (H + 2 * kvd) + 4.0 * (H + 2 * kvd));
+  AttnArgs aa{};
+  aa.q = q, aa.k = gq_hip_kv_k(c, l), aa.v = gq_hip_kv_v(c, l);
+  aa.part_o = w.part_o, aa.part_ml = w.part_ml, aa.out = w.attn;
+  aa.pos_dev = pos_dev, aa.pos = pos;
+  aa.n_heads = m.n_heads, aa.n_kv = m.n_kv_heads, aa.hd = m.head_dim, aa.max_seq = c->kv_max_seq;
+  aa.nch = w.nch, aa.s_max = w.s_max, aa.scale = 1.0f / sqrtf((float)m.head_dim);
+  if ((rc = gq_launch_attention(aa, c->stream, nullptr))) return rc;
+  mark(c, 3, 2.0 * 4.0 * kvd * (double)(std::min(pos + 1, c->kv_max_seq)) + 8.0 * H);
+  /* o-proj + residual (in place on hidden) */
+  {
+    MvArgs a{};
+    a.seg[0] = MvSeg{(const uint8_t *)L.wo.data, hidden, hidden, L.wo.rows};
+    a.nseg = 1, a.cols = L.wo.cols, a.x = w.attn;
+    if ((rc = gq_launch_matvec(L.wo.dtype, MV_RESID, a, c->stream))) return rc;
+    mark(c, mv_class(L.wo.dtype), mv_bytes(L.wo, 1));
+  }
+  /* gate/up + SwiGLU, RMSNorm fused */
+  if (L.w_gate.dtype == L.w_up.dtype) {
+    MvArgs a{};
+    a.seg[0] = MvSeg{(const uint8_t *)L.w_gate.data, w.act, nullptr, L.w_gate.rows};
+    a.seg[1] = MvSeg{(const uint8_t *)L.w_up.data, nullptr, nullptr, L.w_up.rows};
+    a.nseg = 2, a.cols = H, a.x = hidden, a.norm_w = L.rms_ffn, a.eps = m.rms_eps;
+    if ((rc = gq_launch_matvec(L.w_gate.dtype, MV_SWIGLU, a, c->stream))) return rc;
+    mark(c, mv_class(L.w_gate.dtype), mv_bytes(L.w_gate, 0) + mv_bytes(L.w_up, 0) - 4.0 * H - 4.0 * m.ff);
+  } else {
+    for (int i = 0; i < 2; i++) {
+      const gq_weight &g = i ? L.w_up : L.w_gate;
+      MvArgs a{};
+      a.seg[0] = MvSeg{(const uint8_t *)g.data, i ? w.act2 : w.act, nullptr, g.rows};
+      a.nseg = 1, a.cols = H, a.x = hidden, a.norm_w = L.rms_ffn, a.eps = m.rms_eps;
+      if ((rc = gq_launch_matvec(g.dtype, MV_STORE, a, c->stream))) return rc;
+      mark(c, mv_class(g.dtype), mv_bytes(g, 0));
+    }
+    if ((rc = gq_launch_silu_mul(w.act, w.act2, m.ff, c->stream))) return rc;
+    mark(c, 5, 12.0 * m.ff);
+  }
+  /* down + residual (in place on hidden) */
+  {
+    MvArgs a{};
+    a.seg[0] = MvSeg{(const uint8_t *)L.w_down.data, hidden, hidden, L.w_down.rows};
+    a.nseg = 1, a.cols = L.w_down.cols, a.x = w.act;
+    if ((rc = gq_launch_matvec(L.w_down.dtype, MV_RESID, a, c->stream))) return rc;
+    mark(c, mv_class(L.w_down.dtype), mv_bytes(L.w_down, 1));
+  }
+  return 0;
+}
+
+/* embedding -> layers -> final RMSNorm + LM head -> argmax.  Eager form
+ * (token/pos host values) or graph form (device token/pos/step). */
+static int run_step(gq_ctx *c, int token, int pos, bool device_state, float *hidden_per_layer) {
+  const gq_model &m = c->m;
+  Workspace &w = c->ws;
+  int rc;
+  const int *tok_dev = device_state ? w.d_token : nullptr;
+  const int *pos_dev = device_state ? w.d_pos : nullptr;
+  if ((rc = gq_launch_embed(m.embed.dtype, m.embed.data, m.hidden, tok_dev, token, w.hidden, c->stream)))
+    return rc;
+  mark(c, 5, 4.0 * m.hidden);
+  for (int l = 0; l < m.n_layers; l++) {
+    if ((rc = run_layer(c, l, pos, pos_dev, w.hidden))) return rc;
+    if (hidden_per_layer)
+      HIPCHK(c, hipMemcpyAsync(hidden_per_layer + (size_t)l * m.hidden, w.hidden, sizeof(float) * m.hidden,
+                               hipMemcpyDeviceToHost, c->stream));
+  }
+  MvArgs a{};
+  a.seg[0] = MvSeg{(const uint8_t *)m.lm_head.data, w.logits, nullptr, m.lm_head.rows};
+  a.nseg = 1, a.cols = m.hidden, a.x = w.hidden, a.norm_w = m.rms_final, a.eps = m.rms_eps;
+  if ((rc = gq_launch_matvec(m.lm_head.dtype, MV_STORE, a, c->stream))) return rc;
+  mark(c, mv_class(m.lm_head.dtype), mv_bytes(m.lm_head, 0));
+  if ((rc = gq_launch_argmax(w.logits, m.vocab, w.amax, w.amax_blocks, w.d_token,
+                             device_state ? w.d_tokens : nullptr, device_state ? w.d_step : nullptr,
+                             device_state ? w.d_pos : nullptr, c->stream)))
+    return rc;
+  mark(c, 5, 4.0 * m.vocab);
+  return 0;
+}
+
+static int check_pos(gq_ctx *c, int pos, int n) {
+  if (!c->bound) return fail(c, -1, "no model bound");
+  if (pos < 0 || pos + n > c->kv_max_seq)
+    return fail(c, -5, "positions %d..%d outside the KV cache (max_seq %d)", pos, pos + n - 1, c->kv_max_seq);
+  return 0;
+}
+
+extern "C" int gq_hip_decode_layer_dev(gq_ctx *c, int layer, int pos, float *hidden) {
+  if (!c || !hidden) return -1;
+  int rc = check_pos(c, pos, 1);
+  if (rc) return rc;
+  if (layer < 0 || layer >= c->m.n_layers) return fail(c, -1, "bad layer");
+  rc = run_layer(c, layer, pos, nullptr, hidden);
+  return rc ? fail(c, rc, "decode_layer launch failed") : 0;
+}
+
+extern "C" int gq_hip_transformer_layer(gq_ctx *c, int layer, int pos, float *h_hidden, float *h_k,
+                                        float *h_v, int head_stride) {
+  if (!c || !h_hidden) return -1;
+  int rc = check_pos(c, pos, 1);
+  if (rc) return rc;
+  if (layer < 0 || layer >= c->m.n_layers) return fail(c, -1, "bad layer");
+  const int H = c->m.hidden;
+  HIPCHK(c, hipMemcpyAsync(c->ws.hidden, h_hidden, sizeof(float) * H, hipMemcpyHostToDevice, c->stream));
+  if ((rc = run_layer(c, layer, pos, nullptr, c->ws.hidden))) return fail(c, rc, "layer launch failed");
+  HIPCHK(c, hipMemcpyAsync(h_hidden, c->ws.hidden, sizeof(float) * H, hipMemcpyDeviceToHost, c->stream));
+  if (h_k && h_v) { /* keep the host cache coherent for kv_cache_save */
+    const size_t hd = c->kv_hd, row = sizeof(float) * hd;
+    const size_t spitch = row * c->kv_max_seq, dpitch = sizeof(float) * head_stride;
+    HIPCHK(c, hipMemcpy2DAsync(h_k + pos * hd, dpitch, gq_hip_kv_k(c, layer) + pos * hd, spitch, row,
+                               c->kv_heads, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipMemcpy2DAsync(h_v + pos * hd, dpitch, gq_hip_kv_v(c, layer) + pos * hd, spitch, row,
+                               c->kv_heads, hipMemcpyDeviceToHost, c->stream));
+  }
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return 0;
+}
+
+extern "C" int gq_hip_forward_token(gq_ctx *c, int token, int pos, float *logits, float *hidden_per_layer) {
+  if (!c) return -1;
+  int rc = check_pos(c, pos, 1);
+  if (rc) return rc;
+  if (token < 0 || token >= c->m.vocab) return fail(c, -1, "token %d out of range", token);
+  if ((rc = run_step(c, token, pos, false, hidden_per_layer))) return fail(c, rc, "step launch failed");
+  int next = -1;
+  HIPCHK(c, hipMemcpyAsync(&next, c->ws.d_token, sizeof(int), hipMemcpyDeviceToHost, c->stream));
+  if (logits)
+    HIPCHK(c, hipMemcpyAsync(logits, c->ws.logits, sizeof(float) * c->m.vocab, hipMemcpyDeviceToHost,
+                             c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return next;
+}
+
+static int ensure_tokens(gq_ctx *c, int n) {
+  Workspace &w = c->ws;
+  if (w.tokens_cap >= n) return 0;
+  if (w.d_tokens) gq_hip_free(c, w.d_tokens);
+  w.d_tokens = (int *)dev_alloc(c, sizeof(int) * n);
+  if (!w.d_tokens) return -4;
+  w.tokens_cap = n;
+  free_graph(c); /* the graph captured the old pointer */
+  return 0;
+}
+
+extern "C" int gq_hip_decode_loop(gq_ctx *c, int token, int pos, int n_steps, int use_graph,
+                                  int32_t *tokens_out, float *ms) {
+  if (!c || n_steps <= 0 || !tokens_out) return fail(c, -1, "decode_loop: bad argument");
+  int rc = check_pos(c, pos, n_steps);
+  if (rc) return rc;
+  if (token < 0 || token >= c->m.vocab) return fail(c, -1, "token out of range");
+  if ((rc = ensure_tokens(c, n_steps))) return rc;
+  Workspace &w = c->ws;
+  int st[3] = {token, pos, 0};
+  HIPCHK(c, hipMemcpyAsync(w.d_token, st, sizeof st, hipMemcpyHostToDevice, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  if (use_graph && !c->gexec) {
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    HIPCHK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    rc = run_step(c, token, pos, true, nullptr);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(c->stream, &g);
+    if (rc || e != hipSuccess) {
+      if (g) (void)hipGraphDestroy(g);
+      return fail(c, rc ? rc : -4, "graph capture failed");
+    }
+    c->graph = g;
+    if (hipGraphInstantiate(&c->gexec, g, nullptr, nullptr, 0) != hipSuccess) {
+      free_graph(c);
+      return fail(c, -4, "graph instantiate failed");
+    }
+  }
+  hipEvent_t e0, e1;
+  HIPCHK(c, hipEventCreate(&e0));
+  HIPCHK(c, hipEventCreate(&e1));
+  HIPCHK(c, hipEventRecord(e0, c->stream));
+  for (int i = 0; i < n_steps; i++) {
+    if (use_graph) {
+      HIPCHK(c, hipGraphLaunch(c->gexec, c->stream));
+    } else if ((rc = run_step(c, 0, 0, true, nullptr))) {
+      return fail(c, rc, "step launch failed");
+    }
+  }
+  HIPCHK(c, hipEventRecord(e1, c->stream));
+  HIPCHK(c, hipMemcpyAsync(tokens_out, w.d_tokens, sizeof(int32_t) * n_steps, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  float t = 0.f;
+  (void)hipEventElapsedTime(&t, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (ms) *ms = t;
+  return 0;
+}
+
+/* ------------------------------------------------------------ measurement */
+extern "C" int gq_hip_profile_step(gq_ctx *c, int token, int pos, double ms[GQ_NCLASS],
+                                   int launches[GQ_NCLASS], double bytes[GQ_NCLASS]) {
+  if (!c) return -1;
+  int rc = check_pos(c, pos, 1);
+  if (rc) return rc;
+  for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
+  c->ev.clear(), c->ev_class.clear(), c->ev_bytes.clear();
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  c->prof = true;
+  hipEvent_t e0 = next_event(c);
+  (void)hipEventRecord(e0, c->stream);
+  rc = run_step(c, token, pos, false, nullptr);
+  c->prof = false;
+  if (rc) return fail(c, rc, "profile step failed");
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  for (int k = 0; k < GQ_NCLASS; k++) ms[k] = 0, launches[k] = 0, bytes[k] = 0;
+  for (size_t i = 0; i < c->ev_class.size(); i++) {
+    float t = 0.f;
+    (void)hipEventElapsedTime(&t, c->ev[i], c->ev[i + 1]);
+    const int k = c->ev_class[i];
+    ms[k] += t;
+    launches[k] += 1;
+    bytes[k] += c->ev_bytes[i];
+  }
+  return 0;
+}
+
+extern "C" float gq_hip_time_matvec(gq_ctx *c, int dtype, const void *const *w_devs, int n_w, int rows,
+                                    int cols, const float *x, float *y, int n_iter) {
+  if (!c || !w_devs || n_w <= 0 || n_iter <= 0) return -1.f;
+  if (check_mv(c, dtype, w_devs[0], rows, cols, 0, x, y)) return -1.f;
+  hipEvent_t e0, e1;
+  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return -1.f;
+  (void)hipEventRecord(e0, c->stream);
+  for (int i = 0; i < n_iter; i++)
+    if (launch_one_mv(c, dtype, w_devs[i % n_w], rows, cols, x, y + (size_t)(i % n_w) * rows)) return -1.f;
+  (void)hipEventRecord(e1, c->stream);
+  (void)hipEventSynchronize(e1);
+  float t = 0.f;
+  (void)hipEventElapsedTime(&t, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  return t / n_iter;
+}
+
+extern "C" float gq_hip_time_attention(gq_ctx *c, int layer, int pos, const float *q, float *out,
+                                       int n_iter) {
+  if (!c || !c->kslab || !q || !out || n_iter <= 0 || pos < 0 || pos >= c->kv_max_seq) return -1.f;
+  const int n_heads = c->bound ? c->m.n_heads : -1;
+  if (n_heads <= 0) return -1.f;
+  hipEvent_t e0, e1;
+  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return -1.f;
+  AttnArgs aa{};
+  aa.q = q, aa.part_o = c->ws.part_o, aa.part_ml = c->ws.part_ml, aa.out = out;
+  aa.pos = pos, aa.n_heads = n_heads, aa.n_kv = c->kv_heads, aa.hd = c->kv_hd;
+  aa.max_seq = c->kv_max_seq, aa.nch = c->ws.nch, aa.s_max = c->ws.s_max;
+  aa.scale = 1.0f / sqrtf((float)c->kv_hd);
+  (void)hipEventRecord(e0, c->stream);
+  for (int i = 0; i < n_iter; i++) {
+    const int l = (layer + i) % c->kv_layers;
+    aa.k = gq_hip_kv_k(c, l), aa.v = gq_hip_kv_v(c, l);
+    if (gq_launch_attention(aa, c->stream, nullptr)) return -1.f;
+  }
+  (void)hipEventRecord(e1, c->stream);
+  (void)hipEventSynchronize(e1);
+  float t = 0.f;
+  (void)hipEventElapsedTime(&t, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  return t / n_iter;
+}
+
+/* ------------------------------------------------------------ op-level */
+extern "C" int gq_hip_rmsnorm_dev(gq_ctx *c, const float *x, const float *w, float *out, int dim, float eps) {
+  if (!c || !x || !out || dim <= 0) return -1;
+  return gq_launch_rmsnorm(x, w, out, dim, eps, c->stream) ? fail(c, -4, "rmsnorm launch") : 0;
+}
+
+extern "C" int gq_hip_rope_append_dev(gq_ctx *c, int layer, int pos, int n_heads, float *q,
+                                      const float *k, const float *v) {
+  if (!c || !c->kslab || !q || !k || !v || layer < 0 || layer >= c->kv_layers) return fail(c, -1, "rope_append: bad argument");
+  if (pos < 0 || pos >= c->kv_max_seq) return fail(c, -5, "rope_append: position outside the cache");
+  RopeArgs ra{q, k, v, gq_hip_kv_k(c, layer), gq_hip_kv_v(c, layer), c->rope, nullptr, pos,
+              n_heads, c->kv_heads, c->kv_hd, c->kv_max_seq};
+  return gq_launch_rope_append(ra, c->stream) ? fail(c, -4, "rope_append launch") : 0;
+}
+
+extern "C" int gq_hip_attention_dev(gq_ctx *c, int layer, int pos, int n_heads, const float *q, float *out) {
+  if (!c || !c->kslab || !q || !out || layer < 0 || layer >= c->kv_layers || n_heads <= 0 ||
+      n_heads % c->kv_heads)
+    return fail(c, -1, "attention: bad argument");
+  if (pos < 0 || pos >= c->kv_max_seq) return fail(c, -5, "attention: position outside the cache");
+  Workspace &w = c->ws;
+  const int nch = gq_attn_nch(c->kv_heads, c->kv_max_seq);
+  const size_t need_o = (size_t)n_heads * nch * c->kv_hd, need_ml = (size_t)n_heads * nch * 2;
+  if (!c->bound) { /* op-level use without a bound model: private partials */
+    if (w.part_cap < need_o || w.part_ml_cap < need_ml || !w.part_o) {
+      if (w.part_o) gq_hip_free(c, w.part_o);
+      if (w.part_ml) gq_hip_free(c, w.part_ml);
+      w.part_o = (float *)dev_alloc(c, sizeof(float) * need_o);
+      w.part_ml = (float *)dev_alloc(c, sizeof(float) * need_ml);
+      if (!w.part_o || !w.part_ml) return -4;
+      w.part_cap = need_o;
+      w.part_ml_cap = need_ml;
+    }
+    w.nch = nch;
+    w.s_max = gq_attn_smax(c->kv_max_seq, nch);
+  } else if (n_heads != c->m.n_heads) {
+    return fail(c, -1, "attention: n_heads differs from the bound model");
+  }
+  AttnArgs aa{};
+  aa.q = q, aa.k = gq_hip_kv_k(c, layer), aa.v = gq_hip_kv_v(c, layer);
+  aa.part_o = w.part_o, aa.part_ml = w.part_ml, aa.out = out, aa.pos = pos;
+  aa.n_heads = n_heads, aa.n_kv = c->kv_heads, aa.hd = c->kv_hd, aa.max_seq = c->kv_max_seq;
+  aa.nch = w.nch, aa.s_max = w.s_max, aa.scale = 1.0f / sqrtf((float)c->kv_hd);
+  return gq_launch_attention(aa, c->stream, nullptr) ? fail(c, -1, "attention launch (unsupported head_dim/group?)") : 0;
+}
+
+extern "C" int gq_hip_embed_dev(gq_ctx *c, int dtype, const void *table, int hidden, int token, float *out) {
+  if (!c || !table || !out || hidden <= 0 || token < 0) return -1;
+  return gq_launch_embed(dtype, table, hidden, nullptr, token, out, c->stream) ? fail(c, -1, "embed") : 0;
+}
+
+extern "C" int gq_hip_argmax_dev(gq_ctx *c, const float *x, int n, int *out_index_dev) {
+  if (!c || !x || n <= 0 || !out_index_dev) return -1;
+  const int nblk = gq_argmax_blocks(n);
+  float *scratch = (float *)dev_alloc(c, sizeof(float) * 2 * nblk);
+  if (!scratch) return -4;
+  int rc = gq_launch_argmax(x, n, scratch, nblk, out_index_dev, nullptr, nullptr, nullptr, c->stream);
+  (void)hipStreamSynchronize(c->stream);
+  gq_hip_free(c, scratch);
+  return rc ? fail(c, rc, "argmax") : 0;
+}
+
+extern "C" int gq_hip_silu_mul_dev(gq_ctx *c, float *gate, const float *up, int n) {
+  if (!c || !gate || !up || n <= 0) return -1;
+  return gq_launch_silu_mul(gate, up, n, c->stream) ? fail(c, -4, "silu_mul") : 0;
+}

@@ -1,0 +1,102 @@
+"""Synthetic model geometries of the decode hot path.
+
+A ``ModelSpec`` names the shape of a Llama-family model as the reference
+loader describes it (``types.h:110-147``: ``ModelConfig`` / ``LayerWeights``),
+the storage dtype of every weight, and the seed from which every weight byte,
+norm weight and KV pre-fill value is derived (``csrc/gq_synth.h``).  The same
+spec drives the device fill kernels (bench, GPU tests) and the CPU oracle, so
+both sides see bit-identical inputs without shipping weights.
+
+Weights use the reference's ``[rows = out_features][cols = in_features]``
+convention (``loader.c:503-510``).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+# dtype codes of the reference's DataType enum (types.h:16-24)
+F32, Q8_0, Q4_K, Q6_K = 0, 2, 4, 5
+BLOCK = {Q4_K: (256, 144), Q6_K: (256, 210), Q8_0: (32, 34)}
+DTYPE_NAME = {F32: "f32", Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k"}
+
+# tensor slots of gq_tensor_seed()
+SLOT = dict(wq=0, wk=1, wv=2, wo=3, wg=4, wu=5, wd=6, rms_att=7, rms_ffn=8,
+            embed=10, lm_head=11, rms_final=12, kv_k=13, kv_v=14, act=15)
+LAYER_WEIGHTS = ("wq", "wk", "wv", "wo", "wg", "wu", "wd")
+
+
+def qbytes(dtype: int, rows: int, cols: int) -> int:
+    qk, bb = BLOCK[dtype]
+    assert cols % qk == 0, (dtype, cols)
+    return rows * (cols // qk) * bb
+
+
+@dataclass
+class ModelSpec:
+    name: str
+    n_layers: int
+    hidden: int
+    ff: int
+    n_heads: int
+    n_kv_heads: int
+    vocab: int
+    # per-layer dtype rule: dict slot -> dtype, or callable(layer) -> dict
+    layer_dtypes: object = None
+    embed_dtype: int = Q4_K
+    lm_head_dtype: int = Q6_K
+    # the reference hard-codes theta=500000 (kernels_cpu.c:408) and
+    # eps=1e-6 (engine.c:359,524,582); parity runs use those values
+    rope_theta: float = 500000.0
+    rms_eps: float = 1e-6
+    seed: int = 0x5EED
+    head_dim: int = field(init=False)
+
+    def __post_init__(self):
+        assert self.hidden % self.n_heads == 0
+        self.head_dim = self.hidden // self.n_heads  # loader.c:415-417
+
+    def dtypes(self, layer: int) -> dict:
+        rule = self.layer_dtypes
+        d = rule(layer) if callable(rule) else dict(rule)
+        return {k: d.get(k, Q4_K) for k in LAYER_WEIGHTS}
+
+    def shape(self, slot: str) -> tuple:
+        H, F, kvd = self.hidden, self.ff, self.n_kv_heads * self.head_dim
+        return dict(wq=(H, H), wk=(kvd, H), wv=(kvd, H), wo=(H, H), wg=(F, H),
+                    wu=(F, H), wd=(H, F), embed=(self.vocab, H),
+                    lm_head=(self.vocab, H))[slot]
+
+    def weight_bytes_per_token(self) -> int:
+        """Algorithmic weight bytes streamed per decode token."""
+        tot = 0
+        for l in range(self.n_layers):
+            for k, dt in self.dtypes(l).items():
+                tot += qbytes(dt, *self.shape(k))
+        tot += qbytes(self.lm_head_dtype, *self.shape("lm_head"))
+        tot += 4 * self.hidden * (2 * self.n_layers + 1)  # norm weights
+        tot += qbytes(self.embed_dtype, 1, self.hidden)  # one embedding row
+        return tot
+
+    def kv_bytes_per_token(self, pos: int) -> int:
+        """K+V bytes attention reads at position pos (pos+1 rows), all layers."""
+        return 2 * self.n_layers * self.n_kv_heads * (pos + 1) * self.head_dim * 4
+
+
+def _q6k_on_even(layer):
+    # "Q6_K on half the attn_v/ffn_down layers": the even layers
+    return dict(wv=Q6_K, wd=Q6_K) if layer % 2 == 0 else {}
+
+
+LLAMA8B = ModelSpec("llama-3.1-8b-shape-q4_k_m", n_layers=32, hidden=4096, ff=14336,
+                    n_heads=32, n_kv_heads=8, vocab=128256, layer_dtypes=_q6k_on_even)
+
+TINYLLAMA = ModelSpec("tinyllama-1.1b-shape", n_layers=22, hidden=2048, ff=5632,
+                      n_heads=32, n_kv_heads=4, vocab=32000,
+                      layer_dtypes=dict(wv=Q6_K, wd=Q6_K))
+
+# small model used by the quick parity tests: same mixed-dtype rule as the 8B
+# shape, GQA 4:1 like both presets, head_dim 64
+TINY_TEST = ModelSpec("tiny-test", n_layers=2, hidden=512, ff=1024, n_heads=8,
+                      n_kv_heads=2, vocab=1000, layer_dtypes=_q6k_on_even)
+
+PRESETS = {s.name: s for s in (LLAMA8B, TINYLLAMA, TINY_TEST)}

@@ -1,0 +1,225 @@
+/*
+ * gq_hip.h — C ABI of libgq_hip.so, the MI355X (gfx950) decode hot path.
+ *
+ * Plain C types only: opaque context, device pointers as void*, host
+ * pointers, sizes and int status codes.  Every entry point names the
+ * reference interface it replaces (animeshkumarmaitreya/Guanaco, src/...).
+ * A host-side KernelVTable binding (guanaco_amd/host/hip_backend.c) and the
+ * ctypes mirror (guanaco_amd/hip.py) sit on top of it.
+ *
+ * Status codes: 0 success; -1 bad argument / NULL / bad dtype / not
+ * initialised (the reference's matvec code -1, quant_matvec_q4_k.c:143-146);
+ * -2 cols not a multiple of the block length (:150-151); -3 byte_size too
+ * small for the shape (:154-158); -4 HIP runtime error or out of device
+ * memory (the caller falls back to the CPU path, as engine.c:347-350 does
+ * for cuda_transformer_layer_gpu's -1); -5 position outside the KV cache.
+ * gq_hip_last_error() returns a message for the last failure on a context.
+ *
+ * Threading: a context owns one HIP stream; calls on one context are not
+ * thread-safe (matches the reference's single-threaded engine,
+ * engine.c:287-594).  Entry points that return host data synchronise the
+ * stream before returning; *_dev entry points are asynchronous on the
+ * context stream until gq_hip_sync().
+ */
+#ifndef GQ_HIP_H
+#define GQ_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes = the reference's DataType values (types.h:16-24) */
+#define GQ_F32 0
+#define GQ_Q8_0 2
+#define GQ_Q4_K 4
+#define GQ_Q6_K 5
+
+typedef struct gq_ctx gq_ctx;
+
+/* ---------------------------------------------------------------- lifecycle
+ * Replaces the CUDA backend's device bring-up (cuda_backend.c:43-81) and the
+ * hidden static streams (matvec_q4k_cuda.cu:83, cuda_layer_kernels.cu:314). */
+int gq_hip_device_count(void);                 /* 0 when no usable GPU */
+gq_ctx *gq_hip_create(int device_id);          /* NULL when unavailable */
+void gq_hip_destroy(gq_ctx *ctx);              /* frees every device buffer */
+const char *gq_hip_last_error(const gq_ctx *ctx);
+/* Replaces cuda_finish_layer (cuda_layer_kernels.cu:715-717). */
+int gq_hip_sync(gq_ctx *ctx);
+/* Number of compute units and the device name (for reports). */
+int gq_hip_device_info(gq_ctx *ctx, int *n_cu, char *name, int name_len);
+
+/* ------------------------------------------------------- device memory
+ * Replaces cuda_upload_weight (matvec_q4k_cuda.cu:115-133): allocates and
+ * copies `bytes` from host memory (a private file mapping is fine: the copy
+ * is staged), returns the device pointer or NULL (the loader then keeps the
+ * tensor CPU-resident, loader.c:711-717).  Allocations carry 256 bytes of
+ * tail padding so block loads never leave the buffer. */
+void *gq_hip_upload_weight(gq_ctx *ctx, const void *host, size_t bytes);
+void *gq_hip_malloc(gq_ctx *ctx, size_t bytes);
+void gq_hip_free(gq_ctx *ctx, void *dev);
+int gq_hip_h2d(gq_ctx *ctx, void *dev, const void *host, size_t bytes);
+int gq_hip_d2h(gq_ctx *ctx, void *host, const void *dev, size_t bytes);
+
+/* ------------------------------------------------------- synthetic inputs
+ * Device fill with the generator of csrc/gq_synth.h (bit-identical to the
+ * host generator the parity oracle uses).  dtype Q4_K/Q6_K/Q8_0: rows x cols
+ * blocks; normal: n fp32 ~ N(0,1); norm_weight: n fp32 1 + N(0,1)/64. */
+int gq_hip_synth_quant(gq_ctx *ctx, void *dev, int dtype, int rows, int cols, uint64_t seed);
+int gq_hip_synth_normal(gq_ctx *ctx, float *dev, size_t n, uint64_t seed);
+int gq_hip_synth_norm_weight(gq_ctx *ctx, float *dev, size_t n, uint64_t seed);
+
+/* ------------------------------------------------------- quantised matvec
+ * y[rows] = W[rows, cols] . x[cols]; W device-resident in the reference's
+ * on-disk block layout.  Replaces the vtable slots matvec_q4k_f32 /
+ * matvec_q6k_f32 / matvec_q8_0_f32 (backend.h:36-38) and the CUDA host
+ * wrapper cuda_matvec_q4k_f32_impl (matvec_q4k_cuda.cu:85-113): x and y are
+ * HOST pointers (engine scratch), the call returns after y is written.
+ * byte_size 0 skips the size check, as the reference does. */
+int gq_hip_matvec(gq_ctx *ctx, int dtype, const void *w_dev, int rows, int cols,
+                  size_t byte_size, const float *x, float *y);
+/* Same, device x / y, asynchronous on the context stream. */
+int gq_hip_matvec_dev(gq_ctx *ctx, int dtype, const void *w_dev, int rows, int cols,
+                      const float *x_dev, float *y_dev);
+
+/* ------------------------------------------------------- KV cache
+ * Device-resident fp32 cache in the reference layout
+ * [layer][kv_head][max_seq][head_dim], K and V in separate slabs
+ * (kv_cache.c:25-32, offset formula :90-93), zeroed at init
+ * (kv_cache_create, :34-84).  Also uploads the RoPE (cos, sin) table for
+ * positions 0..max_seq-1, computed on the host with the reference's fp32
+ * expressions (kernels_cpu.c:409-413) for the given theta. */
+int gq_hip_kv_init(gq_ctx *ctx, int n_layers, int n_kv_heads, int head_dim, int max_seq,
+                   float rope_theta);
+float *gq_hip_kv_k(gq_ctx *ctx, int layer); /* device pointer of a layer's K slab */
+float *gq_hip_kv_v(gq_ctx *ctx, int layer);
+/* Append one token's K and V rows (n_kv_heads x head_dim each, host memory)
+ * at pos % max_seq — kv_cache_append (kv_cache.c:95-128).  Bit copies. */
+int gq_hip_kv_append(gq_ctx *ctx, int layer, int pos, const float *k, const float *v);
+/* Copy a layer's whole K/V slabs device -> host / host -> device
+ * (kv_cache_raw_k / raw_v + memcpy, kv_cache.c:189-205). */
+int gq_hip_kv_read_layer(gq_ctx *ctx, int layer, float *k, float *v);
+int gq_hip_kv_write_layer(gq_ctx *ctx, int layer, const float *k, const float *v);
+/* T new host rows from position pos of one layer -> device; arguments as
+ * cuda_sync_kv_cache (cuda_layer_kernels.cu:585-603). */
+int gq_hip_kv_sync(gq_ctx *ctx, int layer, int pos, int T, const float *h_k, const float *h_v,
+                   int head_stride, int max_seq);
+/* Seeded N(0,1) history at positions 0..n_pos-1 (gq_synth.h gq_kv_index). */
+int gq_hip_kv_prefill_synth(gq_ctx *ctx, uint64_t seed_k, uint64_t seed_v, int n_pos);
+
+/* ------------------------------------------------------- sessions (.lctx)
+ * Byte-identical to kv_cache_save / kv_cache_load (session.c:52-188): 64-byte
+ * header, int32 tokens, K of all layers, V of all layers at full max_seq
+ * stride.  Save gathers from the DEVICE cache (the device cache is the source
+ * of truth); load validates magic, version, geometry and max_seq and
+ * restores into the device cache.  *tokens is malloc'ed (caller frees) when
+ * the file holds tokens and tokens != NULL. */
+int gq_hip_lctx_save(gq_ctx *ctx, const char *path, int current_pos, const int32_t *tokens,
+                     int n_tokens);
+int gq_hip_lctx_load(gq_ctx *ctx, const char *path, int *current_pos, int32_t **tokens,
+                     int *n_tokens);
+/* Restore K/V from a .lctx image already in host memory (e.g. pinned),
+ * returns the milliseconds the host->device copy took (HIP events). */
+int gq_hip_lctx_restore_image(gq_ctx *ctx, const void *image, size_t size, int *current_pos,
+                              float *ms);
+void *gq_hip_host_alloc_pinned(size_t bytes); /* hipHostMalloc */
+void gq_hip_host_free_pinned(void *p);
+
+/* ------------------------------------------------------- model + decode
+ * Device-resident model description: the GPU side of LayerWeights /
+ * ModelWeights (types.h:127-147).  Weight pointers are device pointers from
+ * gq_hip_upload_weight / gq_hip_malloc; norm weights are device fp32. */
+typedef struct {
+  const void *data;
+  int dtype;
+  int rows, cols;
+} gq_weight;
+
+typedef struct {
+  gq_weight wq, wk, wv, wo, w_gate, w_up, w_down;
+  const float *rms_att, *rms_ffn;
+} gq_layer;
+
+typedef struct {
+  int n_layers, hidden, ff, n_heads, n_kv_heads, head_dim, vocab;
+  float rope_theta, rms_eps;
+  const gq_layer *layers; /* host array, copied */
+  gq_weight embed, lm_head;
+  const float *rms_final;
+} gq_model;
+
+/* Bind a model (after gq_hip_kv_init with matching geometry) and allocate
+ * the decode workspace. */
+int gq_hip_model_bind(gq_ctx *ctx, const gq_model *m);
+
+/* One decode layer on a device hidden vector (hidden -> hidden): RMSNorm,
+ * QKV, RoPE + KV append, split-K GQA attention, o-proj + residual, RMSNorm,
+ * gate/up + SwiGLU, down + residual.  The device-side equivalent of
+ * transformer_layer for T = 1 (engine.c:353-554). */
+int gq_hip_decode_layer_dev(gq_ctx *ctx, int layer, int pos, float *hidden_dev);
+
+/* Drop-in for cuda_transformer_layer_gpu (kernels.h:46-58, called at
+ * engine.c:334): host hidden in/out for one bound layer; also writes the new
+ * K/V rows into the host cache (h_k_cache / h_v_cache with the given head
+ * stride, may be NULL) so a later kv_cache_save sees them.  Returns 0, or
+ * non-zero so the engine falls back to its CPU path. */
+int gq_hip_transformer_layer(gq_ctx *ctx, int layer, int pos, float *h_hidden, float *h_k_cache,
+                             float *h_v_cache, int head_stride);
+
+/* Whole-model decode of one token at position pos on the device: embedding,
+ * every layer, final RMSNorm, LM head, greedy argmax (ties to the lowest
+ * index, tokenizer.c:175-185) — forward() + sample_greedy (engine.c:559-594).
+ * logits (host, vocab floats) and hidden_per_layer (host, n_layers*hidden)
+ * may be NULL.  Returns the next token, or a negative status. */
+int gq_hip_forward_token(gq_ctx *ctx, int token, int pos, float *logits, float *hidden_per_layer);
+
+/* Greedy decode loop of n_steps tokens from (token, pos): the generate.c
+ * decode loop (generate.c:266-325) with sampling on the device.  Each step
+ * is one replay of a captured HIP graph when use_graph != 0.  tokens_out
+ * receives the n_steps generated tokens.  *ms (may be NULL) receives the
+ * device time of the loop (HIP events around it). */
+int gq_hip_decode_loop(gq_ctx *ctx, int token, int pos, int n_steps, int use_graph,
+                       int32_t *tokens_out, float *ms);
+
+/* ------------------------------------------------------- measurement
+ * Runs one eager decode step with HIP events around every kernel launch and
+ * accumulates per-kernel-class device time and launch counts.  Classes:
+ * 0 Q4_K matvec, 1 Q6_K matvec, 2 Q8_0 matvec, 3 attention (partial+merge),
+ * 4 RoPE+append, 5 other (embedding, argmax).  Per-class algorithmic bytes
+ * are accumulated in bytes[]. */
+#define GQ_NCLASS 6
+int gq_hip_profile_step(gq_ctx *ctx, int token, int pos, double ms[GQ_NCLASS],
+                        int launches[GQ_NCLASS], double bytes[GQ_NCLASS]);
+/* Average device time (ms) of n back-to-back launches of one matvec, timed
+ * with HIP events on the context stream; rotating over n_w weight buffers
+ * (to defeat the MALL) with per-buffer outputs. */
+float gq_hip_time_matvec(gq_ctx *ctx, int dtype, const void *const *w_devs, int n_w, int rows,
+                         int cols, const float *x_dev, float *y_dev, int n_iter);
+/* Device time of n launches of the attention kernels for one layer. */
+float gq_hip_time_attention(gq_ctx *ctx, int layer, int pos, const float *q_dev, float *out_dev,
+                            int n_iter);
+
+/* ------------------------------------------------------- op-level entry points
+ * (device pointers, asynchronous) used by the parity tests. */
+int gq_hip_rmsnorm_dev(gq_ctx *ctx, const float *x, const float *w, float *out, int dim,
+                       float eps);
+/* RoPE on q (n_heads x hd) and k (n_kv x hd) at pos, then append k and v to
+ * the cache of `layer` at pos (the step 4 + 5 of transformer_layer,
+ * engine.c:372-392). q, k, v are device buffers; q is rotated in place. */
+int gq_hip_rope_append_dev(gq_ctx *ctx, int layer, int pos, int n_heads, float *q, const float *k,
+                           const float *v);
+/* Split-K single-query GQA attention of `layer` over positions 0..pos
+ * (engine.c:433-509): q (n_heads x hd) -> out (n_heads x hd). */
+int gq_hip_attention_dev(gq_ctx *ctx, int layer, int pos, int n_heads, const float *q,
+                         float *out);
+int gq_hip_embed_dev(gq_ctx *ctx, int dtype, const void *table, int hidden, int token,
+                     float *out);
+int gq_hip_argmax_dev(gq_ctx *ctx, const float *x, int n, int *out_index_dev);
+int gq_hip_silu_mul_dev(gq_ctx *ctx, float *gate, const float *up, int n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GQ_HIP_H */

@@ -1,0 +1,133 @@
+"""GPU parity of the matvec and glue kernels through the C ABI, against the
+CPU oracle (pinned to the reference in test_oracle.py) on the same seeded
+inputs.  Tolerance: relative L2 <= 1e-5 for matvecs (the north star allows
+1e-3 per layer; a correct kernel differs from the CPU order by ~1e-7)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle import F32, Q4_K, Q6_K, Q8_0, OrcTensor, fptr, u8ptr
+from util import bits, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+MV_TOL = 1e-5
+
+
+@pytest.mark.parametrize("dt", [Q4_K, Q6_K, Q8_0])
+def test_device_synth_matches_host(ctx, orc, dt):
+    rows, cols = (37, 5632) if dt != Q8_0 else (37, 1024)
+    seed = 0xABCDEF + dt
+    dev = ctx.synth_quant(dt, rows, cols, seed)
+    host = orc.synth_quant(dt, seed, rows, cols)
+    assert np.array_equal(dev.download(np.uint8, host.size), host)
+    dev.free()
+
+
+def test_device_synth_normal_matches_host(ctx, orc):
+    n = 100003
+    a = ctx.synth_normal(n, 99)
+    b = ctx.synth_norm_weight(n, 98)
+    assert np.array_equal(bits(a.download(count=n)), bits(orc.synth_normal(99, n)))
+    assert np.array_equal(bits(b.download(count=n)), bits(orc.synth_norm_weight(98, n)))
+
+
+SHAPES = [
+    (Q4_K, 1, 256), (Q4_K, 8, 512), (Q4_K, 64, 1024), (Q4_K, 37, 5632), (Q4_K, 1024, 4096),
+    (Q4_K, 4096, 4096), (Q4_K, 301, 14336), (Q4_K, 5632, 2048),
+    (Q6_K, 1, 256), (Q6_K, 8, 512), (Q6_K, 64, 1024), (Q6_K, 37, 5632), (Q6_K, 1024, 4096),
+    (Q6_K, 4096, 4096), (Q6_K, 301, 14336), (Q6_K, 2048, 5632),
+    (Q8_0, 1, 32), (Q8_0, 8, 512), (Q8_0, 33, 1024), (Q8_0, 64, 4096),
+]
+
+
+@pytest.mark.parametrize("dt,rows,cols", SHAPES)
+def test_matvec_vs_oracle(ctx, orc, dt, rows, cols):
+    seed = (dt << 20) ^ (rows << 8) ^ cols
+    w = orc.synth_quant(dt, seed, rows, cols)
+    x = orc.synth_normal(seed + 1, cols)
+    wd = ctx.upload_weight(w)
+    rc, y = ctx.matvec_host(dt, wd, rows, cols, x, byte_size=w.nbytes)
+    assert rc == 0
+    ref = orc.matvec(dt, w, rows, cols, x)
+    assert rel_l2(y, ref) < MV_TOL
+    # every row, not just the norm: no row may be dropped or swapped
+    scale = np.abs(ref).max() + 1e-30
+    assert np.abs(y - ref).max() / scale < 1e-5
+    C.CDLL(None)  # keep ctypes imported for linters
+    __import__("guanaco_amd.hip").hip.lib.gq_hip_free(ctx.h, wd)
+
+
+def test_matvec_error_codes(ctx):
+    """The vtable convention (quant_matvec_q4_k.c:143-158, test_backend.c:71-86):
+    NULL/zeroed tensor -1, cols % 256 -2, short byte_size -3."""
+    w = np.zeros(144 * 4, np.uint8)
+    wd = ctx.upload_weight(w)
+    x = np.zeros(1024, np.float32)
+    assert ctx.matvec_host(Q4_K, None, 1, 1024, x)[0] == -1
+    assert ctx.matvec_host(99, wd, 1, 1024, x)[0] == -1
+    assert ctx.matvec_host(Q4_K, wd, 1, 1000, x)[0] == -2
+    assert ctx.matvec_host(Q4_K, wd, 1, 1024, x, byte_size=144 * 4 - 1)[0] == -3
+    assert ctx.matvec_host(Q4_K, wd, 1, 1024, x, byte_size=144 * 4)[0] == 0
+    assert ctx.matvec_host(Q4_K, wd, 0, 1024, x)[0] == -1
+
+
+def test_q4k_known_answers(ctx):
+    """test_quant.c:94-139 (384) through the GPU kernel."""
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = [0x00, 0x3C]
+    blk[4:16] = 1
+    blk[16:] = 0x12
+    wd = ctx.upload_weight(blk)
+    rc, y = ctx.matvec_host(Q4_K, wd, 1, 256, np.ones(256, np.float32))
+    assert rc == 0 and abs(y[0] - 384.0) < 1e-4
+
+
+def test_rmsnorm(ctx, orc):
+    n = 4096
+    x = orc.synth_normal(3, n) * np.float32(7.0)
+    w = orc.synth_norm_weight(4, n)
+    xb, wb, ob = ctx.upload(x), ctx.upload(w), ctx.alloc(4 * n)
+    ctx.rmsnorm_dev(xb, wb, ob, n, 1e-6)
+    assert rel_l2(ob.download(), orc.rmsnorm(x, w, 1e-6)) < 1e-6
+
+
+@pytest.mark.parametrize("dt", [Q4_K, Q8_0, F32])
+def test_embedding_row_bitexact(ctx, orc, dt):
+    """Embedding dequant rounds like engine.c:241-276: bit-identical rows."""
+    vocab, H = 50, 512
+    if dt == F32:
+        table = orc.synth_normal(5, vocab * H)
+        raw = table.view(np.uint8)
+    else:
+        raw = orc.synth_quant(dt, 5, vocab, H)
+    td = ctx.upload_weight(raw)
+    t = OrcTensor(dt, vocab, H, u8ptr(raw), raw.nbytes)
+    ob = ctx.alloc(4 * H)
+    for tok in (0, 17, vocab - 1):
+        ctx.embed_dev(dt, td, H, tok, ob)
+        exp = np.empty(H, np.float32)
+        orc.lib.orc_embed(C.byref(t), tok, fptr(exp))
+        assert np.array_equal(bits(ob.download()), bits(exp)), tok
+
+
+def test_argmax_first_max(ctx):
+    """Ties go to the lowest index (tokenizer.c:175-185)."""
+    assert ctx.argmax_dev(ctx.upload(np.array([3, 1, 3, 2], np.float32)), 4) == 0
+    x = np.random.default_rng(0).standard_normal(128256).astype(np.float32)
+    x[[70000, 5000, 120000]] = 50.0
+    assert ctx.argmax_dev(ctx.upload(x), x.size) == 5000
+    x[:] = -np.inf
+    assert ctx.argmax_dev(ctx.upload(x), x.size) == 0
+
+
+def test_silu_mul(ctx, orc):
+    n = 14336
+    g = orc.synth_normal(1, n) * np.float32(4)
+    u = orc.synth_normal(2, n)
+    gb, ub = ctx.upload(g), ctx.upload(u)
+    ctx.silu_mul_dev(gb, ub, n)
+    gg = g.copy()
+    orc.lib.orc_silu(fptr(gg), n)
+    assert rel_l2(gb.download(), gg * u) < 1e-6

@@ -1,0 +1,116 @@
+"""BACKEND_HIP behind the reference's KernelVTable (guanaco_amd/host).
+
+The CPU tests check the factory conventions of backend.c:5-66 and
+test_backend.c: a HIP request without a device is NULL, AUTO falls back to
+the CPU backend, dense slots are the CPU kernels, a zeroed Tensor is
+rejected.  The GPU test is the drop-in itself: the reference's compiled
+engine (oracle/_ref/libref.so: forward(), linear_dispatch, its CPU dense
+kernels) runs a whole decode step through the HIP backend's vtable with
+device-resident weights, and matches the all-CPU reference."""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+from oracle import (Q4_K, HostModel, RBackendConfig, RefModel, RTensor, fptr, ref_available,
+                    rtensor)
+from guanaco_amd import spec as S
+from util import rel_l2
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HOST_SO = os.path.join(ROOT, "guanaco_amd", "libgq_host.so")
+BACKEND_AUTO, BACKEND_CPU, BACKEND_HIP = -1, 0, 2
+
+
+class VTable(C.Structure):  # backend.h:20-39
+    _fields_ = [(n, C.c_void_p) for n in ("gemm_f32", "gemm_f32_nn", "rmsnorm", "softmax_inplace",
+                                          "silu_inplace", "rope", "residual_add", "elemwise_mul",
+                                          "matvec_q4k_f32", "matvec_q6k_f32", "matvec_q8_0_f32")]
+
+
+@pytest.fixture(scope="module")
+def host(ref):
+    lib = C.CDLL(HOST_SO)
+    lib.backend_create.argtypes = [C.POINTER(RBackendConfig)]
+    lib.backend_create.restype = C.c_void_p
+    lib.backend_kind.argtypes = [C.c_void_p]
+    lib.backend_kernels.argtypes = [C.c_void_p]
+    lib.backend_kernels.restype = C.POINTER(VTable)
+    lib.backend_destroy.argtypes = [C.c_void_p]
+    lib.hip_backend_upload.argtypes = [C.c_void_p, C.POINTER(RTensor)]
+    lib.hip_backend_context.argtypes = [C.c_void_p]
+    lib.hip_backend_context.restype = C.c_void_p
+    return lib
+
+
+MATVEC = C.CFUNCTYPE(C.c_int, C.POINTER(RTensor), C.POINTER(C.c_float), C.POINTER(C.c_float))
+
+
+def test_factory_without_device(host, ref):
+    import guanaco_amd.hip as H
+    if H.device_count() > 0:
+        pytest.skip("a GPU is present")
+    assert not host.backend_create(C.byref(RBackendConfig(BACKEND_HIP, 2, 0, 0)))
+    b = host.backend_create(C.byref(RBackendConfig(BACKEND_AUTO, 2, 0, 0)))
+    assert b and host.backend_kind(b) == BACKEND_CPU
+    host.backend_destroy(b)
+
+
+def test_cpu_vtable_conventions(host, ref):
+    b = host.backend_create(C.byref(RBackendConfig(BACKEND_CPU, 2, 0, 0)))
+    assert b and host.backend_kind(b) == BACKEND_CPU
+    vt = host.backend_kernels(b).contents
+    assert all(getattr(vt, f) for f, _ in VTable._fields_)
+    # zeroed tensor must fail (test_backend.c:71-86)
+    W = RTensor()
+    x = np.zeros(1, np.float32)
+    y = np.zeros(1, np.float32)
+    assert MATVEC(vt.matvec_q4k_f32)(C.byref(W), fptr(x), fptr(y)) != 0
+    assert MATVEC(vt.matvec_q8_0_f32)(C.byref(W), fptr(x), fptr(y)) != 0
+    # gemm KAT through the vtable (test_backend.c:55-77)
+    GEMM = C.CFUNCTYPE(None, C.POINTER(RTensor), C.POINTER(RTensor), C.POINTER(RTensor))
+    a = np.array([1, 2, 3, 4, 5, 6], np.float32)
+    bm = np.array([7, 8, 9, 10, 11, 12], np.float32)
+    c = np.zeros(4, np.float32)
+    A, B, Cc = rtensor(a, 0, (2, 3)), rtensor(bm, 0, (2, 3)), rtensor(c, 0, (2, 2))
+    GEMM(vt.gemm_f32)(C.byref(A), C.byref(B), C.byref(Cc))
+    assert np.allclose(c, [50, 68, 122, 167])
+    host.backend_destroy(b)
+
+
+@pytest.mark.gpu
+def test_reference_engine_through_hip_vtable(host, ref, orc):
+    """Drop-in: reference forward() + HIP vtable with device-resident weights."""
+    spec, ms, pre = S.TINY_TEST, 64, 24
+    b = host.backend_create(C.byref(RBackendConfig(BACKEND_HIP, 4, 0, spec.n_layers)))
+    assert b, "HIP backend unavailable on a GPU box"
+    assert host.backend_kind(b) == BACKEND_HIP and host.hip_backend_context(b)
+    hm = HostModel(orc, spec, ms)
+    cpu = RefModel(ref, hm)
+    gpu = RefModel(ref, hm)
+    kv = hm.new_kv()
+    kv.prefill(orc, spec, pre)
+    cpu.load_kv(kv)
+    gpu.load_kv(kv)
+    # --n-gpu-layers split (loader.c:677-729): first layer GPU-resident only
+    n_gpu = 1
+    lay = gpu.mw.layers
+    for l in range(n_gpu):
+        for f in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down"):
+            assert host.hip_backend_upload(b, getattr(lay[l], f)) == 0
+            assert getattr(lay[l], f).contents.device_residency == 1
+    assert host.hip_backend_upload(b, gpu.mw.lm_head) == 0
+    hip_vt = C.cast(host.backend_kernels(b), C.c_void_p)
+    tok_c = tok_g = 9
+    for step in range(4):
+        tok_c, lc = cpu.forward(tok_c, pre + step)
+        out = ref.lib.forward(C.byref(gpu.mw), gpu.kv, gpu.scratch, (C.c_int * 1)(tok_g), 1,
+                              pre + step, hip_vt)
+        lg = np.ctypeslib.as_array(C.cast(out.contents.data, C.POINTER(C.c_float)),
+                                   shape=(spec.vocab,)).copy()
+        tok_g = int(ref.lib.sample_greedy(fptr(lg), spec.vocab))
+        assert rel_l2(lg, lc) < 1e-3 and tok_g == tok_c, step
+    cpu.close()
+    gpu.close()
+    host.backend_destroy(b)
