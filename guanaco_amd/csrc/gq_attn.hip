@@ -63,179 +63,202 @@ __global__ __launch_bounds__(kThreads) void rope_append_kernel(RopeArgs a) {
   }
 }
 
-/* Chunk c of [0, L): length S = ceil(L/nch) rounded up to 16. */
-__device__ __forceinline__ void chunk_range(int L, int nch, int c, int &c0, int &c1) {
-  int S = (L + nch - 1) / nch;
-  S = (S + 15) & ~15;
-  c0 = c * S;
-  c1 = min(L, c0 + S);
-}
+/* Positions per split-K chunk (one workgroup). */
+constexpr int kChunk = 128;
 
+/* Workgroup (g, c) handles positions [128c, 128c + 128) of KV head g for the
+ * G query heads sharing it.  Every K and V load of the chunk is issued before
+ * any arithmetic (64 + 64 VGPRs per thread at head_dim 128), so a workgroup
+ * costs one memory round trip plus its FMAs. */
 template <int HD, int G>
 __global__ __launch_bounds__(kThreads) void attn_partial_kernel(AttnArgs a) {
-  constexpr int LPP = HD / 8;         /* lanes per position in phase 1 */
-  constexpr int PPW = GQ_WAVE / LPP;  /* positions per wave step */
-  constexpr int DG = HD / 4;          /* float4 dim groups in phase 3 */
-  constexpr int NPG = kThreads / DG;  /* position groups in phase 3 */
-  extern __shared__ float sm[];
-  float *sq = sm;                     /* [G][HD] */
-  float *ss = sq + G * HD;            /* [G][s_max] scores / probabilities */
-  float *sr = ss + G * a.s_max;       /* [NPG][G][HD] phase-3 partials */
+  constexpr int S = kChunk;
+  constexpr int LPP = HD / 8;          /* lanes per position, phase 1 */
+  constexpr int PPI = kThreads / LPP;  /* positions per pass, phase 1 */
+  constexpr int KIT = S / PPI;
+  constexpr int DG = HD / 4;           /* float4 columns of a V row */
+  constexpr int NPG = kThreads / DG;   /* position groups, phase 3 */
+  constexpr int VIT = S / NPG;
+  __shared__ float ss[G][S];
+  __shared__ float4 sr[NPG][G][DG];
 
-  const int g = blockIdx.x, c = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int pos = a.pos_dev ? *a.pos_dev : a.pos;
+  const int g = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int pos = a.pos_dev ? gld<int>(a.pos_dev) : a.pos;
   const int L = min(pos + 1, a.max_seq);
-  int c0, c1;
-  chunk_range(L, a.nch, c, c0, c1);
+  const int c0 = c * S;
+  const int n = min(S, L - c0);
+  if (n <= 0) return; /* past the sequence: the merge reads chunks < ceil(L/S) */
   const int h0 = g * G;
-  const size_t obase = ((size_t)h0 * a.nch + c);
+  const float *K = a.k + ((size_t)g * a.max_seq + c0) * HD;
+  const float *V = a.v + ((size_t)g * a.max_seq + c0) * HD;
 
-  if (c0 >= c1) { /* empty chunk: neutral element of the merge */
-    for (int t = tid; t < G * HD; t += kThreads) {
-      const int h = t / HD, d = t - h * HD;
-      a.part_o[(obase + (size_t)h * a.nch) * HD + d] = 0.f;
-    }
-    if (tid < G) {
-      a.part_ml[(obase + (size_t)tid * a.nch) * 2] = -INFINITY;
-      a.part_ml[(obase + (size_t)tid * a.nch) * 2 + 1] = 0.f;
-    }
-    return;
+  /* V rows of phase 3 first: they do not depend on the scores */
+  const int dg = tid % DG, pg = tid / DG;
+  float4 vr[VIT];
+#pragma unroll
+  for (int k = 0; k < VIT; k++) vr[k] = gld<float4>(V + (size_t)min(pg + NPG * k, n - 1) * HD + 4 * dg);
+  /* query slices and K rows of phase 1 */
+  const int sub = tid % LPP, pw = tid / LPP;
+  const int d0 = 4 * sub, d1 = HD / 2 + 4 * sub;
+  float4 qa[G], qb[G];
+#pragma unroll
+  for (int h = 0; h < G; h++) {
+    qa[h] = gld<float4>(a.q + (size_t)(h0 + h) * HD + d0);
+    qb[h] = gld<float4>(a.q + (size_t)(h0 + h) * HD + d1);
+  }
+  float4 ka[KIT], kb[KIT];
+#pragma unroll
+  for (int k = 0; k < KIT; k++) {
+    const float *kr = K + (size_t)min(pw + PPI * k, n - 1) * HD;
+    ka[k] = gld<float4>(kr + d0);
+    kb[k] = gld<float4>(kr + d1);
   }
 
-  for (int t = tid; t < G * HD; t += kThreads) sq[t] = a.q[(size_t)h0 * HD + t];
-  __syncthreads();
-
-  const float *K = a.k + (size_t)g * a.max_seq * HD;
-  const float *V = a.v + (size_t)g * a.max_seq * HD;
-
-  /* ---- phase 1: scores ---- */
-  {
-    const int sub = lane % LPP, pw = lane / LPP;
-    const int d0 = 4 * sub, d1 = HD / 2 + 4 * sub;
-    float q0[G][4], q1[G][4];
+  /* phase 1: scores (q . k) * 1/sqrt(hd) */
 #pragma unroll
-    for (int h = 0; h < G; h++)
+  for (int k = 0; k < KIT; k++) {
+    const int j = pw + PPI * k;
 #pragma unroll
-      for (int e = 0; e < 4; e++) q0[h][e] = sq[h * HD + d0 + e], q1[h][e] = sq[h * HD + d1 + e];
-    for (int j0 = c0 + wave * PPW; j0 < c1; j0 += 4 * PPW) {
-      const int j = j0 + pw;
-      const bool ok = j < c1;
-      const float *kr = K + (size_t)(ok ? j : c0) * HD;
-      const float4 ka = *(const float4 *)(kr + d0), kb = *(const float4 *)(kr + d1);
-#pragma unroll
-      for (int h = 0; h < G; h++) {
-        float s = q0[h][0] * ka.x;
-        s = __builtin_fmaf(q0[h][1], ka.y, s);
-        s = __builtin_fmaf(q0[h][2], ka.z, s);
-        s = __builtin_fmaf(q0[h][3], ka.w, s);
-        s = __builtin_fmaf(q1[h][0], kb.x, s);
-        s = __builtin_fmaf(q1[h][1], kb.y, s);
-        s = __builtin_fmaf(q1[h][2], kb.z, s);
-        s = __builtin_fmaf(q1[h][3], kb.w, s);
-        s = LPP == 16 ? gq_row16_sum(s) : gq_row8_sum(s);
-        if (ok && sub == 0) ss[h * a.s_max + (j - c0)] = s * a.scale;
-      }
+    for (int h = 0; h < G; h++) {
+      float s = qa[h].x * ka[k].x;
+      s = __builtin_fmaf(qa[h].y, ka[k].y, s);
+      s = __builtin_fmaf(qa[h].z, ka[k].z, s);
+      s = __builtin_fmaf(qa[h].w, ka[k].w, s);
+      s = __builtin_fmaf(qb[h].x, kb[k].x, s);
+      s = __builtin_fmaf(qb[h].y, kb[k].y, s);
+      s = __builtin_fmaf(qb[h].z, kb[k].z, s);
+      s = __builtin_fmaf(qb[h].w, kb[k].w, s);
+      s = LPP == 16 ? gq_row16_sum(s) : gq_row8_sum(s);
+      if (sub == 0 && j < n) ss[h][j] = s * a.scale;
     }
   }
   __syncthreads();
 
-  /* ---- phase 2: chunk softmax statistics per head ---- */
-  const int n = c1 - c0;
+  /* phase 2: chunk max, exponentials and their sum per head */
+  const size_t ml = (size_t)a.nch * 2;
   for (int h = wave; h < G; h += kThreads / GQ_WAVE) {
-    float *row = ss + h * a.s_max;
     float m = -INFINITY;
-    for (int j = lane; j < n; j += GQ_WAVE) m = fmaxf(m, row[j]);
+    for (int j = lane; j < n; j += GQ_WAVE) m = fmaxf(m, ss[h][j]);
     m = gq_wave_max(m);
     float l = 0.f;
     for (int j = lane; j < n; j += GQ_WAVE) {
-      const float e = expf(row[j] - m);
-      row[j] = e;
+      const float e = expf(ss[h][j] - m);
+      ss[h][j] = e;
       l += e;
     }
     l = gq_wave_sum(l);
     if (lane == 0) {
-      a.part_ml[(obase + (size_t)h * a.nch) * 2] = m;
-      a.part_ml[(obase + (size_t)h * a.nch) * 2 + 1] = l;
+      gst<float>(a.part_ml + (size_t)(h0 + h) * ml + 2 * c, m);
+      gst<float>(a.part_ml + (size_t)(h0 + h) * ml + 2 * c + 1, l);
     }
   }
   __syncthreads();
 
-  /* ---- phase 3: o = P V over the chunk ---- */
-  {
-    const int dg = tid % DG, pg = tid / DG;
-    float acc[G][4];
+  /* phase 3: o = sum_j p_j V_j over the chunk */
+  float4 acc[G];
 #pragma unroll
-    for (int h = 0; h < G; h++) acc[h][0] = acc[h][1] = acc[h][2] = acc[h][3] = 0.f;
-    for (int j = c0 + pg; j < c1; j += NPG) {
-      const float4 v = *(const float4 *)(V + (size_t)j * HD + 4 * dg);
+  for (int h = 0; h < G; h++) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int k = 0; k < VIT; k++) {
+    const int j = pg + NPG * k;
+    if (j < n) {
 #pragma unroll
       for (int h = 0; h < G; h++) {
-        const float p = ss[h * a.s_max + (j - c0)];
-        acc[h][0] = __builtin_fmaf(p, v.x, acc[h][0]);
-        acc[h][1] = __builtin_fmaf(p, v.y, acc[h][1]);
-        acc[h][2] = __builtin_fmaf(p, v.z, acc[h][2]);
-        acc[h][3] = __builtin_fmaf(p, v.w, acc[h][3]);
+        const float p = ss[h][j];
+        acc[h].x = __builtin_fmaf(p, vr[k].x, acc[h].x);
+        acc[h].y = __builtin_fmaf(p, vr[k].y, acc[h].y);
+        acc[h].z = __builtin_fmaf(p, vr[k].z, acc[h].z);
+        acc[h].w = __builtin_fmaf(p, vr[k].w, acc[h].w);
       }
     }
-#pragma unroll
-    for (int h = 0; h < G; h++)
-      *(float4 *)(sr + ((size_t)pg * G + h) * HD + 4 * dg) =
-          make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
   }
+#pragma unroll
+  for (int h = 0; h < G; h++) sr[pg][h][dg] = acc[h];
   __syncthreads();
-  for (int t = tid; t < G * HD; t += kThreads) {
-    float o = 0.f;
-#pragma unroll 4
-    for (int pg = 0; pg < NPG; pg++) o += sr[(size_t)pg * G * HD + t];
-    const int h = t / HD, d = t - h * HD;
-    a.part_o[(obase + (size_t)h * a.nch) * HD + d] = o;
+  for (int t = tid; t < G * DG; t += kThreads) {
+    const int h = t / DG, q = t - h * DG;
+    float4 o = sr[0][h][q];
+#pragma unroll
+    for (int p = 1; p < NPG; p++) {
+      const float4 u = sr[p][h][q];
+      o.x += u.x, o.y += u.y, o.z += u.z, o.w += u.w;
+    }
+    gst<float4>(a.part_o + ((size_t)(h0 + h) * a.nch + c) * HD + 4 * q, o);
   }
 }
 
-__global__ void attn_merge_kernel(AttnArgs a) {
-  const int h = blockIdx.x, d = threadIdx.x;
+/* Merge the chunks of one query head for 32 of its dimensions:
+ * out = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M). */
+__global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
+  extern __shared__ float sw[]; /* [nch] weights e^(m_c - M), then l_c */
+  __shared__ float red[kThreads / GQ_WAVE];
+  __shared__ float sacc[kThreads / 32][32];
+  const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int pos = a.pos_dev ? gld<int>(a.pos_dev) : a.pos;
+  const int L = min(pos + 1, a.max_seq);
+  const int nc = (L + kChunk - 1) / kChunk;
   const float *ml = a.part_ml + (size_t)h * a.nch * 2;
-  float M = -INFINITY;
-  for (int c = 0; c < a.nch; c++) M = fmaxf(M, ml[2 * c]);
-  float o = 0.f, l = 0.f;
-  for (int c = 0; c < a.nch; c++) {
-    const float m = ml[2 * c];
-    if (m == -INFINITY) continue;
-    const float w = expf(m - M);
-    l = __builtin_fmaf(ml[2 * c + 1], w, l);
-    o = __builtin_fmaf(a.part_o[((size_t)h * a.nch + c) * a.hd + d], w, o);
+  float *sl = sw + a.nch;
+  float m = -INFINITY;
+  for (int c = tid; c < nc; c += kThreads) {
+    const float mc = gld<float>(ml + 2 * c);
+    sw[c] = mc;
+    sl[c] = gld<float>(ml + 2 * c + 1);
+    m = fmaxf(m, mc);
   }
-  a.out[(size_t)h * a.hd + d] = o / l;
+  m = gq_wave_max(m);
+  if (lane == 0) red[wave] = m;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float l = 0.f;
+  for (int c = tid; c < nc; c += kThreads) {
+    const float w = expf(sw[c] - M);
+    sw[c] = w;
+    l = __builtin_fmaf(sl[c], w, l);
+  }
+  l = gq_wave_sum(l);
+  __syncthreads();
+  if (lane == 0) red[wave] = l;
+  __syncthreads();
+  const float Ls = (red[0] + red[1]) + (red[2] + red[3]);
+  const int d = blockIdx.y * 32 + (tid & 31), cg = tid >> 5;
+  const float *o = a.part_o + (size_t)h * a.nch * a.hd + d;
+  float acc = 0.f;
+#pragma unroll 8
+  for (int c = cg; c < nc; c += kThreads / 32) acc = __builtin_fmaf(gld<float>(o + (size_t)c * a.hd), sw[c], acc);
+  sacc[cg][tid & 31] = acc;
+  __syncthreads();
+  if (tid < 32) {
+    float t = 0.f;
+#pragma unroll
+    for (int k = 0; k < kThreads / 32; k++) t += sacc[k][tid];
+    gst<float>(a.out + (size_t)h * a.hd + d, t / Ls);
+  }
 }
 
 template <int HD, int G>
 int launch_partial(const AttnArgs &a, hipStream_t s) {
-  constexpr int NPG = kThreads / (HD / 4);
-  const size_t lds = sizeof(float) * ((size_t)G * HD + (size_t)G * a.s_max + (size_t)NPG * G * HD);
-  if (lds > 65536) return -1;
-  hipLaunchKernelGGL((attn_partial_kernel<HD, G>), dim3(a.n_kv, a.nch), dim3(kThreads), lds, s, a);
+  hipLaunchKernelGGL((attn_partial_kernel<HD, G>), dim3(a.n_kv, a.nch), dim3(kThreads), 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
 } // namespace
 
 int gq_attn_nch(int n_kv, int max_seq) {
-  /* about 512 workgroups (2 per CU) for long contexts, at least 64
-   * positions per chunk */
-  int nch = (512 + n_kv - 1) / n_kv;
-  const int by_len = (max_seq + 63) / 64;
-  if (nch > by_len) nch = by_len;
-  return nch < 1 ? 1 : nch;
+  (void)n_kv;
+  return (max_seq + kChunk - 1) / kChunk;
 }
 
 int gq_attn_smax(int max_seq, int nch) {
-  int S = (max_seq + nch - 1) / nch;
-  return (S + 15) & ~15;
+  (void)max_seq;
+  (void)nch;
+  return kChunk;
 }
 
 int gq_launch_attention(const AttnArgs &a, hipStream_t s, hipEvent_t mid) {
-  if (a.n_kv <= 0 || a.n_heads % a.n_kv) return -1;
+  if (a.n_kv <= 0 || a.n_heads % a.n_kv || a.nch != gq_attn_nch(a.n_kv, a.max_seq)) return -1;
+  if (a.hd % 32 || (size_t)a.nch * 2 * sizeof(float) > 32768) return -1;
   const int G = a.n_heads / a.n_kv;
   int rc = -1;
   if (a.hd == 128 && G == 4) rc = launch_partial<128, 4>(a, s);
@@ -246,7 +269,8 @@ int gq_launch_attention(const AttnArgs &a, hipStream_t s, hipEvent_t mid) {
   else if (a.hd == 64 && G == 1) rc = launch_partial<64, 1>(a, s);
   if (rc) return rc;
   if (mid) (void)hipEventRecord(mid, s);
-  hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_heads), dim3(a.hd), 0, s, a);
+  hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_heads, a.hd / 32), dim3(kThreads),
+                     (size_t)a.nch * 2 * sizeof(float), s, a);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 

@@ -18,6 +18,76 @@
 
 typedef uint32_t gq_u32x3 __attribute__((ext_vector_type(3), aligned(4)));
 
+/* Global-address-space accesses.  Pointers read out of kernel-argument
+ * structs lose their address space and would otherwise compile to FLAT
+ * instructions, which count against the LDS wait counter as well: every
+ * s_waitcnt for an LDS read would then also wait for the in-flight HBM loads
+ * and serialise the prefetching. */
+#define GQ_GLOBAL __attribute__((address_space(1)))
+
+/* Native clang vector of the same size as T (HIP's float4 / uint4 are
+ * classes whose constructors cannot bind address-space-qualified
+ * references). */
+template <int N>
+struct gq_native;
+template <>
+struct gq_native<2> {
+  typedef unsigned short type;
+};
+template <>
+struct gq_native<4> {
+  typedef unsigned int type;
+};
+template <>
+struct gq_native<8> {
+  typedef unsigned int type __attribute__((ext_vector_type(2)));
+};
+template <>
+struct gq_native<16> {
+  typedef unsigned int type __attribute__((ext_vector_type(4)));
+};
+
+template <class T>
+__device__ __forceinline__ T gld(const void *p) {
+  typedef typename gq_native<sizeof(T)>::type N;
+  return __builtin_bit_cast(T, *(const GQ_GLOBAL N *)p);
+}
+
+/* 12-byte load (three dwords, 4-byte aligned) */
+__device__ __forceinline__ uint3 gld12(const void *p) {
+  typedef unsigned int N __attribute__((ext_vector_type(3), aligned(4)));
+  const N v = *(const GQ_GLOBAL N *)p;
+  return make_uint3(v.x, v.y, v.z);
+}
+
+template <class T>
+__device__ __forceinline__ void gst(void *p, T v) {
+  typedef typename gq_native<sizeof(T)>::type N;
+  *(GQ_GLOBAL N *)p = __builtin_bit_cast(N, v);
+}
+
+/* LDS accesses through explicit local-address-space pointers (byte offsets
+ * into the workgroup's LDS allocation). */
+#define GQ_LDS __attribute__((address_space(3)))
+
+template <class T>
+__device__ __forceinline__ T lld(const GQ_LDS uint8_t *base, uint32_t off) {
+  typedef typename gq_native<sizeof(T)>::type N;
+  return __builtin_bit_cast(T, *(const GQ_LDS N *)(base + off));
+}
+
+/* Eight bytes at a 2-byte-aligned LDS offset: three aligned dword reads and
+ * two funnel shifts (reads up to 4 bytes past the field). */
+__device__ __forceinline__ uint2 lld8_a2(const GQ_LDS uint8_t *base, uint32_t off) {
+  const uint32_t a = off & ~3u, sh = off & 3u;
+  const uint32_t w0 = lld<uint32_t>(base, a), w1 = lld<uint32_t>(base, a + 4),
+                 w2 = lld<uint32_t>(base, a + 8);
+  uint2 r;
+  r.x = __builtin_amdgcn_alignbyte(w1, w0, sh);
+  r.y = __builtin_amdgcn_alignbyte(w2, w1, sh);
+  return r;
+}
+
 __device__ __forceinline__ float gq_h2f(uint32_t h16) {
   return (float)__builtin_bit_cast(_Float16, (unsigned short)(h16 & 0xffffu));
 }
@@ -65,7 +135,7 @@ __device__ __forceinline__ float gq_wave_max(float v) {
  * 8 requested (callers keep that inside the block). */
 __device__ __forceinline__ uint2 gq_load8_a2(const uint8_t *p) {
   const uintptr_t a = (uintptr_t)p;
-  const gq_u32x3 w = *(const gq_u32x3 *)(a & ~(uintptr_t)3);
+  const uint3 w = gld12((const void *)(a & ~(uintptr_t)3));
   const uint32_t sh = (uint32_t)(a & 3u);
   uint2 r;
   r.x = __builtin_amdgcn_alignbyte(w.y, w.x, sh);

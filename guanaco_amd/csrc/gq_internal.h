@@ -22,11 +22,28 @@
  */
 enum { MV_STORE = 0, MV_RESID = 1, MV_SWIGLU = 2 };
 
+/* Per-segment output kind of MV_STORE launches (the fused q/k/v epilogue):
+ *   SEG_PLAIN  y[r] = (W x)[r]
+ *   SEG_ROPE   rows (2i, 2i+1) of each head rotated by the RoPE table row of
+ *              pos, stored to y (the query)
+ *   SEG_ROPE_KV rotated, stored into the K cache slab at pos
+ *   SEG_KV     stored into the V cache slab at pos
+ * Cache row r = h*head_dim + d lands at ((h*max_seq + pos)*head_dim + d). */
+enum { SEG_PLAIN = 0, SEG_ROPE = 1, SEG_ROPE_KV = 2, SEG_KV = 3 };
+
 struct MvSeg {
   const uint8_t *w;
   float *y;
   const float *r;
   int rows;
+  int kind;
+};
+
+struct MvRope {
+  const float2 *cs; /* [max_seq][head_dim/2] (cos, sin) */
+  const int *pos_dev;
+  int pos;
+  int head_dim, max_seq;
 };
 
 struct MvArgs {
@@ -36,9 +53,12 @@ struct MvArgs {
   const float *x;
   const float *norm_w;
   float eps;
+  MvRope rope;
 };
 
 int gq_launch_matvec(int dtype, int mode, const MvArgs &a, hipStream_t s);
+/* workgroups the matvec launcher puts on the device at most (persistent grid) */
+void gq_matvec_set_cus(int n_cu);
 
 /* ---- attention -------------------------------------------------------- */
 struct AttnArgs {

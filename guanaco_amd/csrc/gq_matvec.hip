@@ -25,6 +25,8 @@
  * d*sc*(q-32) for Q6_K, d*q for Q8_0) with a different summation order; the
  * parity tests hold it to a relative-L2 tolerance against the CPU order.
  */
+#include <stdlib.h>
+
 #include "gq_device.h"
 #include "gq_internal.h"
 
@@ -68,8 +70,37 @@ struct Tr<GQ_Q4_K> {
   }
   __device__ static void load(Frag &f, const uint8_t *row, int b, int p) {
     const uint8_t *blk = row + (size_t)b * BB;
-    f.h = *(const uint4 *)blk;
-    f.q = *(const uint4 *)(blk + 16 + 16 * p);
+    f.h = gld<uint4>(blk);
+    f.q = gld<uint4>(blk + 16 + 16 * p);
+  }
+  __device__ static void load_lds(Frag &f, const GQ_LDS uint8_t *base, uint32_t blk, int p) {
+    f.h = lld<uint4>(base, blk);
+    f.q = lld<uint4>(base, blk + 16 + 16 * p);
+  }
+  /* x slice straight from global memory, times the RMSNorm weight when given;
+   * ss accumulates the raw x^2 of the slice */
+  __device__ static void load_xg(X &x, const float *xg, const float *nw, int b, int p, float &ss) {
+    const int base = 256 * b + 64 * (p >> 1) + 16 * (p & 1);
+    float sl = 0.f, sh = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      float4 u = gld<float4>(xg + base + 4 * k), v = gld<float4>(xg + base + 32 + 4 * k);
+      ss = __builtin_fmaf(u.x, u.x, ss), ss = __builtin_fmaf(u.y, u.y, ss);
+      ss = __builtin_fmaf(u.z, u.z, ss), ss = __builtin_fmaf(u.w, u.w, ss);
+      ss = __builtin_fmaf(v.x, v.x, ss), ss = __builtin_fmaf(v.y, v.y, ss);
+      ss = __builtin_fmaf(v.z, v.z, ss), ss = __builtin_fmaf(v.w, v.w, ss);
+      if (nw) {
+        const float4 wu = gld<float4>(nw + base + 4 * k), wv = gld<float4>(nw + base + 32 + 4 * k);
+        u = make_float4(wu.x * u.x, wu.y * u.y, wu.z * u.z, wu.w * u.w);
+        v = make_float4(wv.x * v.x, wv.y * v.y, wv.z * v.z, wv.w * v.w);
+      }
+      x.lo[4 * k] = u.x, x.lo[4 * k + 1] = u.y, x.lo[4 * k + 2] = u.z, x.lo[4 * k + 3] = u.w;
+      x.hi[4 * k] = v.x, x.hi[4 * k + 1] = v.y, x.hi[4 * k + 2] = v.z, x.hi[4 * k + 3] = v.w;
+      sl += (u.x + u.y) + (u.z + u.w);
+      sh += (v.x + v.y) + (v.z + v.w);
+    }
+    x.slo = sl;
+    x.shi = sh;
   }
   __device__ static float dot(const Frag &f, const X &x, int p) {
     const float d = gq_h2f(f.h.x), dm = gq_h2f(f.h.x >> 16);
@@ -110,7 +141,7 @@ struct Tr<GQ_Q4_K> {
 __device__ __forceinline__ uint2 load8_back(const uint8_t *p) {
   const uintptr_t a = (uintptr_t)p;
   const uintptr_t base = (a - 2) & ~(uintptr_t)3;
-  const gq_u32x3 w = *(const gq_u32x3 *)base;
+  const uint3 w = gld12((const void *)base);
   uint2 r;
   if (a - base == 4) {
     r.x = w.y, r.y = w.z;
@@ -154,7 +185,34 @@ struct Tr<GQ_Q6_K> {
     f.b = gq_load8_a2(blk + 64 * h + 32 + l0);
     f.h = gq_load8_a2(blk + 128 + 32 * h + l0);
     f.s = load8_back(blk + 192 + 8 * h);
-    f.d = *(const uint16_t *)(blk + 208);
+    f.d = gld<uint16_t>(blk + 208);
+  }
+  __device__ static void load_lds(Frag &f, const GQ_LDS uint8_t *base, uint32_t blk, int p) {
+    const int h = p >> 2, l0 = 8 * (p & 3);
+    f.a = lld8_a2(base, blk + 64 * h + l0);
+    f.b = lld8_a2(base, blk + 64 * h + 32 + l0);
+    f.h = lld8_a2(base, blk + 128 + 32 * h + l0);
+    f.s = lld8_a2(base, blk + 192 + 8 * h);
+    f.d = lld<uint16_t>(base, blk + 208);
+  }
+  __device__ static void load_xg(X &x, const float *xg, const float *nw, int b, int p, float &ss) {
+    const int base = 256 * b + 128 * (p >> 2) + 8 * (p & 3);
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      float4 u = gld<float4>(xg + base + 32 * r), v = gld<float4>(xg + base + 32 * r + 4);
+      ss = __builtin_fmaf(u.x, u.x, ss), ss = __builtin_fmaf(u.y, u.y, ss);
+      ss = __builtin_fmaf(u.z, u.z, ss), ss = __builtin_fmaf(u.w, u.w, ss);
+      ss = __builtin_fmaf(v.x, v.x, ss), ss = __builtin_fmaf(v.y, v.y, ss);
+      ss = __builtin_fmaf(v.z, v.z, ss), ss = __builtin_fmaf(v.w, v.w, ss);
+      if (nw) {
+        const float4 wu = gld<float4>(nw + base + 32 * r), wv = gld<float4>(nw + base + 32 * r + 4);
+        u = make_float4(wu.x * u.x, wu.y * u.y, wu.z * u.z, wu.w * u.w);
+        v = make_float4(wv.x * v.x, wv.y * v.y, wv.z * v.z, wv.w * v.w);
+      }
+      x.v[r][0] = u.x, x.v[r][1] = u.y, x.v[r][2] = u.z, x.v[r][3] = u.w;
+      x.v[r][4] = v.x, x.v[r][5] = v.y, x.v[r][6] = v.z, x.v[r][7] = v.w;
+      x.s[r] = ((u.x + u.y) + (u.z + u.w)) + ((v.x + v.y) + (v.z + v.w));
+    }
   }
   __device__ static float dot(const Frag &f, const X &x, int p) {
     const int s = (p & 3) >> 1;
@@ -210,11 +268,34 @@ struct Tr<GQ_Q8_0> {
   __device__ static void load(Frag &f, const uint8_t *row, int b, int p) {
     (void)p;
     const uint8_t *blk = row + (size_t)b * BB;
-    f.d = *(const uint16_t *)blk;
+    f.d = gld<uint16_t>(blk);
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       const uint2 v = gq_load8_a2(blk + 2 + 8 * k);
       f.q[2 * k] = v.x, f.q[2 * k + 1] = v.y;
+    }
+  }
+  __device__ static void load_lds(Frag &f, const GQ_LDS uint8_t *base, uint32_t blk, int p) {
+    (void)p;
+    f.d = lld<uint16_t>(base, blk);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const uint2 v = lld8_a2(base, blk + 2 + 8 * k);
+      f.q[2 * k] = v.x, f.q[2 * k + 1] = v.y;
+    }
+  }
+  __device__ static void load_xg(X &x, const float *xg, const float *nw, int b, int p, float &ss) {
+    (void)p;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      float4 u = gld<float4>(xg + 32 * b + 4 * k);
+      ss = __builtin_fmaf(u.x, u.x, ss), ss = __builtin_fmaf(u.y, u.y, ss);
+      ss = __builtin_fmaf(u.z, u.z, ss), ss = __builtin_fmaf(u.w, u.w, ss);
+      if (nw) {
+        const float4 w = gld<float4>(nw + 32 * b + 4 * k);
+        u = make_float4(w.x * u.x, w.y * u.y, w.z * u.z, w.w * u.w);
+      }
+      x.v[4 * k] = u.x, x.v[4 * k + 1] = u.y, x.v[4 * k + 2] = u.z, x.v[4 * k + 3] = u.w;
     }
   }
   __device__ static float dot(const Frag &f, const X &x, int p) {
@@ -239,7 +320,7 @@ __device__ __forceinline__ void stage_x(const MvArgs &a, float *xs) {
   if (a.norm_w) {
     float ss = 0.f;
     for (int i = tid; i < n4; i += kThreads) {
-      const float4 v = x4[i];
+      const float4 v = gld<float4>(x4 + i);
       ss = __builtin_fmaf(v.x, v.x, ss);
       ss = __builtin_fmaf(v.y, v.y, ss);
       ss = __builtin_fmaf(v.z, v.z, ss);
@@ -254,11 +335,11 @@ __device__ __forceinline__ void stage_x(const MvArgs &a, float *xs) {
     const float r = 1.0f / sqrtf(tot);
     const float4 *w4 = (const float4 *)a.norm_w;
     for (int i = tid; i < n4; i += kThreads) {
-      const float4 v = x4[i], w = w4[i];
+      const float4 v = gld<float4>(x4 + i), w = gld<float4>(w4 + i);
       s4[i] = make_float4(w.x * (v.x * r), w.y * (v.y * r), w.z * (v.z * r), w.w * (v.w * r));
     }
   } else {
-    for (int i = tid; i < n4; i += kThreads) s4[i] = x4[i];
+    for (int i = tid; i < n4; i += kThreads) s4[i] = gld<float4>(x4 + i);
   }
   __syncthreads();
 }
@@ -269,108 +350,517 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return (g * sig) * u;
 }
 
-template <int DT, int R, int MODE>
-__global__ __launch_bounds__(kThreads) void mv_kernel(MvArgs a) {
-  using T = Tr<DT>;
-  extern __shared__ float xs[];
-  stage_x(a, xs);
+/* Segment and local row of global output row gr. */
+__device__ __forceinline__ void locate(const MvArgs &a, int gr, int &s, int &lr) {
+  s = 0;
+  lr = gr;
+  while (s < a.nseg - 1 && lr >= a.seg[s].rows) lr -= a.seg[s++].rows;
+}
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int nb = a.cols / T::QK;
-  const size_t rowbytes = (size_t)nb * T::BB;
-  constexpr int BPT = GQ_WAVE / T::LPB;
-  const int ntile = (nb + BPT - 1) / BPT;
-  const int part = lane % T::LPB, bt = lane / T::LPB;
+__device__ __forceinline__ int total_rows(const MvArgs &a, int mode) {
+  if (mode == MV_SWIGLU) return a.seg[0].rows;
+  int t = 0;
+  for (int i = 0; i < a.nseg; i++) t += a.seg[i].rows;
+  return t;
+}
 
-  /* rows handled by this wave */
-  const uint8_t *rp[R];
-  float *yp[R];
-  const float *rr[R];
-  bool ok[R];
+/* Weight row pointers of the R rows a wave computes in row group g (rows past
+ * the end are clamped to the last row: loaded, never stored). */
+template <int R, int MODE>
+__device__ __forceinline__ void group_rows(const MvArgs &a, int total, int g, int wave, size_t rowbytes,
+                                           const uint8_t *rp[R]) {
   if (MODE == MV_SWIGLU) {
     constexpr int P = R / 2;
-    const int p0 = (blockIdx.x * kWaves + wave) * P;
+    const int p0 = (g * kWaves + wave) * P;
 #pragma unroll
     for (int i = 0; i < P; i++) {
-      const int pr = p0 + i;
-      ok[i] = ok[P + i] = pr < a.seg[0].rows;
-      const int rr0 = ok[i] ? pr : 0;
-      rp[i] = a.seg[0].w + rr0 * rowbytes;
-      rp[P + i] = a.seg[1].w + rr0 * rowbytes;
-      yp[i] = a.seg[0].y + rr0;
-      yp[P + i] = nullptr;
-      rr[i] = rr[P + i] = nullptr;
+      const int pr = min(p0 + i, total - 1);
+      rp[i] = a.seg[0].w + pr * rowbytes;
+      rp[P + i] = a.seg[1].w + pr * rowbytes;
     }
   } else {
-    const int r0 = (blockIdx.x * kWaves + wave) * R;
+    const int r0 = (g * kWaves + wave) * R;
 #pragma unroll
     for (int i = 0; i < R; i++) {
-      int g = r0 + i, s = 0;
-      while (s < a.nseg - 1 && g >= a.seg[s].rows) g -= a.seg[s++].rows;
-      ok[i] = g < a.seg[s].rows;
-      if (!ok[i]) s = 0, g = 0;
-      rp[i] = a.seg[s].w + g * rowbytes;
-      yp[i] = a.seg[s].y + g;
-      rr[i] = MODE == MV_RESID ? a.seg[s].r + g : nullptr;
-    }
-  }
-
-  float acc[R];
-#pragma unroll
-  for (int i = 0; i < R; i++) acc[i] = 0.f;
-  for (int t = 0; t < ntile; t++) {
-    const int b = t * BPT + bt;
-    const bool bok = b < nb;
-    const int bc = bok ? b : nb - 1;
-    typename T::Frag f[R];
-#pragma unroll
-    for (int i = 0; i < R; i++) T::load(f[i], rp[i], bc, part);
-    typename T::X x;
-    T::load_x(x, xs, bc, part);
-#pragma unroll
-    for (int i = 0; i < R; i++) {
-      const float v = T::dot(f[i], x, part);
-      acc[i] += bok ? v : 0.f;
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < R; i++) acc[i] = gq_wave_sum(acc[i]);
-
-  if (MODE == MV_SWIGLU) {
-    constexpr int P = R / 2;
-#pragma unroll
-    for (int i = 0; i < P; i++)
-      if (lane == i && ok[i]) *yp[i] = silu_mul(acc[i], acc[P + i]);
-  } else {
-#pragma unroll
-    for (int i = 0; i < R; i++) {
-      if (lane == i && ok[i]) {
-        if (MODE == MV_RESID)
-          *yp[i] = acc[i] + *rr[i];
-        else
-          *yp[i] = acc[i];
-      }
+      int s, lr;
+      locate(a, min(r0 + i, total - 1), s, lr);
+      rp[i] = a.seg[s].w + lr * rowbytes;
     }
   }
 }
 
-template <int DT, int MODE>
-int launch_dm(const MvArgs &a, hipStream_t s) {
-  constexpr int R = 4;
-  int rows;
+/* Store the R reduced row values of group g (every lane holds all of them;
+ * lane i stores row i). */
+template <int R, int MODE>
+__device__ __forceinline__ void epilogue(const MvArgs &a, int total, int g, int wave, int lane,
+                                         const float (&acc)[R]) {
+#pragma clang fp contract(off)
   if (MODE == MV_SWIGLU) {
-    if (a.nseg != 2 || a.seg[0].rows != a.seg[1].rows) return -1;
-    rows = a.seg[0].rows;
-  } else {
-    rows = 0;
-    for (int i = 0; i < a.nseg; i++) rows += a.seg[i].rows;
+    constexpr int P = R / 2;
+    const int p0 = (g * kWaves + wave) * P;
+#pragma unroll
+    for (int i = 0; i < P; i++)
+      if (lane == i && p0 + i < total) gst<float>(a.seg[0].y + p0 + i, silu_mul(acc[i], acc[P + i]));
+    return;
   }
-  const int per_wg = kWaves * (MODE == MV_SWIGLU ? R / 2 : R);
-  const int grid = (rows + per_wg - 1) / per_wg;
-  if (grid <= 0) return -1;
+  const int r0 = (g * kWaves + wave) * R;
+#pragma unroll
+  for (int i = 0; i < R; i++) {
+    if (lane != i || r0 + i >= total) continue;
+    int s, lr;
+    locate(a, r0 + i, s, lr);
+    const MvSeg &sg = a.seg[s];
+    if (MODE == MV_RESID) {
+      gst<float>(sg.y + lr, acc[i] + gld<float>(sg.r + lr));
+      continue;
+    }
+    float v = acc[i];
+    if (sg.kind == SEG_PLAIN) {
+      gst<float>(sg.y + lr, v);
+      continue;
+    }
+    const int hd = a.rope.head_dim;
+    const int pos = a.rope.pos_dev ? gld<int>(a.rope.pos_dev) : a.rope.pos;
+    if (pos < 0 || pos >= a.rope.max_seq) continue; /* rejected on the host */
+    const int h = lr / hd, d = lr - h * hd;
+    if (sg.kind != SEG_KV) {
+      /* adjacent pair (d & ~1, d | 1) rotated by the row of pos
+       * (kernels_cpu.c:415-429: products and difference rounded apart) */
+      const float2 cs = gld<float2>(a.rope.cs + (size_t)pos * (hd >> 1) + (d >> 1));
+      const float x0 = acc[i & ~1], x1 = acc[i | 1];
+      v = (d & 1) ? x0 * cs.y + x1 * cs.x : x0 * cs.x - x1 * cs.y;
+    }
+    if (sg.kind == SEG_ROPE)
+      gst<float>(sg.y + lr, v);
+    else
+      gst<float>(sg.y + ((size_t)h * a.rope.max_seq + pos) * hd + d, v);
+  }
+}
+
+/* Persistent grid: workgroup b handles row groups b, b + gridDim.x, ... with x
+ * staged in LDS once.  A wave walks (group, tile) steps and loads the weight
+ * fragments of step s+1 before computing step s; the first step's loads are
+ * issued before x is staged so both latencies overlap. */
+template <int DT, int R, int MODE>
+__global__ __launch_bounds__(kThreads) void mv_kernel(MvArgs a) {
+  using T = Tr<DT>;
+  extern __shared__ float xs[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nb = a.cols / T::QK;
+  const size_t rowbytes = (size_t)nb * T::BB;
+  constexpr int BPT = GQ_WAVE / T::LPB;
+  constexpr int P = MODE == MV_SWIGLU ? R / 2 : R;
+  const int ntile = (nb + BPT - 1) / BPT;
+  const int part = lane % T::LPB, bt = lane / T::LPB;
+  const int total = total_rows(a, MODE);
+  const int ngroups = (total + kWaves * P - 1) / (kWaves * P);
+  const int mygroups = (int)blockIdx.x < ngroups ? (ngroups - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+  const int nsteps = mygroups * ntile;
+
+  typename T::Frag cur[R], nxt[R];
+  const uint8_t *rp[R];
+  int g = blockIdx.x, t = 0;
+  if (nsteps > 0) {
+    group_rows<R, MODE>(a, total, g, wave, rowbytes, rp);
+    const int bc = min(bt, nb - 1);
+#pragma unroll
+    for (int i = 0; i < R; i++) T::load(cur[i], rp[i], bc, part);
+  }
+  stage_x(a, xs);
+
+  float acc[R];
+#pragma unroll
+  for (int i = 0; i < R; i++) acc[i] = 0.f;
+  for (int s = 0; s < nsteps; s++) {
+    int t1 = t + 1, g1 = g;
+    const uint8_t *rn[R];
+#pragma unroll
+    for (int i = 0; i < R; i++) rn[i] = rp[i];
+    if (s + 1 < nsteps) {
+      if (t1 == ntile) {
+        t1 = 0;
+        g1 = g + gridDim.x;
+        group_rows<R, MODE>(a, total, g1, wave, rowbytes, rn);
+      }
+      const int bc = min(t1 * BPT + bt, nb - 1);
+#pragma unroll
+      for (int i = 0; i < R; i++) T::load(nxt[i], rn[i], bc, part);
+    }
+    {
+      const int b = t * BPT + bt;
+      const bool bok = b < nb;
+      typename T::X x;
+      T::load_x(x, xs, bok ? b : nb - 1, part);
+#pragma unroll
+      for (int i = 0; i < R; i++) {
+        const float v = T::dot(cur[i], x, part);
+        acc[i] += bok ? v : 0.f;
+      }
+    }
+    if (t == ntile - 1) {
+#pragma unroll
+      for (int i = 0; i < R; i++) acc[i] = gq_wave_sum(acc[i]);
+      epilogue<R, MODE>(a, total, g, wave, lane, acc);
+#pragma unroll
+      for (int i = 0; i < R; i++) acc[i] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+      cur[i] = nxt[i];
+      rp[i] = rn[i];
+    }
+    t = t1;
+    g = g1;
+  }
+}
+
+/* ------------------------------------------------------------------------
+ * LDS-streamed matvec.
+ *
+ * The weight rows of a workgroup's row groups ("stages" of rs rows) are
+ * streamed into a ring of kStages LDS buffers with direct global->LDS DMA
+ * loads (global_load_lds_dwordx4: 1 KB per wave instruction, no VGPRs), two
+ * stages ahead of the one being computed, so each CU keeps tens of KB of HBM
+ * reads in flight independent of register pressure and of the 2-byte block
+ * alignment of Q6_K.  Waves keep their x slices in registers for the whole
+ * kernel (RMSNorm folded as y = r * W (w .* x)); a team of ts waves splits K
+ * (wave j owns tiles j, j+ts, ...) and the per-row partials meet in LDS. */
+constexpr int kStages = 3;
+constexpr int kStageCap = 24576; /* bytes of weights per stage buffer */
+
+struct MvPlan {
+  int rs;           /* weight rows per stage (MV_SWIGLU: rs/2 gate + rs/2 up) */
+  int ts, nteam;    /* waves per team, teams per workgroup */
+  int ntile;        /* column tiles per row */
+  int ngroups;      /* stages over the whole launch */
+  int rowbytes;
+  int stride;       /* LDS bytes per stage buffer */
+  int total;        /* output rows */
+};
+
+/* Wave `wave`'s 1 KB copy instructions for nbytes (a multiple of 16). */
+__device__ __forceinline__ int copy_count(int nbytes, int wave) {
+  const int ng = (nbytes / 16 + 63) / 64;
+  return wave < ng ? (ng - wave + kWaves - 1) / kWaves : 0;
+}
+
+/* The DMA loads are issued from inline assembly on purpose: the compiler's
+ * wait-count pass treats a visible LDS-DMA load as a write to every LDS
+ * location and would put s_waitcnt vmcnt(0) in front of each LDS read of the
+ * compute loop, draining the stages in flight.  Completion is tracked by hand
+ * (wait_vmcnt + barrier).  VMEM loads retire in order, so the compiler's own
+ * waits for other loads can only wait longer than needed, never less. */
+__device__ __forceinline__ void dma16(const uint8_t *src, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(lds_addr)
+               : "m0");
+}
+
+__device__ __forceinline__ void copy_range(const uint8_t *src, int nbytes, GQ_LDS uint8_t *dst, int wave,
+                                           int lane) {
+  const int nchunk = nbytes / 16, ng = (nchunk + 63) / 64;
+  const uint32_t base = (uint32_t)(uintptr_t)dst;
+  for (int g = wave; g < ng; g += kWaves) {
+    const int c = g * 64 + lane;
+    const uint32_t d = __builtin_amdgcn_readfirstlane(base + (uint32_t)g * 1024u);
+    if (c < nchunk) dma16(src + (size_t)c * 16, d);
+  }
+}
+
+/* One dword per lane into LDS (the residual rows of a stage). */
+__device__ __forceinline__ void dma4(const float *src, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off"
+               :
+               : "v"(src), "s"(lds_addr)
+               : "m0");
+}
+
+/* Stage `g`'s rows: global rows [g*rs, g*rs+rs) (clamped to the end of their
+ * segment), or for MV_SWIGLU gate and up rows [g*rs/2, g*rs/2 + rs/2); for
+ * MV_RESID also the stage's residual values into `rbuf`.  Returns this wave's
+ * DMA instruction count. */
+template <int MODE>
+__device__ __forceinline__ int issue_stage(const MvArgs &a, const MvPlan &pl, int g, GQ_LDS uint8_t *buf,
+                                           GQ_LDS float *rbuf, int wave, int lane) {
+  if (MODE == MV_SWIGLU) {
+    const int h = pl.rs / 2, r0 = g * h, n = min(h, pl.total - r0);
+    const int nb = n * pl.rowbytes;
+    copy_range(a.seg[0].w + (size_t)r0 * pl.rowbytes, nb, buf, wave, lane);
+    copy_range(a.seg[1].w + (size_t)r0 * pl.rowbytes, nb, buf + h * pl.rowbytes, wave, lane);
+    return 2 * copy_count(nb, wave);
+  }
+  const int r0 = g * pl.rs;
+  int s, lr;
+  locate(a, r0, s, lr);
+  const int n = min(pl.rs, a.seg[s].rows - lr);
+  const int nb = n * pl.rowbytes;
+  copy_range(a.seg[s].w + (size_t)lr * pl.rowbytes, nb, buf, wave, lane);
+  int c = copy_count(nb, wave);
+  if (MODE == MV_RESID && wave == kWaves - 1) {
+    const uint32_t d = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)rbuf);
+    if (lane < n) dma4(a.seg[s].r + lr + lane, d);
+    c++;
+  }
+  return c;
+}
+
+/* s_waitcnt vmcnt(n) with the other counters left alone (n <= 63). */
+__device__ __forceinline__ void wait_vmcnt(int n) {
+#define GQ_W(N)                                                                                   \
+  case N: __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | (7 << 4) | (15 << 8)); break;
+  switch (n) {
+    GQ_W(0) GQ_W(1) GQ_W(2) GQ_W(3) GQ_W(4) GQ_W(5) GQ_W(6) GQ_W(7) GQ_W(8) GQ_W(9) GQ_W(10)
+    GQ_W(11) GQ_W(12) GQ_W(13) GQ_W(14) GQ_W(15) GQ_W(16) GQ_W(17) GQ_W(18) GQ_W(19) GQ_W(20)
+    GQ_W(21) GQ_W(22) GQ_W(23) GQ_W(24)
+  default: __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); break; /* vmcnt(0) */
+  }
+#undef GQ_W
+}
+
+/* Store one finished output row `lr` of segment `s` (`s` is the same for the
+ * whole stage: a stage never straddles segments).  No vector global loads
+ * here: inside the pipelined loop every operand comes from LDS, registers or
+ * scalar loads of the kernel arguments (see dma16). */
+template <int MODE>
+__device__ __forceinline__ void store_row(const MvArgs &a, int s, int lr, float v, float partner,
+                                          float resid, int pos, const float2 *scs) {
+#pragma clang fp contract(off)
+  if (MODE == MV_SWIGLU) {
+    gst<float>(a.seg[0].y + lr, silu_mul(v, partner));
+    return;
+  }
+  const MvSeg &sg = a.seg[s];
+  if (MODE == MV_RESID) {
+    gst<float>(sg.y + lr, v + resid);
+    return;
+  }
+  if (sg.kind == SEG_PLAIN) {
+    gst<float>(sg.y + lr, v);
+    return;
+  }
+  const int hd = a.rope.head_dim;
+  if (pos < 0 || pos >= a.rope.max_seq) return; /* rejected on the host */
+  const int h = lr / hd, d = lr - h * hd;
+  if (sg.kind != SEG_KV) {
+    /* adjacent pair rotated by the row of pos (kernels_cpu.c:415-429) */
+    const float2 cs = scs[d >> 1];
+    const float x0 = (d & 1) ? partner : v, x1 = (d & 1) ? v : partner;
+    v = (d & 1) ? x0 * cs.y + x1 * cs.x : x0 * cs.x - x1 * cs.y;
+  }
+  if (sg.kind == SEG_ROPE)
+    gst<float>(sg.y + lr, v);
+  else
+    gst<float>(sg.y + ((size_t)h * a.rope.max_seq + pos) * hd + d, v);
+}
+
+template <int DT, int MODE, int TPW>
+__global__ __launch_bounds__(kThreads) void mvl_kernel(MvArgs a, MvPlan pl) {
+  using T = Tr<DT>;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  GQ_LDS uint8_t *lds = (GQ_LDS uint8_t *)smem;
+  __shared__ float red[2][32][kWaves];
+  __shared__ float red_ss[kWaves];
+  __shared__ __attribute__((aligned(16))) float rres[4][32];
+  __shared__ float2 scs[256];
+  GQ_LDS float *lres = (GQ_LDS float *)&rres[0][0];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); /* scalar: the DMA counts are too */
+  constexpr int BPT = GQ_WAVE / T::LPB;
+  const int nb = a.cols / T::QK;
+  const int part = lane % T::LPB, bt = lane / T::LPB;
+  const int team = wave / pl.ts, wj = wave - team * pl.ts;
+  const bool active = team < pl.nteam;
+  const int mygroups = (int)blockIdx.x < pl.ngroups ? (pl.ngroups - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+
+  /* everything the loop needs from global memory besides the weights is
+   * loaded and consumed first: x slices (and the RMSNorm sum of squares from
+   * team 0), the position and the RoPE table row */
+  typename T::X xs[TPW];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < TPW; i++) {
+    const int b = (wj + i * pl.ts) * BPT + bt;
+    float s2 = 0.f;
+    T::load_xg(xs[i], a.x, a.norm_w, min(b, nb - 1), part, s2);
+    if (b < nb && (wj + i * pl.ts) < pl.ntile) ss += s2;
+  }
+  int pos = 0;
+  if (MODE == MV_STORE && a.rope.cs) {
+    pos = a.rope.pos_dev ? gld<int>(a.rope.pos_dev) : a.rope.pos;
+    const int half = a.rope.head_dim >> 1;
+    if (pos >= 0 && pos < a.rope.max_seq)
+      for (int i = threadIdx.x; i < half && i < 256; i += kThreads)
+        scs[i] = gld<float2>(a.rope.cs + (size_t)pos * half + i);
+  }
+  float rscale = 1.f;
+  if (a.norm_w) {
+    ss = gq_wave_sum(ss);
+    if (lane == 0) red_ss[wave] = active && team == 0 ? ss : 0.f;
+    __syncthreads();
+    float tot = (red_ss[0] + red_ss[1]) + (red_ss[2] + red_ss[3]);
+    tot = tot / (float)a.cols;
+    tot = tot + a.eps;
+    rscale = 1.0f / sqrtf(tot);
+  }
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); /* those loads are done */
+
+  /* nxt: this wave's DMA instructions for stage k+1 (issued, maybe pending) */
+  static_assert(kStages == 3, "the DMA bookkeeping below assumes three stages");
+  int nxt = 0;
+  if (mygroups > 0) (void)issue_stage<MODE>(a, pl, blockIdx.x, lds, lres, wave, lane);
+  if (mygroups > 1) nxt = issue_stage<MODE>(a, pl, blockIdx.x + gridDim.x, lds + pl.stride, lres + 32, wave, lane);
+
+  const int hrows = MODE == MV_SWIGLU ? pl.rs / 2 : pl.rs;
+  int slot = 0; /* k % kStages */
+  for (int k = 0; k <= mygroups; k++) {
+    if (k < mygroups) {
+      const int kn = k + kStages - 1, sn = slot == 0 ? 2 : slot - 1; /* kn % kStages */
+      const int nn = kn < mygroups ? issue_stage<MODE>(a, pl, blockIdx.x + kn * gridDim.x,
+                                                       lds + sn * pl.stride, lres + (kn & 3) * 32, wave, lane)
+                                   : 0;
+      /* VMEM loads complete in issue order: with at most the stage k+1 and
+       * k+2 copies outstanding, this wave's copies of stage k have landed;
+       * the barrier extends that to every wave's */
+      wait_vmcnt(nxt + nn);
+      nxt = nn;
+    }
+    __syncthreads();
+    if (k > 0) { /* finish the rows of stage k-1 */
+      const int r0 = (blockIdx.x + (k - 1) * gridDim.x) * hrows;
+      int s = 0, lr0 = r0;
+      if (MODE != MV_SWIGLU) locate(a, r0, s, lr0);
+      s = __builtin_amdgcn_readfirstlane(s);
+      lr0 = __builtin_amdgcn_readfirstlane(lr0);
+      const int t = threadIdx.x;
+      if (t < hrows && r0 + t < pl.total) {
+        const int tp = MODE == MV_SWIGLU ? t + hrows : (t ^ 1);
+        float v = 0.f, w = 0.f;
+        for (int j = 0; j < pl.ts; j++) v += red[(k - 1) & 1][t][j], w += red[(k - 1) & 1][tp][j];
+        store_row<MODE>(a, s, lr0 + t, v * rscale, w * rscale,
+                        MODE == MV_RESID ? rres[(k - 1) & 3][t] : 0.f, pos, scs);
+      }
+    }
+    if (k == mygroups) break;
+    if (active) {
+      const GQ_LDS uint8_t *buf = lds + slot * pl.stride;
+      for (int i = team; i < pl.rs; i += pl.nteam) {
+        float acc = 0.f;
+#pragma unroll
+        for (int ti = 0; ti < TPW; ti++) {
+          const int t = wj + ti * pl.ts;
+          const int b = t * BPT + bt;
+          if (t < pl.ntile) {
+            typename T::Frag f;
+            T::load_lds(f, buf, i * pl.rowbytes + min(b, nb - 1) * T::BB, part);
+            const float v = T::dot(f, xs[ti], part);
+            acc += b < nb ? v : 0.f;
+          }
+        }
+        acc = gq_wave_sum(acc);
+        if (lane == 0) red[k & 1][i][wj] = acc;
+      }
+    }
+    __syncthreads();
+    slot = slot == kStages - 1 ? 0 : slot + 1;
+  }
+}
+
+int g_n_cu = 256;
+int g_wg_per_cu = 4;
+int g_use_lds = 1;
+
+template <int DT, int MODE, int R>
+int launch_r(const MvArgs &a, int total, hipStream_t s) {
+  constexpr int P = MODE == MV_SWIGLU ? R / 2 : R;
+  const int ngroups = (total + kWaves * P - 1) / (kWaves * P);
+  /* enough workgroups to fill every CU a few times over, never more than
+   * there are row groups */
+  const int grid = g_wg_per_cu > 0 ? min(ngroups, g_wg_per_cu * g_n_cu) : ngroups;
   const size_t lds = (size_t)a.cols * sizeof(float);
   hipLaunchKernelGGL((mv_kernel<DT, R, MODE>), dim3(grid), dim3(kThreads), lds, s, a);
   return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+/* Plan and launch the LDS-streamed kernel; returns 1 when the shape does not
+ * fit it (rows not a multiple of 16 bytes, more than 8 column tiles, or
+ * segments that a stage would straddle) so the caller uses mv_kernel. */
+template <int DT, int MODE>
+int launch_lds(const MvArgs &a, int total, hipStream_t s) {
+  using T = Tr<DT>;
+  const int nb = a.cols / T::QK;
+  const int rowbytes = nb * T::BB;
+  if (rowbytes % 16) return 1;
+  if (a.rope.cs && a.rope.head_dim > 512) return 1; /* the kernel's RoPE row holds 256 pairs */
+  constexpr int BPT = GQ_WAVE / T::LPB;
+  const int ntile = (nb + BPT - 1) / BPT;
+  const int tpw = ntile <= kWaves ? 1 : 2;
+  const int ts = (ntile + tpw - 1) / tpw;
+  if (ts > kWaves) return 1;
+  const int nteam = kWaves / ts;
+  int rs = min(32, kStageCap / rowbytes);
+  rs -= rs % (2 * nteam);
+  /* with several segments a stage must not straddle two: rs divides them all */
+  if (MODE != MV_SWIGLU && a.nseg > 1)
+    for (int i = 0; i < a.nseg && rs >= 2 * nteam;) {
+      if (a.seg[i].rows % rs)
+        rs -= 2 * nteam, i = 0;
+      else
+        i++;
+    }
+  if (rs < 2 * nteam || rs < 2) return 1;
+  MvPlan pl;
+  pl.rs = rs, pl.ts = ts, pl.nteam = nteam, pl.ntile = ntile, pl.rowbytes = rowbytes, pl.total = total;
+  pl.stride = (rs * rowbytes + 64 + 1023) / 1024 * 1024;
+  const int per = MODE == MV_SWIGLU ? rs / 2 : rs;
+  pl.ngroups = (total + per - 1) / per;
+  const size_t lds = (size_t)kStages * pl.stride;
+  const int per_cu = max(1, (int)(160 * 1024 / (lds + 2048)));
+  const int grid = min(pl.ngroups, per_cu * g_n_cu);
+  static bool attr_set = false;
+  if (!attr_set) {
+    (void)hipFuncSetAttribute((const void *)mvl_kernel<DT, MODE, 1>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
+    (void)hipFuncSetAttribute((const void *)mvl_kernel<DT, MODE, 2>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
+    attr_set = true;
+  }
+  if (tpw == 1)
+    hipLaunchKernelGGL((mvl_kernel<DT, MODE, 1>), dim3(grid), dim3(kThreads), lds, s, a, pl);
+  else
+    hipLaunchKernelGGL((mvl_kernel<DT, MODE, 2>), dim3(grid), dim3(kThreads), lds, s, a, pl);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+template <int DT, int MODE>
+int launch_dm(const MvArgs &a, hipStream_t s) {
+  int total = 0;
+  if (MODE == MV_SWIGLU) {
+    if (a.nseg != 2 || a.seg[0].rows != a.seg[1].rows) return -1;
+    total = a.seg[0].rows;
+  } else {
+    bool fused = false;
+    for (int i = 0; i < a.nseg; i++) {
+      if (a.seg[i].kind != SEG_PLAIN) {
+        fused = true;
+        if (MODE != MV_STORE || !a.rope.cs || a.rope.head_dim <= 0 || (a.rope.head_dim & 1) ||
+            a.seg[i].rows % a.rope.head_dim)
+          return -1;
+      }
+      total += a.seg[i].rows;
+    }
+    /* fused RoPE pairs rows inside a wave: every segment must start on a wave
+     * boundary */
+    if (fused)
+      for (int i = 0; i < a.nseg; i++)
+        if (a.seg[i].rows % 4) return -1;
+  }
+  if (total <= 0) return -1;
+  if (g_use_lds) {
+    const int rc = launch_lds<DT, MODE>(a, total, s);
+    if (rc <= 0) return rc;
+  }
+  return launch_r<DT, MODE, 4>(a, total, s);
 }
 
 template <int DT>
@@ -384,6 +874,24 @@ int launch_dt(int mode, const MvArgs &a, hipStream_t s) {
 }
 
 } // namespace
+
+void gq_matvec_set_cus(int n_cu) {
+  if (n_cu > 0) g_n_cu = n_cu;
+  static bool env_read = false;
+  if (env_read) return;
+  env_read = true;
+  /* GQ_MV_WG_PER_CU: workgroups per CU of the register-path kernel's
+   * persistent grid (0 = one workgroup per row group); default 4 */
+  if (const char *e = getenv("GQ_MV_WG_PER_CU")) g_wg_per_cu = atoi(e);
+  /* GQ_MV_LDS=0: register-path kernel only (same as gq_hip_set_matvec_path(0)) */
+  if (const char *e = getenv("GQ_MV_LDS")) g_use_lds = atoi(e) != 0;
+}
+
+extern "C" int gq_hip_set_matvec_path(int lds) {
+  const int prev = g_use_lds;
+  g_use_lds = lds != 0;
+  return prev;
+}
 
 int gq_launch_matvec(int dtype, int mode, const MvArgs &a, hipStream_t s) {
   if (a.nseg < 1 || a.nseg > 3 || a.cols <= 0 || a.cols > 16384 || (a.cols & 3)) return -1;

@@ -116,6 +116,7 @@ extern "C" gq_ctx *gq_hip_create(int device_id) {
   if (hipGetDeviceProperties(&p, device_id) == hipSuccess) {
     c->n_cu = p.multiProcessorCount;
     snprintf(c->name, sizeof c->name, "%s", p.gcnArchName);
+    gq_matvec_set_cus(c->n_cu);
   }
   return c;
 }
@@ -630,28 +631,30 @@ static int run_layer(gq_ctx *c, int l, int pos, const int *pos_dev, float *hidde
   const int H = m.hidden, kvd = m.n_kv_heads * m.head_dim;
   float *q = w.qkv, *k = w.qkv + H, *v = w.qkv + H + kvd;
   int rc;
-  /* q, k, v: one launch per distinct dtype, RMSNorm fused into each */
+  /* q, k, v: one launch per distinct dtype, RMSNorm fused into the x
+   * staging; RoPE of q and k and the K/V cache append fused into the
+   * epilogue (engine.c:356-392 in one pass) */
+  (void)k;
+  (void)v;
   const gq_weight *W[3] = {&L.wq, &L.wk, &L.wv};
-  float *Y[3] = {q, k, v};
+  float *Y[3] = {q, gq_hip_kv_k(c, l), gq_hip_kv_v(c, l)};
+  const int kind[3] = {SEG_ROPE, SEG_ROPE_KV, SEG_KV};
   bool done[3] = {false, false, false};
   for (int i = 0; i < 3; i++) {
     if (done[i]) continue;
     MvArgs a{};
     a.cols = H, a.x = hidden, a.norm_w = L.rms_att, a.eps = m.rms_eps;
+    a.rope = MvRope{c->rope, pos_dev, pos, m.head_dim, c->kv_max_seq};
     double bytes = 4.0 * H;
     for (int j = i; j < 3; j++)
       if (!done[j] && W[j]->dtype == W[i]->dtype) {
-        a.seg[a.nseg++] = MvSeg{(const uint8_t *)W[j]->data, Y[j], nullptr, W[j]->rows};
+        a.seg[a.nseg++] = MvSeg{(const uint8_t *)W[j]->data, Y[j], nullptr, W[j]->rows, kind[j]};
         bytes += mv_bytes(*W[j], 0) - 4.0 * H;
         done[j] = true;
       }
     if ((rc = gq_launch_matvec(W[i]->dtype, MV_STORE, a, c->stream))) return rc;
     mark(c, mv_class(W[i]->dtype), bytes);
   }
-  RopeArgs ra{q, k, v, gq_hip_kv_k(c, l), gq_hip_kv_v(c, l), c->rope, pos_dev, pos,
-              m.n_heads, m.n_kv_heads, m.head_dim, c->kv_max_seq};
-  if ((rc = gq_launch_rope_append(ra, c->stream))) return rc;
-  mark(c, 4, 4.0 * (H + 2 * kvd) + 4.0 * (H + 2 * kvd));
   AttnArgs aa{};
   aa.q = q, aa.k = gq_hip_kv_k(c, l), aa.v = gq_hip_kv_v(c, l);
   aa.part_o = w.part_o, aa.part_ml = w.part_ml, aa.out = w.attn;
@@ -916,6 +919,37 @@ extern "C" float gq_hip_time_attention(gq_ctx *c, int layer, int pos, const floa
 }
 
 /* ------------------------------------------------------------ op-level */
+extern "C" int gq_hip_qkv_rope_dev(gq_ctx *c, int layer, int pos, const float *hidden, float *q_out,
+                                   int fused) {
+  if (!c || !hidden || !q_out) return -1;
+  int rc = check_pos(c, pos, 1);
+  if (rc) return rc;
+  if (layer < 0 || layer >= c->m.n_layers) return fail(c, -1, "bad layer");
+  const gq_model &m = c->m;
+  const gq_layer &L = c->layers[layer];
+  Workspace &w = c->ws;
+  const int H = m.hidden, kvd = m.n_kv_heads * m.head_dim;
+  float *k = w.qkv + H, *v = w.qkv + H + kvd;
+  const gq_weight *W[3] = {&L.wq, &L.wk, &L.wv};
+  float *Y[3] = {q_out, fused ? gq_hip_kv_k(c, layer) : k, fused ? gq_hip_kv_v(c, layer) : v};
+  const int kind[3] = {SEG_ROPE, SEG_ROPE_KV, SEG_KV};
+  for (int i = 0; i < 3; i++) {
+    MvArgs a{};
+    a.cols = H, a.x = hidden, a.norm_w = L.rms_att, a.eps = m.rms_eps;
+    a.rope = MvRope{c->rope, nullptr, pos, m.head_dim, c->kv_max_seq};
+    a.seg[0] = MvSeg{(const uint8_t *)W[i]->data, Y[i], nullptr, W[i]->rows, fused ? kind[i] : SEG_PLAIN};
+    a.nseg = 1;
+    if ((rc = gq_launch_matvec(W[i]->dtype, MV_STORE, a, c->stream))) return fail(c, rc, "qkv launch");
+  }
+  if (!fused) {
+    RopeArgs ra{q_out, k, v, gq_hip_kv_k(c, layer), gq_hip_kv_v(c, layer), c->rope, nullptr, pos,
+                m.n_heads, m.n_kv_heads, m.head_dim, c->kv_max_seq};
+    if ((rc = gq_launch_rope_append(ra, c->stream))) return fail(c, rc, "rope_append launch");
+  }
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return 0;
+}
+
 extern "C" int gq_hip_rmsnorm_dev(gq_ctx *c, const float *x, const float *w, float *out, int dim, float eps) {
   if (!c || !x || !out || dim <= 0) return -1;
   return gq_launch_rmsnorm(x, w, out, dim, eps, c->stream) ? fail(c, -4, "rmsnorm launch") : 0;

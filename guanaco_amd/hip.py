@@ -71,10 +71,12 @@ def _load():
                                           C.POINTER(C.c_int), C.POINTER(C.c_double)]),
         "gq_hip_time_matvec": (C.c_float, [_vp, C.c_int, C.POINTER(_vp), C.c_int, C.c_int,
                                            C.c_int, _vp, _vp, C.c_int]),
+        "gq_hip_set_matvec_path": (C.c_int, [C.c_int]),
         "gq_hip_time_attention": (C.c_float, [_vp, C.c_int, C.c_int, _vp, _vp, C.c_int]),
         "gq_hip_rmsnorm_dev": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, C.c_float]),
         "gq_hip_rope_append_dev": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp]),
         "gq_hip_attention_dev": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]),
+        "gq_hip_qkv_rope_dev": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp, C.c_int]),
         "gq_hip_embed_dev": (C.c_int, [_vp, C.c_int, _vp, C.c_int, C.c_int, _vp]),
         "gq_hip_argmax_dev": (C.c_int, [_vp, _vp, C.c_int, _vp]),
         "gq_hip_silu_mul_dev": (C.c_int, [_vp, _vp, _vp, C.c_int]),
@@ -89,6 +91,22 @@ def _load():
 lib, EXPORTS = _load()
 NCLASS = 6
 CLASS_NAMES = ("q4_k_matvec", "q6_k_matvec", "q8_0_matvec", "attention", "rope_append", "other")
+MATVEC_PATHS = ("register", "lds")
+
+
+class matvec_path:
+    """Context manager selecting the matvec kernel ("lds": LDS-streamed where
+    the shape fits, the default; "register": register-path kernel only)."""
+
+    def __init__(self, name):
+        self.lds = MATVEC_PATHS.index(name)
+
+    def __enter__(self):
+        self.prev = lib.gq_hip_set_matvec_path(self.lds)
+        return self
+
+    def __exit__(self, *exc):
+        lib.gq_hip_set_matvec_path(self.prev)
 
 
 class GqWeight(C.Structure):

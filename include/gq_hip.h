@@ -197,6 +197,11 @@ int gq_hip_profile_step(gq_ctx *ctx, int token, int pos, double ms[GQ_NCLASS],
  * (to defeat the MALL) with per-buffer outputs. */
 float gq_hip_time_matvec(gq_ctx *ctx, int dtype, const void *const *w_devs, int n_w, int rows,
                          int cols, const float *x_dev, float *y_dev, int n_iter);
+/* Selects the matvec kernel for later launches in this process: 1 (default)
+ * the LDS-streamed kernel where the shape fits it, 0 the register-path kernel
+ * only.  Returns the previous setting.  No reference counterpart: a switch
+ * for the parity tests (both kernels against the oracle) and for timing. */
+int gq_hip_set_matvec_path(int lds);
 /* Device time of n launches of the attention kernels for one layer. */
 float gq_hip_time_attention(gq_ctx *ctx, int layer, int pos, const float *q_dev, float *out_dev,
                             int n_iter);
@@ -214,6 +219,12 @@ int gq_hip_rope_append_dev(gq_ctx *ctx, int layer, int pos, int n_heads, float *
  * (engine.c:433-509): q (n_heads x hd) -> out (n_heads x hd). */
 int gq_hip_attention_dev(gq_ctx *ctx, int layer, int pos, int n_heads, const float *q,
                          float *out);
+/* q/k/v projections of a bound layer from a device hidden vector with the
+ * layer's RMSNorm, RoPE and K/V append: fused != 0 runs the decode path's
+ * single fused epilogue, fused == 0 plain matvecs followed by the standalone
+ * RoPE+append kernel (the two must agree bit for bit). */
+int gq_hip_qkv_rope_dev(gq_ctx *ctx, int layer, int pos, const float *hidden, float *q_out,
+                        int fused);
 int gq_hip_embed_dev(gq_ctx *ctx, int dtype, const void *table, int hidden, int token,
                      float *out);
 int gq_hip_argmax_dev(gq_ctx *ctx, const float *x, int n, int *out_index_dev);

@@ -24,8 +24,15 @@ def tiny(ctx, orc):
     return spec, ms, pre, hm, dm
 
 
-def test_forward_per_layer_and_tokens(ctx, orc, tiny):
+@pytest.mark.parametrize("path", ["lds", "register"])
+def test_forward_per_layer_and_tokens(ctx, orc, tiny, path):
+    import guanaco_amd.hip as H
     spec, ms, pre, hm, dm = tiny
+    with H.matvec_path(path):
+        _forward_per_layer_and_tokens(ctx, orc, spec, pre, hm, dm)
+
+
+def _forward_per_layer_and_tokens(ctx, orc, spec, pre, hm, dm):
     ctx.kv_prefill_synth(*[__import__("guanaco_amd.synth").synth.tensor_seed(spec.seed, -1, s)
                            for s in (13, 14)], pre)
     kv = hm.new_kv()
@@ -99,6 +106,33 @@ def test_transformer_layer_host_mirror(ctx, orc, tiny):
         sl = slice((h * ms + pre) * spec.head_dim, (h * ms + pre + 1) * spec.head_dim)
         assert np.array_equal(hk[sl], dk[sl]) and np.array_equal(hv[sl], dv[sl])
         assert rel_l2(dk[sl], kv.k[sl]) < LAYER_TOL
+
+
+def test_fused_qkv_rope_append_bitexact(ctx, orc, tiny):
+    """The decode path's fused q/k/v epilogue (RoPE + K/V append inside the
+    matvec) equals plain matvecs followed by the standalone RoPE+append kernel
+    (itself bit-exact against the reference's rope + kv_cache_append)."""
+    import guanaco_amd.hip as H
+    from util import bits
+    spec, ms, pre, hm, dm = tiny
+    hd, nkv = spec.head_dim, spec.n_kv_heads
+    h = ctx.upload(orc.synth_normal(8, spec.hidden) * np.float32(3))
+    q1, q2 = ctx.alloc(4 * spec.hidden), ctx.alloc(4 * spec.hidden)
+    pos, layer = pre + 3, 1
+    assert H.lib.gq_hip_qkv_rope_dev(ctx.h, layer, pos, h.ptr, q1.ptr, 0) == 0
+    k1, v1 = ctx.kv_read_layer(layer)
+    z = np.zeros_like(k1)
+    ctx.kv_write_layer(layer, z, z)
+    assert H.lib.gq_hip_qkv_rope_dev(ctx.h, layer, pos, h.ptr, q2.ptr, 1) == 0
+    k2, v2 = ctx.kv_read_layer(layer)
+    assert np.array_equal(bits(q1.download()), bits(q2.download()))
+    r1 = lambda a: a.reshape(nkv, ms, hd)[:, pos]  # noqa: E731
+    assert np.abs(r1(k2)).sum() > 0 and np.abs(r1(v2)).sum() > 0
+    assert np.array_equal(bits(r1(k1)), bits(r1(k2))) and np.array_equal(bits(r1(v1)), bits(r1(v2)))
+    # nothing else in the slab was written
+    k2r = k2.reshape(nkv, ms, hd).copy()
+    k2r[:, pos] = 0
+    assert not k2r.any()
 
 
 def test_profile_step_accounts_every_launch(ctx, tiny):

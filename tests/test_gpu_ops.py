@@ -42,13 +42,16 @@ SHAPES = [
 ]
 
 
+@pytest.mark.parametrize("path", ["lds", "register"])
 @pytest.mark.parametrize("dt,rows,cols", SHAPES)
-def test_matvec_vs_oracle(ctx, orc, dt, rows, cols):
+def test_matvec_vs_oracle(ctx, orc, dt, rows, cols, path):
+    import guanaco_amd.hip as H
     seed = (dt << 20) ^ (rows << 8) ^ cols
     w = orc.synth_quant(dt, seed, rows, cols)
     x = orc.synth_normal(seed + 1, cols)
     wd = ctx.upload_weight(w)
-    rc, y = ctx.matvec_host(dt, wd, rows, cols, x, byte_size=w.nbytes)
+    with H.matvec_path(path):
+        rc, y = ctx.matvec_host(dt, wd, rows, cols, x, byte_size=w.nbytes)
     assert rc == 0
     ref = orc.matvec(dt, w, rows, cols, x)
     assert rel_l2(y, ref) < MV_TOL
