@@ -76,6 +76,12 @@ __device__ __forceinline__ T lld(const GQ_LDS uint8_t *base, uint32_t off) {
   return __builtin_bit_cast(T, *(const GQ_LDS N *)(base + off));
 }
 
+template <class T>
+__device__ __forceinline__ void lst(GQ_LDS uint8_t *base, uint32_t off, T v) {
+  typedef typename gq_native<sizeof(T)>::type N;
+  *(GQ_LDS N *)(base + off) = __builtin_bit_cast(N, v);
+}
+
 /* Eight bytes at a 2-byte-aligned LDS offset: three aligned dword reads and
  * two funnel shifts (reads up to 4 bytes past the field). */
 __device__ __forceinline__ uint2 lld8_a2(const GQ_LDS uint8_t *base, uint32_t off) {
@@ -124,6 +130,24 @@ __device__ __forceinline__ float gq_wave_sum(float v) {
   return v;
 }
 
+/* Full wave64 sum with DPP only (no LDS round trip): row sums, then
+ * row_bcast:15 and row_bcast:31 fold rows 0-1 and 2-3 into lane 63, which is
+ * returned to every lane (a scalar). */
+__device__ __forceinline__ float gq_wave_total(float v) {
+  v = gq_row16_sum(v);
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142, 0xa, 0xf, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xc, 0xf, false));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+/* Load of a wave-uniform value through the scalar data cache (counts against
+ * lgkmcnt, not vmcnt).  Only for data written before the kernel started. */
+template <class T>
+__device__ __forceinline__ T gq_sld(const void *p) {
+  typedef typename gq_native<sizeof(T)>::type N;
+  return __builtin_bit_cast(T, *(const __attribute__((address_space(4))) N *)p);
+}
+
 __device__ __forceinline__ float gq_wave_max(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
@@ -144,5 +168,17 @@ __device__ __forceinline__ uint2 gq_load8_a2(const uint8_t *p) {
 }
 
 __device__ __forceinline__ uint32_t gq_byte(uint32_t w, int k) { return (w >> (8 * k)) & 0xffu; }
+
+typedef float gq_f32x2 __attribute__((ext_vector_type(2)));
+
+/* Two 4-bit integers held in bytes 0,1 (HI = false) or 2,3 (HI = true) of w
+ * (each byte 0..15) to float, times 2^-9, in one v_cvt_pk_f32_fp8.  A byte
+ * 0..15 read as OCP FP8 E4M3 (bias 7) is exactly v * 2^-9: 0..7 are the
+ * subnormals m * 2^-3 * 2^-6, 8..15 the first normal binade
+ * (1 + m/8) * 2^-6 = (8 + m) * 2^-9. */
+template <bool HI>
+__device__ __forceinline__ gq_f32x2 gq_nib2f(uint32_t w) {
+  return __builtin_amdgcn_cvt_pk_f32_fp8((int)w, HI);
+}
 
 #endif

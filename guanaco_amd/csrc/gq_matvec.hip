@@ -27,6 +27,8 @@
  */
 #include <stdlib.h>
 
+#include <algorithm>
+
 #include "gq_device.h"
 #include "gq_internal.h"
 
@@ -39,58 +41,39 @@ template <int DT>
 struct Tr;
 
 /* ---------------------------------------------------------------- Q4_K
- * Lane part p (0..7) of a block reads qs[16p .. 16p+15]: chunk cc = p/2 of
- * 64 weights, half (p&1).  Low nibbles are weights 64cc + 16(p&1) + i of
- * sub-block 2cc, high nibbles weights 64cc + 32 + 16(p&1) + i of sub-block
- * 2cc+1 (quant_matvec_q4_k.c:93-132). */
+ * Lane part p (0..3) of a block owns chunk p of 64 weights: it reads
+ * qs[32p .. 32p+31], whose low nibbles are weights 64p + i of sub-block 2p
+ * and high nibbles weights 64p + 32 + i of sub-block 2p+1, i = 0..31
+ * (quant_matvec_q4_k.c:93-132). */
 template <>
 struct Tr<GQ_Q4_K> {
-  static constexpr int QK = 256, BB = 144, LPB = 8;
+  static constexpr int QK = 256, BB = 144, LPB = 4;
   struct Frag {
-    uint4 h, q;
+    uint4 h, q0, q1;
   };
   struct X {
-    float lo[16], hi[16];
+    float lo[32], hi[32];
     float slo, shi;
   };
-  __device__ static void load_x(X &x, const float *xs, int b, int p) {
-    const float *base = xs + 256 * b + 64 * (p >> 1) + 16 * (p & 1);
-    const float4 *a = (const float4 *)base, *c = (const float4 *)(base + 32);
+  /* x slice of block b from x staged in LDS (byte base xs), times the
+   * RMSNorm weight staged at nw when given; *ss (when given) accumulates the
+   * raw x^2 of the slice */
+  __device__ static void load_x(X &x, const GQ_LDS uint8_t *xs, const GQ_LDS uint8_t *nw, int b, int p,
+                                float *ss = nullptr) {
+    const uint32_t a = 4u * (256 * b + 64 * p), c = a + 128;
     float sl = 0.f, sh = 0.f;
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      float4 u = a[k], v = c[k];
-      x.lo[4 * k] = u.x, x.lo[4 * k + 1] = u.y, x.lo[4 * k + 2] = u.z, x.lo[4 * k + 3] = u.w;
-      x.hi[4 * k] = v.x, x.hi[4 * k + 1] = v.y, x.hi[4 * k + 2] = v.z, x.hi[4 * k + 3] = v.w;
-      sl += (u.x + u.y) + (u.z + u.w);
-      sh += (v.x + v.y) + (v.z + v.w);
-    }
-    x.slo = sl;
-    x.shi = sh;
-  }
-  __device__ static void load(Frag &f, const uint8_t *row, int b, int p) {
-    const uint8_t *blk = row + (size_t)b * BB;
-    f.h = gld<uint4>(blk);
-    f.q = gld<uint4>(blk + 16 + 16 * p);
-  }
-  __device__ static void load_lds(Frag &f, const GQ_LDS uint8_t *base, uint32_t blk, int p) {
-    f.h = lld<uint4>(base, blk);
-    f.q = lld<uint4>(base, blk + 16 + 16 * p);
-  }
-  /* x slice straight from global memory, times the RMSNorm weight when given;
-   * ss accumulates the raw x^2 of the slice */
-  __device__ static void load_xg(X &x, const float *xg, const float *nw, int b, int p, float &ss) {
-    const int base = 256 * b + 64 * (p >> 1) + 16 * (p & 1);
-    float sl = 0.f, sh = 0.f;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      float4 u = gld<float4>(xg + base + 4 * k), v = gld<float4>(xg + base + 32 + 4 * k);
-      ss = __builtin_fmaf(u.x, u.x, ss), ss = __builtin_fmaf(u.y, u.y, ss);
-      ss = __builtin_fmaf(u.z, u.z, ss), ss = __builtin_fmaf(u.w, u.w, ss);
-      ss = __builtin_fmaf(v.x, v.x, ss), ss = __builtin_fmaf(v.y, v.y, ss);
-      ss = __builtin_fmaf(v.z, v.z, ss), ss = __builtin_fmaf(v.w, v.w, ss);
+    for (int k = 0; k < 8; k++) {
+      float4 u = lld<float4>(xs, a + 16 * k), v = lld<float4>(xs, c + 16 * k);
+      if (ss) {
+        float q = *ss;
+        q = __builtin_fmaf(u.x, u.x, q), q = __builtin_fmaf(u.y, u.y, q), q = __builtin_fmaf(u.z, u.z, q);
+        q = __builtin_fmaf(u.w, u.w, q), q = __builtin_fmaf(v.x, v.x, q), q = __builtin_fmaf(v.y, v.y, q);
+        q = __builtin_fmaf(v.z, v.z, q), q = __builtin_fmaf(v.w, v.w, q);
+        *ss = q;
+      }
       if (nw) {
-        const float4 wu = gld<float4>(nw + base + 4 * k), wv = gld<float4>(nw + base + 32 + 4 * k);
+        const float4 wu = lld<float4>(nw, a + 16 * k), wv = lld<float4>(nw, c + 16 * k);
         u = make_float4(wu.x * u.x, wu.y * u.y, wu.z * u.z, wu.w * u.w);
         v = make_float4(wv.x * v.x, wv.y * v.y, wv.z * v.z, wv.w * v.w);
       }
@@ -102,36 +85,156 @@ struct Tr<GQ_Q4_K> {
     x.slo = sl;
     x.shi = sh;
   }
+  __device__ static void load(Frag &f, const uint8_t *row, int b, int p) {
+    const uint8_t *blk = row + (size_t)b * BB;
+    f.h = gld<uint4>(blk);
+    f.q0 = gld<uint4>(blk + 16 + 32 * p);
+    f.q1 = gld<uint4>(blk + 32 + 32 * p);
+  }
+  __device__ static void load_lds(Frag &f, const GQ_LDS uint8_t *base, uint32_t blk, int p) {
+    f.h = lld<uint4>(base, blk);
+    f.q0 = lld<uint4>(base, blk + 16 + 32 * p);
+    f.q1 = lld<uint4>(base, blk + 32 + 32 * p);
+  }
   __device__ static float dot(const Frag &f, const X &x, int p) {
     const float d = gq_h2f(f.h.x), dm = gq_h2f(f.h.x >> 16);
-    /* 6-bit (scale, min) of sub-blocks j = 2cc, 2cc+1 (quant_matvec_q4_k.c:47-56) */
-    const int cc = p >> 1;
-    const int sh = 16 * (cc & 1);
+    /* 6-bit (scale, min) of sub-blocks j = 2p, 2p+1 (quant_matvec_q4_k.c:47-56):
+     * j < 4:  sc = s[j] & 63,  m = s[j+4] & 63
+     * j >= 4: sc = (s[j+4] & 15) | (s[j-4] >> 6) << 4,
+     *         m  = (s[j+4] >> 4) | (s[j] >> 6) << 4
+     * with s[0..3] = h.y, s[4..7] = h.z, s[8..11] = h.w; both sub-blocks at
+     * once in bytes 0 and 1 of S and M, without branching on p */
+    const uint32_t sh = 16u * (uint32_t)(p & 1);
+    const bool hi = p >= 2;
     const uint32_t y = f.h.y >> sh, z = f.h.z >> sh, w = f.h.w >> sh;
-    uint32_t s0, m0, s1, m1;
-    if (cc < 2) {
-      s0 = y & 63u, m0 = z & 63u;
-      s1 = (y >> 8) & 63u, m1 = (z >> 8) & 63u;
-    } else {
-      s0 = (w & 15u) | (((y >> 6) & 3u) << 4), m0 = ((w >> 4) & 15u) | (((z >> 6) & 3u) << 4);
-      s1 = ((w >> 8) & 15u) | (((y >> 14) & 3u) << 4);
-      m1 = ((w >> 12) & 15u) | (((z >> 14) & 3u) << 4);
-    }
-    const uint32_t qw[4] = {f.q.x, f.q.y, f.q.z, f.q.w};
+    const uint32_t mlo = hi ? 0x0f0fu : 0x3f3fu, mhi = hi ? 0x3030u : 0u;
+    const uint32_t S = ((hi ? w : y) & mlo) | ((y >> 2) & mhi);
+    const uint32_t M = ((hi ? (w >> 4) : z) & mlo) | ((z >> 2) & mhi);
+    const uint32_t qw[8] = {f.q0.x, f.q0.y, f.q0.z, f.q0.w, f.q1.x, f.q1.y, f.q1.z, f.q1.w};
+    /* al, ah: 2^-9 * sum q x over the chunk's two sub-blocks (q converted as
+     * fp8, see gq_nib2f) */
     float al = 0.f, ah = 0.f;
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const uint32_t lo = qw[k] & 0x0f0f0f0fu, hi = (qw[k] >> 4) & 0x0f0f0f0fu;
+    for (int k = 0; k < 8; k++) {
+      const uint32_t lo = qw[k] & 0x0f0f0f0fu, hq = (qw[k] >> 4) & 0x0f0f0f0fu;
+      const gq_f32x2 l01 = gq_nib2f<false>(lo), l23 = gq_nib2f<true>(lo);
+      const gq_f32x2 h01 = gq_nib2f<false>(hq), h23 = gq_nib2f<true>(hq);
+      al = __builtin_fmaf(l01.x, x.lo[4 * k], al);
+      ah = __builtin_fmaf(h01.x, x.hi[4 * k], ah);
+      al = __builtin_fmaf(l01.y, x.lo[4 * k + 1], al);
+      ah = __builtin_fmaf(h01.y, x.hi[4 * k + 1], ah);
+      al = __builtin_fmaf(l23.x, x.lo[4 * k + 2], al);
+      ah = __builtin_fmaf(h23.x, x.hi[4 * k + 2], ah);
+      al = __builtin_fmaf(l23.y, x.lo[4 * k + 3], al);
+      ah = __builtin_fmaf(h23.y, x.hi[4 * k + 3], ah);
+    }
+    /* (d 2^9 sc)(2^-9 sum q x): power-of-two rescalings are exact, so this
+     * rounds as (d sc)(sum q x) */
+    const float d9 = d * 512.f;
+    float r = (d9 * (float)(S & 0xffu)) * al;
+    r = __builtin_fmaf(-(dm * (float)(M & 0xffu)), x.slo, r);
+    r = __builtin_fmaf(d9 * (float)((S >> 8) & 0xffu), ah, r);
+    r = __builtin_fmaf(-(dm * (float)((M >> 8) & 0xffu)), x.shi, r);
+    return r;
+  }
+};
+
+/* Q4_K with 8 lanes per block, for the kernels that split a row's columns
+ * over the waves of a workgroup (a wave covers 8 blocks per column tile).
+ * Lane part p (0..7) reads qs[16p .. 16p+15]: chunk cc = p/2 of 64 weights,
+ * half (p&1).  Low nibbles are weights 64cc + 16(p&1) + i of sub-block 2cc,
+ * high nibbles weights 64cc + 32 + 16(p&1) + i of sub-block 2cc+1
+ * (quant_matvec_q4_k.c:93-132). */
+struct TrQ4K8 {
+  static constexpr int QK = 256, BB = 144, LPB = 8;
+  struct Frag {
+    uint4 h, q;
+  };
+  struct X {
+    float lo[16], hi[16];
+    float slo, shi;
+  };
+  __device__ static void fill(X &x, float4 (&u)[4], float4 (&v)[4]) {
+    float sl = 0.f, sh = 0.f;
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        al = __builtin_fmaf((float)gq_byte(lo, j), x.lo[4 * k + j], al);
-        ah = __builtin_fmaf((float)gq_byte(hi, j), x.hi[4 * k + j], ah);
+    for (int k = 0; k < 4; k++) {
+      x.lo[4 * k] = u[k].x, x.lo[4 * k + 1] = u[k].y, x.lo[4 * k + 2] = u[k].z, x.lo[4 * k + 3] = u[k].w;
+      x.hi[4 * k] = v[k].x, x.hi[4 * k + 1] = v[k].y, x.hi[4 * k + 2] = v[k].z, x.hi[4 * k + 3] = v[k].w;
+      sl += (u[k].x + u[k].y) + (u[k].z + u[k].w);
+      sh += (v[k].x + v[k].y) + (v[k].z + v[k].w);
+    }
+    x.slo = sl;
+    x.shi = sh;
+  }
+  __device__ static void load_x(X &x, const GQ_LDS uint8_t *xs, const GQ_LDS uint8_t *nw, int b, int p,
+                                float *ss = nullptr) {
+    (void)nw, (void)ss;
+    const uint32_t a = 4u * (256 * b + 64 * (p >> 1) + 16 * (p & 1));
+    float4 u[4], v[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) u[k] = lld<float4>(xs, a + 16 * k), v[k] = lld<float4>(xs, a + 128 + 16 * k);
+    fill(x, u, v);
+  }
+  /* x slice straight from global memory, times the RMSNorm weight when given;
+   * ss accumulates the raw x^2 of the slice */
+  __device__ static void load_xg(X &x, const float *xg, const float *nw, int b, int p, float &ss) {
+    const int base = 256 * b + 64 * (p >> 1) + 16 * (p & 1);
+    float4 u[4], v[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      u[k] = gld<float4>(xg + base + 4 * k), v[k] = gld<float4>(xg + base + 32 + 4 * k);
+      ss = __builtin_fmaf(u[k].x, u[k].x, ss), ss = __builtin_fmaf(u[k].y, u[k].y, ss);
+      ss = __builtin_fmaf(u[k].z, u[k].z, ss), ss = __builtin_fmaf(u[k].w, u[k].w, ss);
+      ss = __builtin_fmaf(v[k].x, v[k].x, ss), ss = __builtin_fmaf(v[k].y, v[k].y, ss);
+      ss = __builtin_fmaf(v[k].z, v[k].z, ss), ss = __builtin_fmaf(v[k].w, v[k].w, ss);
+      if (nw) {
+        const float4 wu = gld<float4>(nw + base + 4 * k), wv = gld<float4>(nw + base + 32 + 4 * k);
+        u[k] = make_float4(wu.x * u[k].x, wu.y * u[k].y, wu.z * u[k].z, wu.w * u[k].w);
+        v[k] = make_float4(wv.x * v[k].x, wv.y * v[k].y, wv.z * v[k].z, wv.w * v[k].w);
       }
     }
-    float r = (d * (float)s0) * al;
-    r = __builtin_fmaf(-(dm * (float)m0), x.slo, r);
-    r = __builtin_fmaf(d * (float)s1, ah, r);
-    r = __builtin_fmaf(-(dm * (float)m1), x.shi, r);
+    fill(x, u, v);
+  }
+  __device__ static void load(Frag &f, const uint8_t *row, int b, int p) {
+    const uint8_t *blk = row + (size_t)b * BB;
+    f.h = gld<uint4>(blk);
+    f.q = gld<uint4>(blk + 16 + 16 * p);
+  }
+  __device__ static void load_lds(Frag &f, const GQ_LDS uint8_t *base, uint32_t blk, int p) {
+    f.h = lld<uint4>(base, blk);
+    f.q = lld<uint4>(base, blk + 16 + 16 * p);
+  }
+  __device__ static float dot(const Frag &f, const X &x, int p) {
+    const float d = gq_h2f(f.h.x), dm = gq_h2f(f.h.x >> 16);
+    /* (scale, min) of sub-blocks 2cc, 2cc+1 decoded as in Tr<GQ_Q4_K>::dot */
+    const int cc = p >> 1;
+    const uint32_t sh = 16u * (uint32_t)(cc & 1);
+    const bool hi = cc >= 2;
+    const uint32_t y = f.h.y >> sh, z = f.h.z >> sh, w = f.h.w >> sh;
+    const uint32_t mlo = hi ? 0x0f0fu : 0x3f3fu, mhi = hi ? 0x3030u : 0u;
+    const uint32_t S = ((hi ? w : y) & mlo) | ((y >> 2) & mhi);
+    const uint32_t M = ((hi ? (w >> 4) : z) & mlo) | ((z >> 2) & mhi);
+    const uint32_t qw[4] = {f.q.x, f.q.y, f.q.z, f.q.w};
+    float al = 0.f, ah = 0.f; /* 2^-9 sum q x (gq_nib2f) */
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const uint32_t lo = qw[k] & 0x0f0f0f0fu, hq = (qw[k] >> 4) & 0x0f0f0f0fu;
+      const gq_f32x2 l01 = gq_nib2f<false>(lo), l23 = gq_nib2f<true>(lo);
+      const gq_f32x2 h01 = gq_nib2f<false>(hq), h23 = gq_nib2f<true>(hq);
+      al = __builtin_fmaf(l01.x, x.lo[4 * k], al);
+      ah = __builtin_fmaf(h01.x, x.hi[4 * k], ah);
+      al = __builtin_fmaf(l01.y, x.lo[4 * k + 1], al);
+      ah = __builtin_fmaf(h01.y, x.hi[4 * k + 1], ah);
+      al = __builtin_fmaf(l23.x, x.lo[4 * k + 2], al);
+      ah = __builtin_fmaf(h23.x, x.hi[4 * k + 2], ah);
+      al = __builtin_fmaf(l23.y, x.lo[4 * k + 3], al);
+      ah = __builtin_fmaf(h23.y, x.hi[4 * k + 3], ah);
+    }
+    const float d9 = d * 512.f;
+    float r = (d9 * (float)(S & 0xffu)) * al;
+    r = __builtin_fmaf(-(dm * (float)(M & 0xffu)), x.slo, r);
+    r = __builtin_fmaf(d9 * (float)((S >> 8) & 0xffu), ah, r);
+    r = __builtin_fmaf(-(dm * (float)((M >> 8) & 0xffu)), x.shi, r);
     return r;
   }
 };
@@ -168,11 +271,43 @@ struct Tr<GQ_Q6_K> {
     float v[4][8];
     float s[4];
   };
-  __device__ static void load_x(X &x, const float *xs, int b, int p) {
-    const float *base = xs + 256 * b + 128 * (p >> 2) + 8 * (p & 3);
+  __device__ static void load_x(X &x, const GQ_LDS uint8_t *xs, const GQ_LDS uint8_t *nw, int b, int p,
+                                float *ss = nullptr) {
+    const uint32_t base = 4u * (256 * b + 128 * (p >> 2) + 8 * (p & 3));
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-      const float4 u = *(const float4 *)(base + 32 * r), v = *(const float4 *)(base + 32 * r + 4);
+      float4 u = lld<float4>(xs, base + 128 * r), v = lld<float4>(xs, base + 128 * r + 16);
+      if (ss) {
+        float q = *ss;
+        q = __builtin_fmaf(u.x, u.x, q), q = __builtin_fmaf(u.y, u.y, q), q = __builtin_fmaf(u.z, u.z, q);
+        q = __builtin_fmaf(u.w, u.w, q), q = __builtin_fmaf(v.x, v.x, q), q = __builtin_fmaf(v.y, v.y, q);
+        q = __builtin_fmaf(v.z, v.z, q), q = __builtin_fmaf(v.w, v.w, q);
+        *ss = q;
+      }
+      if (nw) {
+        const float4 wu = lld<float4>(nw, base + 128 * r), wv = lld<float4>(nw, base + 128 * r + 16);
+        u = make_float4(wu.x * u.x, wu.y * u.y, wu.z * u.z, wu.w * u.w);
+        v = make_float4(wv.x * v.x, wv.y * v.y, wv.z * v.z, wv.w * v.w);
+      }
+      x.v[r][0] = u.x, x.v[r][1] = u.y, x.v[r][2] = u.z, x.v[r][3] = u.w;
+      x.v[r][4] = v.x, x.v[r][5] = v.y, x.v[r][6] = v.z, x.v[r][7] = v.w;
+      x.s[r] = ((u.x + u.y) + (u.z + u.w)) + ((v.x + v.y) + (v.z + v.w));
+    }
+  }
+  __device__ static void load_xg(X &x, const float *xg, const float *nw, int b, int p, float &ss) {
+    const int base = 256 * b + 128 * (p >> 2) + 8 * (p & 3);
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      float4 u = gld<float4>(xg + base + 32 * r), v = gld<float4>(xg + base + 32 * r + 4);
+      ss = __builtin_fmaf(u.x, u.x, ss), ss = __builtin_fmaf(u.y, u.y, ss);
+      ss = __builtin_fmaf(u.z, u.z, ss), ss = __builtin_fmaf(u.w, u.w, ss);
+      ss = __builtin_fmaf(v.x, v.x, ss), ss = __builtin_fmaf(v.y, v.y, ss);
+      ss = __builtin_fmaf(v.z, v.z, ss), ss = __builtin_fmaf(v.w, v.w, ss);
+      if (nw) {
+        const float4 wu = gld<float4>(nw + base + 32 * r), wv = gld<float4>(nw + base + 32 * r + 4);
+        u = make_float4(wu.x * u.x, wu.y * u.y, wu.z * u.z, wu.w * u.w);
+        v = make_float4(wv.x * v.x, wv.y * v.y, wv.z * v.z, wv.w * v.w);
+      }
       x.v[r][0] = u.x, x.v[r][1] = u.y, x.v[r][2] = u.z, x.v[r][3] = u.w;
       x.v[r][4] = v.x, x.v[r][5] = v.y, x.v[r][6] = v.z, x.v[r][7] = v.w;
       x.s[r] = ((u.x + u.y) + (u.z + u.w)) + ((v.x + v.y) + (v.z + v.w));
@@ -194,25 +329,6 @@ struct Tr<GQ_Q6_K> {
     f.h = lld8_a2(base, blk + 128 + 32 * h + l0);
     f.s = lld8_a2(base, blk + 192 + 8 * h);
     f.d = lld<uint16_t>(base, blk + 208);
-  }
-  __device__ static void load_xg(X &x, const float *xg, const float *nw, int b, int p, float &ss) {
-    const int base = 256 * b + 128 * (p >> 2) + 8 * (p & 3);
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      float4 u = gld<float4>(xg + base + 32 * r), v = gld<float4>(xg + base + 32 * r + 4);
-      ss = __builtin_fmaf(u.x, u.x, ss), ss = __builtin_fmaf(u.y, u.y, ss);
-      ss = __builtin_fmaf(u.z, u.z, ss), ss = __builtin_fmaf(u.w, u.w, ss);
-      ss = __builtin_fmaf(v.x, v.x, ss), ss = __builtin_fmaf(v.y, v.y, ss);
-      ss = __builtin_fmaf(v.z, v.z, ss), ss = __builtin_fmaf(v.w, v.w, ss);
-      if (nw) {
-        const float4 wu = gld<float4>(nw + base + 32 * r), wv = gld<float4>(nw + base + 32 * r + 4);
-        u = make_float4(wu.x * u.x, wu.y * u.y, wu.z * u.z, wu.w * u.w);
-        v = make_float4(wv.x * v.x, wv.y * v.y, wv.z * v.z, wv.w * v.w);
-      }
-      x.v[r][0] = u.x, x.v[r][1] = u.y, x.v[r][2] = u.z, x.v[r][3] = u.w;
-      x.v[r][4] = v.x, x.v[r][5] = v.y, x.v[r][6] = v.z, x.v[r][7] = v.w;
-      x.s[r] = ((u.x + u.y) + (u.z + u.w)) + ((v.x + v.y) + (v.z + v.w));
-    }
   }
   __device__ static float dot(const Frag &f, const X &x, int p) {
     const int s = (p & 3) >> 1;
@@ -256,12 +372,37 @@ struct Tr<GQ_Q8_0> {
   struct X {
     float v[32];
   };
-  __device__ static void load_x(X &x, const float *xs, int b, int p) {
+  __device__ static void load_x(X &x, const GQ_LDS uint8_t *xs, const GQ_LDS uint8_t *nw, int b, int p,
+                                float *ss = nullptr) {
     (void)p;
-    const float4 *base = (const float4 *)(xs + 32 * b);
+    const uint32_t base = 128u * b;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
-      const float4 u = base[k];
+      float4 u = lld<float4>(xs, base + 16 * k);
+      if (ss) {
+        float q = *ss;
+        q = __builtin_fmaf(u.x, u.x, q), q = __builtin_fmaf(u.y, u.y, q);
+        q = __builtin_fmaf(u.z, u.z, q), q = __builtin_fmaf(u.w, u.w, q);
+        *ss = q;
+      }
+      if (nw) {
+        const float4 w = lld<float4>(nw, base + 16 * k);
+        u = make_float4(w.x * u.x, w.y * u.y, w.z * u.z, w.w * u.w);
+      }
+      x.v[4 * k] = u.x, x.v[4 * k + 1] = u.y, x.v[4 * k + 2] = u.z, x.v[4 * k + 3] = u.w;
+    }
+  }
+  __device__ static void load_xg(X &x, const float *xg, const float *nw, int b, int p, float &ss) {
+    (void)p;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      float4 u = gld<float4>(xg + 32 * b + 4 * k);
+      ss = __builtin_fmaf(u.x, u.x, ss), ss = __builtin_fmaf(u.y, u.y, ss);
+      ss = __builtin_fmaf(u.z, u.z, ss), ss = __builtin_fmaf(u.w, u.w, ss);
+      if (nw) {
+        const float4 w = gld<float4>(nw + 32 * b + 4 * k);
+        u = make_float4(w.x * u.x, w.y * u.y, w.z * u.z, w.w * u.w);
+      }
       x.v[4 * k] = u.x, x.v[4 * k + 1] = u.y, x.v[4 * k + 2] = u.z, x.v[4 * k + 3] = u.w;
     }
   }
@@ -284,20 +425,6 @@ struct Tr<GQ_Q8_0> {
       f.q[2 * k] = v.x, f.q[2 * k + 1] = v.y;
     }
   }
-  __device__ static void load_xg(X &x, const float *xg, const float *nw, int b, int p, float &ss) {
-    (void)p;
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-      float4 u = gld<float4>(xg + 32 * b + 4 * k);
-      ss = __builtin_fmaf(u.x, u.x, ss), ss = __builtin_fmaf(u.y, u.y, ss);
-      ss = __builtin_fmaf(u.z, u.z, ss), ss = __builtin_fmaf(u.w, u.w, ss);
-      if (nw) {
-        const float4 w = gld<float4>(nw + 32 * b + 4 * k);
-        u = make_float4(w.x * u.x, w.y * u.y, w.z * u.z, w.w * u.w);
-      }
-      x.v[4 * k] = u.x, x.v[4 * k + 1] = u.y, x.v[4 * k + 2] = u.z, x.v[4 * k + 3] = u.w;
-    }
-  }
   __device__ static float dot(const Frag &f, const X &x, int p) {
     (void)p;
     float acc = 0.f;
@@ -308,6 +435,18 @@ struct Tr<GQ_Q8_0> {
         acc = __builtin_fmaf((float)(int8_t)(f.q[k] >> (8 * j)), x.v[4 * k + j], acc);
     return acc * gq_h2f(f.d);
   }
+};
+
+/* Traits of the kernels that split a row's columns over the waves of a
+ * workgroup (the split-K LDS kernel and the register-path kernel): Q4_K with
+ * 8 lanes per block there, 4 in the whole-row kernels. */
+template <int DT>
+struct TrSplit {
+  using type = Tr<DT>;
+};
+template <>
+struct TrSplit<GQ_Q4_K> {
+  using type = TrQ4K8;
 };
 
 /* Stage x (optionally RMS-normalised: w * (x * 1/sqrt(mean(x^2) + eps)),
@@ -443,7 +582,7 @@ __device__ __forceinline__ void epilogue(const MvArgs &a, int total, int g, int 
  * issued before x is staged so both latencies overlap. */
 template <int DT, int R, int MODE>
 __global__ __launch_bounds__(kThreads) void mv_kernel(MvArgs a) {
-  using T = Tr<DT>;
+  using T = typename TrSplit<DT>::type;
   extern __shared__ float xs[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nb = a.cols / T::QK;
@@ -490,7 +629,7 @@ __global__ __launch_bounds__(kThreads) void mv_kernel(MvArgs a) {
       const int b = t * BPT + bt;
       const bool bok = b < nb;
       typename T::X x;
-      T::load_x(x, xs, bok ? b : nb - 1, part);
+      T::load_x(x, (const GQ_LDS uint8_t *)xs, nullptr, bok ? b : nb - 1, part);
 #pragma unroll
       for (int i = 0; i < R; i++) {
         const float v = T::dot(cur[i], x, part);
@@ -518,15 +657,21 @@ __global__ __launch_bounds__(kThreads) void mv_kernel(MvArgs a) {
  * LDS-streamed matvec.
  *
  * The weight rows of a workgroup's row groups ("stages" of rs rows) are
- * streamed into a ring of kStages LDS buffers with direct global->LDS DMA
- * loads (global_load_lds_dwordx4: 1 KB per wave instruction, no VGPRs), two
+ * streamed into a ring of kNS LDS buffers with direct global->LDS DMA loads
+ * (global_load_lds_dwordx4: 1 KB per wave instruction, no VGPRs), kNS-1
  * stages ahead of the one being computed, so each CU keeps tens of KB of HBM
  * reads in flight independent of register pressure and of the 2-byte block
  * alignment of Q6_K.  Waves keep their x slices in registers for the whole
  * kernel (RMSNorm folded as y = r * W (w .* x)); a team of ts waves splits K
- * (wave j owns tiles j, j+ts, ...) and the per-row partials meet in LDS. */
-constexpr int kStages = 3;
-constexpr int kStageCap = 24576; /* bytes of weights per stage buffer */
+ * (wave j owns tiles j, j+ts, ...).  A wave computes RW rows at a time (all
+ * their LDS reads issued before the arithmetic), reduces each row over its
+ * 16-lane DPP rows only, and the 4 row partials per wave meet in LDS, where
+ * the epilogue adds them. */
+constexpr int kNS = 3;    /* stage buffers: deeper rings measured no faster */
+constexpr int kRing = 8;  /* residual-row ring slots (>= kNS + 1) */
+constexpr int kRedW = kWaves * 4; /* row partials per row: 4 per wave */
+int g_stage_cap = 24576;  /* bytes of weights per stage buffer */
+int g_lds_wg_per_cu = 0;  /* 0: as many workgroups per CU as LDS allows */
 
 struct MvPlan {
   int rs;           /* weight rows per stage (MV_SWIGLU: rs/2 gate + rs/2 up) */
@@ -538,10 +683,11 @@ struct MvPlan {
   int total;        /* output rows */
 };
 
-/* Wave `wave`'s 1 KB copy instructions for nbytes (a multiple of 16). */
-__device__ __forceinline__ int copy_count(int nbytes, int wave) {
+/* Wave `wave`'s 1 KB copy instructions for nbytes (a multiple of 16) split
+ * over nwv waves. */
+__device__ __forceinline__ int copy_count(int nbytes, int wave, int nwv = kWaves) {
   const int ng = (nbytes / 16 + 63) / 64;
-  return wave < ng ? (ng - wave + kWaves - 1) / kWaves : 0;
+  return wave < ng ? (ng - wave + nwv - 1) / nwv : 0;
 }
 
 /* The DMA loads are issued from inline assembly on purpose: the compiler's
@@ -549,19 +695,17 @@ __device__ __forceinline__ int copy_count(int nbytes, int wave) {
  * location and would put s_waitcnt vmcnt(0) in front of each LDS read of the
  * compute loop, draining the stages in flight.  Completion is tracked by hand
  * (wait_vmcnt + barrier).  VMEM loads retire in order, so the compiler's own
- * waits for other loads can only wait longer than needed, never less. */
+ * waits for other loads can only wait longer than needed, never less.  The
+ * LDS address goes in M0 (the "{m0}" operand: the compiler writes M0). */
 __device__ __forceinline__ void dma16(const uint8_t *src, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
-               :
-               : "v"(src), "s"(lds_addr)
-               : "m0");
+  asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(lds_addr));
 }
 
 __device__ __forceinline__ void copy_range(const uint8_t *src, int nbytes, GQ_LDS uint8_t *dst, int wave,
-                                           int lane) {
+                                           int lane, int nwv = kWaves) {
   const int nchunk = nbytes / 16, ng = (nchunk + 63) / 64;
   const uint32_t base = (uint32_t)(uintptr_t)dst;
-  for (int g = wave; g < ng; g += kWaves) {
+  for (int g = wave; g < ng; g += nwv) {
     const int c = g * 64 + lane;
     const uint32_t d = __builtin_amdgcn_readfirstlane(base + (uint32_t)g * 1024u);
     if (c < nchunk) dma16(src + (size_t)c * 16, d);
@@ -570,10 +714,7 @@ __device__ __forceinline__ void copy_range(const uint8_t *src, int nbytes, GQ_LD
 
 /* One dword per lane into LDS (the residual rows of a stage). */
 __device__ __forceinline__ void dma4(const float *src, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off"
-               :
-               : "v"(src), "s"(lds_addr)
-               : "m0");
+  asm volatile("global_load_lds_dword %0, off" : : "v"(src), "{m0}"(lds_addr));
 }
 
 /* Stage `g`'s rows: global rows [g*rs, g*rs+rs) (clamped to the end of their
@@ -605,14 +746,18 @@ __device__ __forceinline__ int issue_stage(const MvArgs &a, const MvPlan &pl, in
   return c;
 }
 
-/* s_waitcnt vmcnt(n) with the other counters left alone (n <= 63). */
+/* s_waitcnt vmcnt(n) with the other counters left alone (vmcnt(0) for n > 63). */
 __device__ __forceinline__ void wait_vmcnt(int n) {
 #define GQ_W(N)                                                                                   \
   case N: __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | (7 << 4) | (15 << 8)); break;
   switch (n) {
     GQ_W(0) GQ_W(1) GQ_W(2) GQ_W(3) GQ_W(4) GQ_W(5) GQ_W(6) GQ_W(7) GQ_W(8) GQ_W(9) GQ_W(10)
     GQ_W(11) GQ_W(12) GQ_W(13) GQ_W(14) GQ_W(15) GQ_W(16) GQ_W(17) GQ_W(18) GQ_W(19) GQ_W(20)
-    GQ_W(21) GQ_W(22) GQ_W(23) GQ_W(24)
+    GQ_W(21) GQ_W(22) GQ_W(23) GQ_W(24) GQ_W(25) GQ_W(26) GQ_W(27) GQ_W(28) GQ_W(29) GQ_W(30)
+    GQ_W(31) GQ_W(32) GQ_W(33) GQ_W(34) GQ_W(35) GQ_W(36) GQ_W(37) GQ_W(38) GQ_W(39) GQ_W(40)
+    GQ_W(41) GQ_W(42) GQ_W(43) GQ_W(44) GQ_W(45) GQ_W(46) GQ_W(47) GQ_W(48) GQ_W(49) GQ_W(50)
+    GQ_W(51) GQ_W(52) GQ_W(53) GQ_W(54) GQ_W(55) GQ_W(56) GQ_W(57) GQ_W(58) GQ_W(59) GQ_W(60)
+    GQ_W(61) GQ_W(62) GQ_W(63)
   default: __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); break; /* vmcnt(0) */
   }
 #undef GQ_W
@@ -654,14 +799,15 @@ __device__ __forceinline__ void store_row(const MvArgs &a, int s, int lr, float 
     gst<float>(sg.y + ((size_t)h * a.rope.max_seq + pos) * hd + d, v);
 }
 
-template <int DT, int MODE, int TPW>
+template <int DT, int MODE, int TPW, int RW>
 __global__ __launch_bounds__(kThreads) void mvl_kernel(MvArgs a, MvPlan pl) {
-  using T = Tr<DT>;
+  using T = typename TrSplit<DT>::type;
+  constexpr int NS = kNS;
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   GQ_LDS uint8_t *lds = (GQ_LDS uint8_t *)smem;
-  __shared__ float red[2][32][kWaves];
+  __shared__ __attribute__((aligned(16))) float red[2][32][kRedW];
   __shared__ float red_ss[kWaves];
-  __shared__ __attribute__((aligned(16))) float rres[4][32];
+  __shared__ __attribute__((aligned(16))) float rres[kRing][32];
   __shared__ float2 scs[256];
   GQ_LDS float *lres = (GQ_LDS float *)&rres[0][0];
   const int lane = threadIdx.x & 63;
@@ -694,7 +840,7 @@ __global__ __launch_bounds__(kThreads) void mvl_kernel(MvArgs a, MvPlan pl) {
         scs[i] = gld<float2>(a.rope.cs + (size_t)pos * half + i);
   }
   float rscale = 1.f;
-  if (a.norm_w) {
+  if (a.norm_w) { /* 1/sqrt(mean(x^2) + eps) (kernels_cpu.c:242-253) */
     ss = gq_wave_sum(ss);
     if (lane == 0) red_ss[wave] = active && team == 0 ? ss : 0.f;
     __syncthreads();
@@ -705,70 +851,458 @@ __global__ __launch_bounds__(kThreads) void mvl_kernel(MvArgs a, MvPlan pl) {
   }
   __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); /* those loads are done */
 
-  /* nxt: this wave's DMA instructions for stage k+1 (issued, maybe pending) */
-  static_assert(kStages == 3, "the DMA bookkeeping below assumes three stages");
-  int nxt = 0;
-  if (mygroups > 0) (void)issue_stage<MODE>(a, pl, blockIdx.x, lds, lres, wave, lane);
-  if (mygroups > 1) nxt = issue_stage<MODE>(a, pl, blockIdx.x + gridDim.x, lds + pl.stride, lres + 32, wave, lane);
+  static_assert(NS == 3 && NS + 1 <= kRing, "the loop below keeps two stages in flight");
+  /* Stage k's copies are issued at iteration k-2, before that iteration's
+   * wait, into the slot stage k-3 used (computed at iteration k-3, before
+   * the barrier closing it); at iteration k they are waited for, computed
+   * and at iteration k+1 its rows are finished (reduced, stored). */
+  (void)issue_stage<MODE>(a, pl, blockIdx.x, lds, lres, wave, lane); /* mygroups >= 1 */
+  int nxt = mygroups > 1 ? issue_stage<MODE>(a, pl, blockIdx.x + gridDim.x, lds + pl.stride, lres + 32, wave, lane)
+                         : 0; /* this wave's copies of stage k+1 */
 
   const int hrows = MODE == MV_SWIGLU ? pl.rs / 2 : pl.rs;
-  int slot = 0; /* k % kStages */
+  const int rpw = pl.rs / pl.nteam; /* rows per team and stage, a multiple of RW */
+  int slot = 0;                     /* k % NS */
   for (int k = 0; k <= mygroups; k++) {
     if (k < mygroups) {
-      const int kn = k + kStages - 1, sn = slot == 0 ? 2 : slot - 1; /* kn % kStages */
-      const int nn = kn < mygroups ? issue_stage<MODE>(a, pl, blockIdx.x + kn * gridDim.x,
-                                                       lds + sn * pl.stride, lres + (kn & 3) * 32, wave, lane)
+      const int kn = k + 2, sn = slot == 0 ? 2 : slot - 1; /* kn % NS */
+      const int nn = kn < mygroups ? issue_stage<MODE>(a, pl, blockIdx.x + kn * gridDim.x, lds + sn * pl.stride,
+                                                       lres + (kn % kRing) * 32, wave, lane)
                                    : 0;
-      /* VMEM loads complete in issue order: with at most the stage k+1 and
-       * k+2 copies outstanding, this wave's copies of stage k have landed;
-       * the barrier extends that to every wave's */
+      /* VMEM loads complete in issue order: with at most stages k+1 and k+2
+       * outstanding, this wave's copies of stage k have landed; the barrier
+       * extends that to every wave's */
       wait_vmcnt(nxt + nn);
       nxt = nn;
     }
     __syncthreads();
-    if (k > 0) { /* finish the rows of stage k-1 */
+    if (k > 0) { /* finish the rows of stage k-1: row t on lane t/4 of wave t%4 */
       const int r0 = (blockIdx.x + (k - 1) * gridDim.x) * hrows;
       int s = 0, lr0 = r0;
       if (MODE != MV_SWIGLU) locate(a, r0, s, lr0);
       s = __builtin_amdgcn_readfirstlane(s);
       lr0 = __builtin_amdgcn_readfirstlane(lr0);
-      const int t = threadIdx.x;
+      const int t = lane * kWaves + wave;
       if (t < hrows && r0 + t < pl.total) {
         const int tp = MODE == MV_SWIGLU ? t + hrows : (t ^ 1);
+        const int nred = 4 * pl.ts;
         float v = 0.f, w = 0.f;
-        for (int j = 0; j < pl.ts; j++) v += red[(k - 1) & 1][t][j], w += red[(k - 1) & 1][tp][j];
+        for (int j = 0; j < nred; j++) v += red[(k - 1) & 1][t][j], w += red[(k - 1) & 1][tp][j];
         store_row<MODE>(a, s, lr0 + t, v * rscale, w * rscale,
-                        MODE == MV_RESID ? rres[(k - 1) & 3][t] : 0.f, pos, scs);
+                        MODE == MV_RESID ? rres[(k - 1) % kRing][t] : 0.f, pos, scs);
       }
     }
     if (k == mygroups) break;
     if (active) {
       const GQ_LDS uint8_t *buf = lds + slot * pl.stride;
-      for (int i = team; i < pl.rs; i += pl.nteam) {
-        float acc = 0.f;
+      for (int i0 = team * rpw; i0 < (team + 1) * rpw; i0 += RW) {
+        float acc[RW];
+#pragma unroll
+        for (int r = 0; r < RW; r++) acc[r] = 0.f;
 #pragma unroll
         for (int ti = 0; ti < TPW; ti++) {
           const int t = wj + ti * pl.ts;
           const int b = t * BPT + bt;
           if (t < pl.ntile) {
-            typename T::Frag f;
-            T::load_lds(f, buf, i * pl.rowbytes + min(b, nb - 1) * T::BB, part);
-            const float v = T::dot(f, xs[ti], part);
-            acc += b < nb ? v : 0.f;
+            typename T::Frag f[RW];
+            const uint32_t off = i0 * pl.rowbytes + min(b, nb - 1) * T::BB;
+#pragma unroll
+            for (int r = 0; r < RW; r++) T::load_lds(f[r], buf, off + r * pl.rowbytes, part);
+#pragma unroll
+            for (int r = 0; r < RW; r++) {
+              const float v = T::dot(f[r], xs[ti], part);
+              acc[r] += b < nb ? v : 0.f;
+            }
           }
         }
-        acc = gq_wave_sum(acc);
-        if (lane == 0) red[k & 1][i][wj] = acc;
+#pragma unroll
+        for (int r = 0; r < RW; r++) acc[r] = gq_row16_sum(acc[r]);
+        if ((lane & 15) == 0)
+#pragma unroll
+          for (int r = 0; r < RW; r++) red[k & 1][i0 + r][wj * 4 + (lane >> 4)] = acc[r];
       }
     }
     __syncthreads();
-    slot = slot == kStages - 1 ? 0 : slot + 1;
+    slot = slot == NS - 1 ? 0 : slot + 1;
   }
 }
 
+/* ------------------------------------------------------------------------
+ * Wave-private LDS-streamed matvec, for shapes where one wave covers whole
+ * rows (at most two column tiles, x slices in registers: every 4096-column
+ * projection and the LM head).
+ *
+ * Each wave owns groups of RW weight rows (MV_SWIGLU: RW/2 gate + RW/2 up
+ * rows) and streams them with DMA into a private ring of ns LDS slots, ns-1
+ * groups ahead of the one it computes; it reduces each row over the wave with
+ * DPP and stores.  Waves never wait for each other after the prologue: no
+ * barriers in the loop, so one wave's memory latency overlaps the others'
+ * arithmetic.  The ring depth ns (3..8) is chosen per launch to fill LDS.
+ *
+ * LDS is slot-major: slot k of every wave, for k = 0..ns-1.  The prologue
+ * stages x (and the RMSNorm weight) in the last slot row, which only the
+ * loop's first DMA overwrites, so x's copy overlaps the first ns-1 groups'
+ * copies; the waves take their x slices into registers before the loop. */
+constexpr int kMaxWaves = 16;
+constexpr int kMaxNS = 8;
+
+struct MwPlan {
+  int ngroups;  /* groups over the launch */
+  int rowbytes;
+  int slot;     /* LDS bytes per ring slot */
+  int ns;       /* ring slots per wave */
+  int x_off;    /* LDS offset of staged x (the last slot row) */
+  int nw_off;   /* LDS offset of the staged norm weight */
+  int total;    /* output rows */
+};
+
+/* Rows of group g: first local row and count, segment (uniform). */
+template <int MODE, int RW>
+__device__ __forceinline__ void group_span(const MvArgs &a, const MwPlan &pl, int g, int &s, int &lr, int &n) {
+  if (MODE == MV_SWIGLU) {
+    constexpr int P = RW / 2;
+    s = 0, lr = g * P, n = min(P, pl.total - lr);
+  } else {
+    locate(a, g * RW, s, lr);
+    n = min(RW, a.seg[s].rows - lr);
+  }
+}
+
+/* This wave's DMA instruction count for group g. */
+template <int MODE, int RW>
+__device__ __forceinline__ int group_count(const MvArgs &a, const MwPlan &pl, int g) {
+  int s, lr, n;
+  group_span<MODE, RW>(a, pl, g, s, lr, n);
+  const int c = copy_count(n * pl.rowbytes, 0, 1);
+  return MODE == MV_SWIGLU ? 2 * c : c + (MODE == MV_RESID ? 1 : 0);
+}
+
+/* Rows of group g into ring slot `buf` (one wave), and for MV_RESID the
+ * group's residual values into `rbuf`. */
+template <int MODE, int RW>
+__device__ __forceinline__ void issue_group(const MvArgs &a, const MwPlan &pl, int g, GQ_LDS uint8_t *buf,
+                                            GQ_LDS float *rbuf, int lane) {
+  int s, lr, n;
+  group_span<MODE, RW>(a, pl, g, s, lr, n);
+  const int nb = n * pl.rowbytes;
+  if (MODE == MV_SWIGLU) {
+    copy_range(a.seg[0].w + (size_t)lr * pl.rowbytes, nb, buf, 0, lane, 1);
+    copy_range(a.seg[1].w + (size_t)lr * pl.rowbytes, nb, buf + (RW / 2) * pl.rowbytes, 0, lane, 1);
+    return;
+  }
+  copy_range(a.seg[s].w + (size_t)lr * pl.rowbytes, nb, buf, 0, lane, 1);
+  if (MODE == MV_RESID) {
+    const uint32_t d = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)rbuf);
+    if (lane < n) dma4(a.seg[s].r + lr + lane, d);
+  }
+}
+
+template <int DT, int MODE, int TPW, int RW>
+__global__ __launch_bounds__(kMaxWaves * GQ_WAVE) void mvw_kernel(MvArgs a, MwPlan pl) {
+  using T = Tr<DT>;
+  constexpr int P = MODE == MV_SWIGLU ? RW / 2 : RW; /* output rows per group */
+  static_assert(RW <= 4 && (MODE != MV_SWIGLU || RW % 2 == 0), "group shape");
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  GQ_LDS uint8_t *lds = (GQ_LDS uint8_t *)smem;
+  __shared__ float red_ss[kMaxWaves];
+  __shared__ __attribute__((aligned(16))) float2 scs[256];
+  __shared__ __attribute__((aligned(16))) float rres[kMaxWaves][kMaxNS][4];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nwv = blockDim.x >> 6;
+  constexpr int BPT = GQ_WAVE / T::LPB;
+  const int nb = a.cols / T::QK;
+  const int part = lane % T::LPB, bt = lane / T::LPB;
+  const int gw = blockIdx.x * nwv + wave, W = gridDim.x * nwv;
+  const int mygroups = gw < pl.ngroups ? (pl.ngroups - 1 - gw) / W + 1 : 0;
+  const int ns = pl.ns, row = nwv * pl.slot; /* bytes of one slot row */
+  GQ_LDS uint8_t *ring = lds + wave * pl.slot; /* slot k at ring + k * row */
+  GQ_LDS float *rr = (GQ_LDS float *)&rres[wave][0][0];
+
+  /* prologue: x, the norm weight and the RoPE row into LDS (the whole
+   * workgroup), then this wave's first ns-1 groups, all with DMA */
+  const int xb = a.cols * 4;
+  copy_range((const uint8_t *)a.x, xb, lds + pl.x_off, wave, lane, nwv);
+  if (a.norm_w) copy_range((const uint8_t *)a.norm_w, xb, lds + pl.nw_off, wave, lane, nwv);
+  int pos = 0;
+  if (MODE == MV_STORE && a.rope.cs) {
+    pos = a.rope.pos_dev ? gq_sld<int>(a.rope.pos_dev) : a.rope.pos;
+    const int hd = a.rope.head_dim; /* floats in one table row (hd/2 pairs) */
+    if (wave == 0 && pos >= 0 && pos < a.rope.max_seq) {
+      const float *crow = (const float *)(a.rope.cs + (size_t)pos * (hd >> 1));
+      const uint32_t base = (uint32_t)(uintptr_t)(GQ_LDS float2 *)scs;
+      for (int o = 0; o < hd; o += 64)
+        if (lane < hd - o) dma4(crow + o + lane, __builtin_amdgcn_readfirstlane(base + 4u * o));
+    }
+  }
+  int pend = 0; /* this wave's DMA instructions of the groups after the current one */
+  for (int k = 0; k < ns - 1 && k < mygroups; k++) {
+    issue_group<MODE, RW>(a, pl, gw + k * W, ring + k * row, rr + 4 * k, lane);
+    pend += group_count<MODE, RW>(a, pl, gw + k * W);
+  }
+  /* VMEM loads complete in issue order: with at most the groups' copies
+   * outstanding, this wave's part of x (and the rest) has landed; the barrier
+   * extends that to every wave's */
+  wait_vmcnt(pend);
+  __syncthreads();
+  float rscale = 1.f;
+  if (a.norm_w) { /* 1/sqrt(mean(x^2) + eps) (kernels_cpu.c:242-253) */
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < (a.cols >> 2); i += blockDim.x) {
+      const float4 v = lld<float4>(lds + pl.x_off, 16u * i);
+      ss = __builtin_fmaf(v.x, v.x, ss), ss = __builtin_fmaf(v.y, v.y, ss);
+      ss = __builtin_fmaf(v.z, v.z, ss), ss = __builtin_fmaf(v.w, v.w, ss);
+    }
+    ss = gq_wave_total(ss);
+    if (lane == 0) red_ss[wave] = ss;
+    __syncthreads();
+    float tot = 0.f;
+    for (int w = 0; w < nwv; w++) tot += red_ss[w];
+    tot = tot / (float)a.cols;
+    tot = tot + a.eps;
+    rscale = 1.0f / sqrtf(tot);
+  }
+  typename T::X xs[TPW];
+#pragma unroll
+  for (int i = 0; i < TPW; i++)
+    T::load_x(xs[i], lds + pl.x_off, a.norm_w ? lds + pl.nw_off : nullptr, min(i * BPT + bt, nb - 1), part);
+  __syncthreads(); /* the last slot row is free from here on */
+
+  int slot = 0; /* j % ns */
+  for (int j = 0; j < mygroups; j++) {
+    const int g = gw + j * W;
+    {
+      const int jn = j + ns - 1, sn = slot == 0 ? ns - 1 : slot - 1; /* jn % ns: computed at j-1 */
+      if (jn < mygroups) {
+        issue_group<MODE, RW>(a, pl, gw + jn * W, ring + sn * row, rr + 4 * sn, lane);
+        pend += group_count<MODE, RW>(a, pl, gw + jn * W);
+      }
+      pend -= group_count<MODE, RW>(a, pl, g);
+      wait_vmcnt(pend); /* group j has landed */
+    }
+    const GQ_LDS uint8_t *buf = ring + slot * row;
+    float acc[RW];
+#pragma unroll
+    for (int r = 0; r < RW; r++) acc[r] = 0.f;
+#pragma unroll
+    for (int ti = 0; ti < TPW; ti++) {
+      const int b = ti * BPT + bt;
+      typename T::Frag f[RW];
+      const uint32_t off = min(b, nb - 1) * T::BB;
+#pragma unroll
+      for (int r = 0; r < RW; r++) T::load_lds(f[r], buf, off + r * pl.rowbytes, part);
+#pragma unroll
+      for (int r = 0; r < RW; r++) {
+        const float v = T::dot(f[r], xs[ti], part);
+        acc[r] += b < nb ? v : 0.f;
+      }
+    }
+    float tot[RW];
+#pragma unroll
+    for (int r = 0; r < RW; r++) tot[r] = gq_wave_total(acc[r]) * rscale;
+    /* lane r < P finishes output row r of the group */
+    float v = tot[0], w = MODE == MV_SWIGLU ? tot[P] : tot[RW > 1 ? 1 : 0];
+#pragma unroll
+    for (int r = 1; r < P; r++)
+      if (lane == r) v = tot[r], w = MODE == MV_SWIGLU ? tot[P + r] : tot[r ^ 1];
+    int s, lr0, n;
+    group_span<MODE, RW>(a, pl, g, s, lr0, n);
+    s = __builtin_amdgcn_readfirstlane(s);
+    lr0 = __builtin_amdgcn_readfirstlane(lr0);
+    if (lane < n)
+      store_row<MODE>(a, s, lr0 + lane, v, w, MODE == MV_RESID ? rres[wave][slot][lane] : 0.f, pos,
+                      (const float2 *)scs);
+    slot = slot == ns - 1 ? 0 : slot + 1;
+  }
+}
+
+/* ------------------------------------------------------------------------
+ * Register-ring matvec, for shapes where one wave covers whole rows.
+ *
+ * Each wave streams its groups of RW weight rows straight into registers
+ * with ordinary global loads, kRB - 1 groups ahead of the one it computes
+ * (a ring of kRB register buffers, rotated by unrolling so no data moves),
+ * so the compiler tracks every load and waits on exactly the group it needs.
+ * Nothing but x goes through LDS; the register file (512 KB per CU) holds
+ * far more bytes in flight than LDS could.  x (times the RMSNorm weight) is
+ * staged once per workgroup and each wave keeps its slices in registers and
+ * computes the norm's sum of squares itself (a wave holds all of x).  Finished
+ * rows are parked in LDS and stored after the loop: no store sits between a
+ * load and its wait. */
+constexpr int kRB = 3;
+
+template <int DT, int TPW, int RW>
+struct RBuf {
+  typename Tr<DT>::Frag f[RW][TPW];
+  float res;  /* MV_RESID: residual of row `lane` of the group */
+  float2 cs;  /* fused RoPE: (cos, sin) of row `lane` of the group */
+};
+
+/* Loads of group g into B.  Groups past the wave's last are replaced by its
+ * last group (already cached): the load sequence is the same on every path,
+ * which keeps the compiler's wait counts exact. */
+template <int DT, int MODE, int TPW, int RW>
+__device__ __forceinline__ void rload(const MvArgs &a, const MwPlan &pl, int g, RBuf<DT, TPW, RW> &B, int lane,
+                                      int part, int bt, int nb, int pos) {
+  using T = Tr<DT>;
+  constexpr int BPT = GQ_WAVE / T::LPB;
+  int s, lr, n;
+  group_span<MODE, RW>(a, pl, g, s, lr, n);
+#pragma unroll
+  for (int r = 0; r < RW; r++) {
+    const uint8_t *row;
+    if (MODE == MV_SWIGLU) {
+      constexpr int H = RW / 2;
+      row = a.seg[r / H].w + (size_t)(lr + min(r % H, n - 1)) * pl.rowbytes;
+    } else {
+      row = a.seg[s].w + (size_t)(lr + min(r, n - 1)) * pl.rowbytes;
+    }
+#pragma unroll
+    for (int ti = 0; ti < TPW; ti++) T::load(B.f[r][ti], row, min(ti * BPT + bt, nb - 1), part);
+  }
+  if (MODE == MV_RESID) B.res = gld<float>(a.seg[s].r + lr + min(lane, n - 1));
+  if (MODE == MV_STORE && a.rope.cs) {
+    const int hd = a.rope.head_dim;
+    const int d = (lr + min(lane, n - 1)) % hd;
+    const int p = pos >= 0 && pos < a.rope.max_seq ? pos : 0;
+    B.cs = gld<float2>(a.rope.cs + (size_t)p * (hd >> 1) + (d >> 1));
+  }
+}
+
+/* Destination of output row lr of segment s (nullptr: position rejected). */
+template <int MODE>
+__device__ __forceinline__ float *rdest(const MvArgs &a, int s, int lr, int pos) {
+  if (MODE == MV_SWIGLU) return a.seg[0].y + lr;
+  const MvSeg &sg = a.seg[s];
+  if (MODE == MV_RESID || sg.kind == SEG_PLAIN || sg.kind == SEG_ROPE) return sg.y + lr;
+  if (pos < 0 || pos >= a.rope.max_seq) return nullptr; /* rejected on the host */
+  const int hd = a.rope.head_dim, h = lr / hd, d = lr - h * hd;
+  return sg.y + ((size_t)h * a.rope.max_seq + pos) * hd + d;
+}
+
+template <int DT, int MODE, int TPW, int RW>
+__global__ __launch_bounds__(8 * GQ_WAVE) void mvr_kernel(MvArgs a, MwPlan pl) {
+  using T = Tr<DT>;
+  constexpr int P = MODE == MV_SWIGLU ? RW / 2 : RW; /* output rows per group */
+  static_assert(RW <= 4 && RW % 2 == 0, "group shape");
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  GQ_LDS uint8_t *lds = (GQ_LDS uint8_t *)smem;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nwv = blockDim.x >> 6;
+  constexpr int BPT = GQ_WAVE / T::LPB;
+  const int nb = a.cols / T::QK;
+  const int part = lane % T::LPB, bt = lane / T::LPB;
+  const int gw = blockIdx.x * nwv + wave, W = gridDim.x * nwv;
+  const int mygroups = gw < pl.ngroups ? (pl.ngroups - 1 - gw) / W + 1 : 0;
+  const int glast = gw + max(mygroups - 1, 0) * W;
+  int pos = 0;
+  if (MODE == MV_STORE && a.rope.cs) pos = a.rope.pos_dev ? gq_sld<int>(a.rope.pos_dev) : a.rope.pos;
+  /* parked outputs: P floats per group, pl.slot groups per wave */
+  GQ_LDS float *obuf = (GQ_LDS float *)(lds + pl.x_off) + (size_t)wave * pl.slot * P;
+
+  RBuf<DT, TPW, RW> B0, B1, B2;
+  if (mygroups > 0) {
+    rload<DT, MODE, TPW, RW>(a, pl, gw, B0, lane, part, bt, nb, pos);
+    rload<DT, MODE, TPW, RW>(a, pl, min(gw + W, glast), B1, lane, part, bt, nb, pos);
+  }
+  /* x and the norm weight into LDS (DMA, whole workgroup), behind the first
+   * groups' loads; everything this wave issued has landed after vmcnt(0),
+   * every wave's after the barrier */
+  const int xb = a.cols * 4;
+  copy_range((const uint8_t *)a.x, xb, lds, wave, lane, nwv);
+  if (a.norm_w) copy_range((const uint8_t *)a.norm_w, xb, lds + pl.nw_off, wave, lane, nwv);
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); /* vmcnt(0) */
+  __syncthreads();
+  float ss = 0.f;
+  typename T::X xs[TPW];
+#pragma unroll
+  for (int i = 0; i < TPW; i++) {
+    const int b = i * BPT + bt;
+    float q = 0.f;
+    T::load_x(xs[i], lds, a.norm_w ? lds + pl.nw_off : nullptr, min(b, nb - 1), part, &q);
+    if (b < nb) ss += q;
+  }
+  float rscale = 1.f;
+  if (a.norm_w) { /* 1/sqrt(mean(x^2) + eps) (kernels_cpu.c:242-253) over the whole x */
+    float tot = gq_wave_total(ss);
+    tot = tot / (float)a.cols;
+    tot = tot + a.eps;
+    rscale = 1.0f / sqrtf(tot);
+  }
+
+  /* group j is computed from buffer j % 3 after the loads of group j+2 are
+   * issued into the buffer group j-1 used */
+  auto step = [&](int j, RBuf<DT, TPW, RW> &cur, RBuf<DT, TPW, RW> &nxt2) {
+    rload<DT, MODE, TPW, RW>(a, pl, min(gw + (j + kRB - 1) * W, glast), nxt2, lane, part, bt, nb, pos);
+    if (j >= mygroups) return;
+    float acc[RW];
+#pragma unroll
+    for (int r = 0; r < RW; r++) acc[r] = 0.f;
+#pragma unroll
+    for (int ti = 0; ti < TPW; ti++) {
+      const int b = ti * BPT + bt;
+#pragma unroll
+      for (int r = 0; r < RW; r++) {
+        const float v = T::dot(cur.f[r][ti], xs[ti], part);
+        acc[r] += b < nb ? v : 0.f;
+      }
+    }
+    float tot[RW];
+#pragma unroll
+    for (int r = 0; r < RW; r++) tot[r] = gq_wave_total(acc[r]) * rscale;
+    /* lane r < P finishes output row r of the group */
+    float v = tot[0], w = MODE == MV_SWIGLU ? tot[P] : tot[1];
+#pragma unroll
+    for (int r = 1; r < P; r++)
+      if (lane == r) v = tot[r], w = MODE == MV_SWIGLU ? tot[P + r] : tot[r ^ 1];
+    float out;
+    {
+#pragma clang fp contract(off)
+      if (MODE == MV_SWIGLU) {
+        out = silu_mul(v, w);
+      } else if (MODE == MV_RESID) {
+        out = v + cur.res;
+      } else {
+        out = v;
+        int s, lr, n;
+        group_span<MODE, RW>(a, pl, gw + j * W, s, lr, n);
+        const int kind = a.seg[__builtin_amdgcn_readfirstlane(s)].kind;
+        if (a.rope.cs && (kind == SEG_ROPE || kind == SEG_ROPE_KV)) {
+          /* adjacent pair rotated by the row of pos (kernels_cpu.c:415-429);
+           * groups start on even rows */
+          const float x0 = (lane & 1) ? w : v, x1 = (lane & 1) ? v : w;
+          out = (lane & 1) ? x0 * cur.cs.y + x1 * cur.cs.x : x0 * cur.cs.x - x1 * cur.cs.y;
+        }
+      }
+    }
+    if (lane < P) obuf[j * P + lane] = out;
+  };
+  for (int j = 0; j < mygroups; j += kRB) {
+    step(j, B0, B2);
+    step(j + 1, B1, B0);
+    step(j + 2, B2, B1);
+  }
+  /* the parked rows go out; nothing is loaded from here on */
+  for (int j = 0; j < mygroups; j++) {
+    int s, lr, n;
+    group_span<MODE, RW>(a, pl, gw + j * W, s, lr, n);
+    s = __builtin_amdgcn_readfirstlane(s);
+    if (lane < n) {
+      float *dst = rdest<MODE>(a, s, lr + lane, pos);
+      if (dst) gst<float>(dst, obuf[j * P + lane]);
+    }
+  }
+}
+
+
 int g_n_cu = 256;
 int g_wg_per_cu = 4;
-int g_use_lds = 1;
+constexpr size_t kMaxDynLds = 144 * 1024;
+constexpr size_t kMaxDynLdsW = 152 * 1024;
+/* matvec kernels: 0 register path, 1 split-K LDS, 2 wave-private LDS ring,
+ * 3 register ring (each where it fits, falling back down the list), 4 auto */
+int g_use_lds = 4;
 
 template <int DT, int MODE, int R>
 int launch_r(const MvArgs &a, int total, hipStream_t s) {
@@ -787,7 +1321,7 @@ int launch_r(const MvArgs &a, int total, hipStream_t s) {
  * segments that a stage would straddle) so the caller uses mv_kernel. */
 template <int DT, int MODE>
 int launch_lds(const MvArgs &a, int total, hipStream_t s) {
-  using T = Tr<DT>;
+  using T = typename TrSplit<DT>::type;
   const int nb = a.cols / T::QK;
   const int rowbytes = nb * T::BB;
   if (rowbytes % 16) return 1;
@@ -798,7 +1332,7 @@ int launch_lds(const MvArgs &a, int total, hipStream_t s) {
   const int ts = (ntile + tpw - 1) / tpw;
   if (ts > kWaves) return 1;
   const int nteam = kWaves / ts;
-  int rs = min(32, kStageCap / rowbytes);
+  int rs = min(32, g_stage_cap / rowbytes);
   rs -= rs % (2 * nteam);
   /* with several segments a stage must not straddle two: rs divides them all */
   if (MODE != MV_SWIGLU && a.nseg > 1)
@@ -814,21 +1348,130 @@ int launch_lds(const MvArgs &a, int total, hipStream_t s) {
   pl.stride = (rs * rowbytes + 64 + 1023) / 1024 * 1024;
   const int per = MODE == MV_SWIGLU ? rs / 2 : rs;
   pl.ngroups = (total + per - 1) / per;
-  const size_t lds = (size_t)kStages * pl.stride;
-  const int per_cu = max(1, (int)(160 * 1024 / (lds + 2048)));
+  const size_t lds = (size_t)kNS * pl.stride;
+  if (lds > kMaxDynLds) return 1;
+  int per_cu = max(1, (int)(160 * 1024 / (lds + 8192)));
+  if (g_lds_wg_per_cu > 0) per_cu = min(per_cu, g_lds_wg_per_cu);
   const int grid = min(pl.ngroups, per_cu * g_n_cu);
+  /* rows per team per stage is even (rs is a multiple of 2 nteam) */
+  const int rw = (rs / nteam) % 4 == 0 ? 4 : 2;
   static bool attr_set = false;
   if (!attr_set) {
-    (void)hipFuncSetAttribute((const void *)mvl_kernel<DT, MODE, 1>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
-    (void)hipFuncSetAttribute((const void *)mvl_kernel<DT, MODE, 2>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
+    const void *fs[] = {(const void *)mvl_kernel<DT, MODE, 1, 2>, (const void *)mvl_kernel<DT, MODE, 2, 2>,
+                        (const void *)mvl_kernel<DT, MODE, 1, 4>, (const void *)mvl_kernel<DT, MODE, 2, 4>};
+    for (const void *f : fs) (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds);
     attr_set = true;
   }
-  if (tpw == 1)
-    hipLaunchKernelGGL((mvl_kernel<DT, MODE, 1>), dim3(grid), dim3(kThreads), lds, s, a, pl);
-  else
-    hipLaunchKernelGGL((mvl_kernel<DT, MODE, 2>), dim3(grid), dim3(kThreads), lds, s, a, pl);
+  const dim3 g(grid), b(kThreads);
+  if (rw == 2 && tpw == 1) hipLaunchKernelGGL((mvl_kernel<DT, MODE, 1, 2>), g, b, lds, s, a, pl);
+  if (rw == 2 && tpw == 2) hipLaunchKernelGGL((mvl_kernel<DT, MODE, 2, 2>), g, b, lds, s, a, pl);
+  if (rw == 4 && tpw == 1) hipLaunchKernelGGL((mvl_kernel<DT, MODE, 1, 4>), g, b, lds, s, a, pl);
+  if (rw == 4 && tpw == 2) hipLaunchKernelGGL((mvl_kernel<DT, MODE, 2, 4>), g, b, lds, s, a, pl);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+int g_mw_rw = 4;   /* rows per group of the wave-private kernel */
+int g_mw_waves = 0; /* waves per workgroup of the wave-private kernel (0: chosen per shape) */
+
+template <int DT, int MODE, int TPW>
+int launch_w_rw(int rw, const MvArgs &a, const MwPlan &pl, int grid, int nwv, size_t lds, hipStream_t s) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    const void *fs[] = {(const void *)mvw_kernel<DT, MODE, TPW, 2>, (const void *)mvw_kernel<DT, MODE, TPW, 4>};
+    for (const void *f : fs) (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLdsW);
+    attr_set = true;
+  }
+  const dim3 g(grid), b(nwv * GQ_WAVE);
+  if (rw == 4) hipLaunchKernelGGL((mvw_kernel<DT, MODE, TPW, 4>), g, b, lds, s, a, pl);
+  else hipLaunchKernelGGL((mvw_kernel<DT, MODE, TPW, 2>), g, b, lds, s, a, pl);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+/* Plan and launch the wave-private kernel; returns 1 when the shape does not
+ * fit it (more than two column tiles, rows not a multiple of 16 bytes,
+ * segments that a group would straddle, or too little LDS). */
+template <int DT, int MODE>
+int launch_w(const MvArgs &a, int total, hipStream_t s) {
+  using T = Tr<DT>;
+  const int nb = a.cols / T::QK;
+  const int rowbytes = nb * T::BB;
+  if (rowbytes % 16) return 1;
+  constexpr int BPT = GQ_WAVE / T::LPB;
+  const int ntile = (nb + BPT - 1) / BPT;
+  if (ntile > 2) return 1;
+  bool rope = false;
+  if (MODE == MV_STORE)
+    for (int i = 0; i < a.nseg; i++) rope = rope || a.seg[i].kind != SEG_PLAIN;
+  if (rope && a.rope.head_dim > 512) return 1; /* the kernel's RoPE row holds 256 pairs */
+  const int rw = g_mw_rw >= 4 ? 4 : 2; /* even: RoPE pairs rows (2i, 2i+1) inside a group */
+  if (MODE != MV_SWIGLU && a.nseg > 1)
+    for (int i = 0; i < a.nseg; i++)
+      if (a.seg[i].rows % rw) return 1;
+  MwPlan pl;
+  pl.rowbytes = rowbytes;
+  pl.total = total;
+  const int per = MODE == MV_SWIGLU ? rw / 2 : rw;
+  pl.ngroups = (total + per - 1) / per;
+  pl.slot = (rw * rowbytes + 64 + 255) / 256 * 256;
+  const int xneed = a.cols * 4 * (a.norm_w ? 2 : 1); /* staged in the last slot row */
+  /* waves per workgroup: 4 (or the override), as many ring slots as LDS
+   * holds (at most kMaxNS), the last slot row large enough for x */
+  int nwv = g_mw_waves > 0 ? std::min(g_mw_waves, kMaxWaves) : 4;
+  while (nwv < kMaxWaves && nwv * pl.slot < xneed) nwv *= 2;
+  const int ns = std::min(kMaxNS, (int)(kMaxDynLdsW / ((size_t)nwv * pl.slot)));
+  if (ns < 3 || nwv * pl.slot < xneed) return 1;
+  pl.ns = ns;
+  pl.x_off = (ns - 1) * nwv * pl.slot;
+  pl.nw_off = pl.x_off + a.cols * 4;
+  const size_t lds = (size_t)ns * nwv * pl.slot;
+  const int per_cu = std::max(1, (int)((160 * 1024) / (lds + 4096)));
+  const int grid = std::min((pl.ngroups + nwv - 1) / nwv, per_cu * g_n_cu);
+  if (ntile == 1) return launch_w_rw<DT, MODE, 1>(rw, a, pl, grid, nwv, lds, s);
+  return launch_w_rw<DT, MODE, 2>(rw, a, pl, grid, nwv, lds, s);
+}
+
+/* Plan and launch the register-ring kernel; returns 1 when the shape does
+ * not fit it (more than one column tile: the two-tile ring does not fit the
+ * register file; or segments a group would straddle). */
+template <int DT, int MODE>
+int launch_reg(const MvArgs &a, int total, hipStream_t s) {
+  using T = Tr<DT>;
+  const int nb = a.cols / T::QK;
+  constexpr int BPT = GQ_WAVE / T::LPB;
+  const int ntile = (nb + BPT - 1) / BPT;
+  if (ntile > 1) return 1;
+  /* 4 rows per group when that still gives every wave of a full grid work
+   * (and the loads of 3 groups fit the 63 outstanding loads), else 2 */
+  const int nw = 8;
+  const int per4 = MODE == MV_SWIGLU ? 2 : 4;
+  int rw = (total + per4 - 1) / per4 >= 2 * nw * g_n_cu ? 4 : 2;
+  if (g_mw_rw == 2) rw = 2;
+  if (MODE != MV_SWIGLU && a.nseg > 1)
+    for (int i = 0; i < a.nseg; i++)
+      if (a.seg[i].rows % rw) return 1;
+  MwPlan pl;
+  pl.rowbytes = nb * T::BB;
+  pl.total = total;
+  const int per = MODE == MV_SWIGLU ? rw / 2 : rw;
+  pl.ngroups = (total + per - 1) / per;
+  const int grid = std::min((pl.ngroups + nw - 1) / nw, g_n_cu);
+  const int mg = (pl.ngroups + grid * nw - 1) / (grid * nw); /* groups per wave, at most */
+  const int xb = (a.cols * 4 + 255) / 256 * 256;
+  pl.nw_off = xb;
+  pl.x_off = xb * (a.norm_w ? 2 : 1); /* parked outputs after x and the norm weight */
+  pl.slot = mg + 2;                    /* parked groups per wave (+ the unrolled tail) */
+  pl.ns = 0;
+  const size_t lds = (size_t)pl.x_off + (size_t)nw * pl.slot * per * 4;
+  if (lds > kMaxDynLdsW) return 1;
+  static bool attr_set = false;
+  if (!attr_set) {
+    const void *fs[] = {(const void *)mvr_kernel<DT, MODE, 1, 2>, (const void *)mvr_kernel<DT, MODE, 1, 4>};
+    for (const void *f : fs) (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLdsW);
+    attr_set = true;
+  }
+  const dim3 g(grid), b(nw * GQ_WAVE);
+  if (rw == 2) hipLaunchKernelGGL((mvr_kernel<DT, MODE, 1, 2>), g, b, lds, s, a, pl);
+  else hipLaunchKernelGGL((mvr_kernel<DT, MODE, 1, 4>), g, b, lds, s, a, pl);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
@@ -856,6 +1499,16 @@ int launch_dm(const MvArgs &a, hipStream_t s) {
         if (a.seg[i].rows % 4) return -1;
   }
   if (total <= 0) return -1;
+  if (g_use_lds == 3) {
+    const int rc = launch_reg<DT, MODE>(a, total, s);
+    if (rc <= 0) return rc;
+  }
+  /* auto: the wave-private ring for gate/up (measured fastest there), the
+   * split-K kernel for everything else */
+  if (g_use_lds == 2 || g_use_lds == 3 || (g_use_lds == 4 && MODE == MV_SWIGLU)) {
+    const int rc = launch_w<DT, MODE>(a, total, s);
+    if (rc <= 0) return rc;
+  }
   if (g_use_lds) {
     const int rc = launch_lds<DT, MODE>(a, total, s);
     if (rc <= 0) return rc;
@@ -884,12 +1537,21 @@ void gq_matvec_set_cus(int n_cu) {
    * persistent grid (0 = one workgroup per row group); default 4 */
   if (const char *e = getenv("GQ_MV_WG_PER_CU")) g_wg_per_cu = atoi(e);
   /* GQ_MV_LDS=0: register-path kernel only (same as gq_hip_set_matvec_path(0)) */
-  if (const char *e = getenv("GQ_MV_LDS")) g_use_lds = atoi(e) != 0;
+  if (const char *e = getenv("GQ_MV_LDS")) g_use_lds = std::min(std::max(atoi(e), 0), 4);
+  /* wave-private kernel: rows per group (GQ_MV_RW, 2 or 4) and waves per
+   * workgroup (GQ_MV_WAVES, 4..16; 0 = chosen per shape) */
+  if (const char *e = getenv("GQ_MV_RW")) g_mw_rw = atoi(e) >= 4 ? 4 : 2;
+  if (const char *e = getenv("GQ_MV_WAVES")) g_mw_waves = std::max(atoi(e), 0);
+  /* LDS-streamed kernel: bytes of weights per stage (GQ_MV_STAGE_BYTES, at
+   * most 40 KB) and workgroups per CU (GQ_MV_LDS_WG, 0 = as many as LDS
+   * allows) */
+  if (const char *e = getenv("GQ_MV_STAGE_BYTES")) g_stage_cap = std::min(std::max(atoi(e), 4096), 40960);
+  if (const char *e = getenv("GQ_MV_LDS_WG")) g_lds_wg_per_cu = std::max(atoi(e), 0);
 }
 
-extern "C" int gq_hip_set_matvec_path(int lds) {
+extern "C" int gq_hip_set_matvec_path(int path) {
   const int prev = g_use_lds;
-  g_use_lds = lds != 0;
+  if (path >= 0 && path <= 4) g_use_lds = path;
   return prev;
 }
 

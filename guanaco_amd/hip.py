@@ -91,12 +91,17 @@ def _load():
 lib, EXPORTS = _load()
 NCLASS = 6
 CLASS_NAMES = ("q4_k_matvec", "q6_k_matvec", "q8_0_matvec", "attention", "rope_append", "other")
-MATVEC_PATHS = ("register", "lds")
+MATVEC_PATHS = ("register", "lds", "wave", "ring", "auto")
 
 
 class matvec_path:
-    """Context manager selecting the matvec kernel ("lds": LDS-streamed where
-    the shape fits, the default; "register": register-path kernel only)."""
+    """Context manager selecting the matvec kernels: "auto" (default) the
+    wave-private LDS ring for gate/up launches and the split-K LDS kernel for
+    the rest; "ring" the register-ring kernel where a wave covers whole rows
+    in one column tile; "wave" the wave-private LDS-ring kernel where a wave
+    covers whole rows; "lds" the split-K LDS-streamed kernel; "register" the
+    register-path kernel only.  Each choice falls back down the list
+    ring -> wave -> lds -> register for shapes it does not fit."""
 
     def __init__(self, name):
         self.lds = MATVEC_PATHS.index(name)

@@ -197,11 +197,16 @@ int gq_hip_profile_step(gq_ctx *ctx, int token, int pos, double ms[GQ_NCLASS],
  * (to defeat the MALL) with per-buffer outputs. */
 float gq_hip_time_matvec(gq_ctx *ctx, int dtype, const void *const *w_devs, int n_w, int rows,
                          int cols, const float *x_dev, float *y_dev, int n_iter);
-/* Selects the matvec kernel for later launches in this process: 1 (default)
- * the LDS-streamed kernel where the shape fits it, 0 the register-path kernel
- * only.  Returns the previous setting.  No reference counterpart: a switch
- * for the parity tests (both kernels against the oracle) and for timing. */
-int gq_hip_set_matvec_path(int lds);
+/* Selects the matvec kernels for later launches in this process: 4 (default)
+ * auto: the wave-private LDS ring for gate/up launches, the split-K LDS
+ * kernel for the rest; 3 the register-ring kernel where a wave covers whole
+ * rows in one column tile; 2 the wave-private LDS-ring kernel where a wave
+ * covers whole rows; 1 the split-K LDS-streamed kernel; 0 the register-path
+ * kernel only.  Each setting falls back down 3 -> 2 -> 1 -> 0 for shapes it
+ * does not fit.  Returns the previous setting.  No reference counterpart: a
+ * switch for the parity tests (every kernel against the oracle) and for
+ * timing. */
+int gq_hip_set_matvec_path(int path);
 /* Device time of n launches of the attention kernels for one layer. */
 float gq_hip_time_attention(gq_ctx *ctx, int layer, int pos, const float *q_dev, float *out_dev,
                             int n_iter);
