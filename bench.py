@@ -7,9 +7,12 @@ KV cache are resident before the timed region.  Steps start at position
 8192 (warm-up steps are run from the same position first and overwritten).
 
 Prints ONE JSON line.  value = tokens/s over exactly --steps tokens between
-two device synchronisations.  roofline = the dominant kernel (the Q4_K
-matvec) measured live with HIP events around each launch of an eager step at
-the same position: algorithmic bytes / average launch time.  cpu_baseline =
+two device synchronisations.  roofline = the dominant kernel (the fused
+gate/up + SwiGLU matvec, mvw_kernel<Q4_K, MV_SWIGLU>): its algorithmic bytes
+per launch over its average duration, measured live with HIP events around
+64 back-to-back launches cycling over the 32 layers at the same position;
+traffic = its HBM bytes per launch from the committed rocprofv3 counter runs
+(profiles/mvw_gate_up_llama8b_hbm_traffic.md).  cpu_baseline =
 the reference's own CPU forward() (oracle/_ref/libref.so) timed on this
 host on a bounded sample, or the oracle port when the reference build is
 absent.
@@ -29,6 +32,24 @@ CTX = 8192
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "mvw_gate_up_llama8b_hbm_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the gate/up kernel, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE runs (scaled by a copy kernel of known
+    size; the file gives the commands), or None when that file is absent."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(spec, seconds=20.0, threads=8):
@@ -109,10 +130,18 @@ def main():
 
     # per-kernel-class device time of one eager step at the first timed position
     prof = dm.profile_step(start_tok, CTX)
-    q4 = prof["q4_k_matvec"]
-    avg_ms = q4["ms"] / max(q4["launches"], 1)
-    bytes_per_launch = q4["bytes"] / max(q4["launches"], 1)
+    # the dominant kernel: the fused gate/up + SwiGLU matvec (one launch per
+    # layer, mvw_kernel<Q4_K, MV_SWIGLU>); algorithmic bytes per launch =
+    # 2 x 14336 x 4096 Q4_K weights (144 B per 256) + x, norm weight, output
+    gu = prof["gate_up"]
+    bytes_per_launch = gu["bytes"] / max(gu["launches"], 1)
+    # its average launch duration: back-to-back launches over all 32 layers
+    # between two HIP events on the stream the kernels run on
+    op_ms = {op: round(dm.time_op(op, CTX, 64 if op != "lm_head" else 8), 5)
+             for op in H.CLASS_NAMES if op != "other"}
+    avg_ms = op_ms["gate_up"]
     achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9
+    log(f"back-to-back ms per launch: {json.dumps(op_ms)}")
     classes = {k: {"ms": round(v["ms"], 4), "launches": v["launches"],
                    "GB_per_s": round(v["bytes"] / max(v["ms"], 1e-9) / 1e6, 1)}
                for k, v in prof.items() if v["launches"]}
@@ -139,12 +168,14 @@ def main():
                    "model": spec.name, "global_batch": 1, "seq_len": CTX, "parallelism": "none (1 GPU)",
                    "max_seq": max_seq, "graph": not args.eager},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "mv_kernel<Q4_K> (all Q4_K projections of one token)",
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(),
+                     "kernel": "mvw_kernel<Q4_K, MV_SWIGLU> (gate/up + SwiGLU, one launch per layer)",
                      "avg_launch_ms": round(avg_ms, 5), "bytes_per_launch": int(bytes_per_launch)},
         "per_token": {"weight_bytes": weight_bytes, "kv_bytes_at_8192": kv_bytes,
                       "effective_GB_per_s": round((weight_bytes + kv_bytes) * tok_s / 1e9, 1),
-                      "eager_step_kernel_ms": round(step_ms, 4), "classes": classes},
+                      "eager_step_kernel_ms": round(step_ms, 4), "classes": classes,
+                      "op_ms_back_to_back": op_ms},
         "device": {"arch": arch, "cus": n_cu},
     }
     ctx.close()

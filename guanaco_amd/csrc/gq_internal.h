@@ -100,6 +100,7 @@ int gq_launch_argmax(const float *x, int n, float *scratch, int nblk, int *out_i
                      int *tokens, int *step_dev, int *pos_dev, hipStream_t s);
 int gq_argmax_blocks(int n);
 int gq_launch_silu_mul(float *gate, const float *up, int n, hipStream_t s);
+int gq_launch_copy(void *dst, const void *src, size_t bytes, int n_cu, hipStream_t s);
 int gq_launch_synth_quant(void *dev, int dtype, int rows, int cols, uint64_t seed, hipStream_t s);
 int gq_launch_synth_normal(float *dev, size_t n, uint64_t seed, int norm_weight, hipStream_t s);
 int gq_launch_synth_kv(float *slab, int n_layers, int n_kv, int hd, int max_seq, int n_pos,

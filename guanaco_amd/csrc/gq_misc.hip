@@ -3,6 +3,8 @@
  * greedy argmax (with the decode loop's device-side bookkeeping), SiLU*up,
  * and the device fills of the synthetic-input generator (gq_synth.h).
  */
+#include <algorithm>
+
 #include "gq_device.h"
 #include "gq_internal.h"
 #include "gq_synth.h"
@@ -127,6 +129,13 @@ __global__ void silu_mul_kernel(float *gate, const float *up, int n) {
   }
 }
 
+/* Plain 16-byte-per-thread grid-stride copy: the reference workload for
+ * scaling the HBM byte counters (n16 = bytes / 16). */
+__global__ __launch_bounds__(kThreads) void copy_kernel(const uint4 *src, uint4 *dst, size_t n16) {
+  for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < n16; i += (size_t)gridDim.x * kThreads)
+    gst<uint4>(dst + i, gld<uint4>(src + i));
+}
+
 /* ---- synthetic fills: one thread per 4 output bytes / one float ---- */
 __global__ void synth_quant_kernel(uint8_t *out, int dtype, size_t nbytes, int bb, uint64_t seed) {
   const size_t i4 = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
@@ -191,6 +200,16 @@ int gq_launch_argmax(const float *x, int n, float *scratch, int nblk, int *out_i
 
 int gq_launch_silu_mul(float *gate, const float *up, int n, hipStream_t s) {
   hipLaunchKernelGGL(silu_mul_kernel, dim3((n + 255) / 256), dim3(256), 0, s, gate, up, n);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+int gq_launch_copy(void *dst, const void *src, size_t bytes, int n_cu, hipStream_t s) {
+  if ((bytes & 15) || ((uintptr_t)dst & 15) || ((uintptr_t)src & 15)) return -1;
+  const size_t n16 = bytes / 16;
+  const size_t blocks = std::min((n16 + kThreads - 1) / kThreads, (size_t)n_cu * 8);
+  if (!blocks) return 0;
+  hipLaunchKernelGGL(copy_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, s, (const uint4 *)src, (uint4 *)dst,
+                     n16);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 

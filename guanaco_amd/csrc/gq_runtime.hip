@@ -93,7 +93,8 @@ static size_t block_bytes(int dtype, int *qk) {
   }
 }
 
-static int mv_class(int dtype) { return dtype == GQ_Q4_K ? 0 : dtype == GQ_Q6_K ? 1 : 2; }
+/* profile classes (gq_hip.h) */
+enum { PC_QKV = 0, PC_ATTN, PC_O, PC_GATE_UP, PC_DOWN, PC_LM_HEAD, PC_OTHER };
 
 /* ------------------------------------------------------------ lifecycle */
 extern "C" int gq_hip_device_count(void) {
@@ -623,83 +624,124 @@ static double mv_bytes(const gq_weight &w, int extra_vectors) {
   return (double)w.rows * (w.cols / qk) * bb + 4.0 * w.cols + 4.0 * w.rows * (1 + extra_vectors);
 }
 
-/* One decode layer; positions come from pos_dev when not NULL. */
-static int run_layer(gq_ctx *c, int l, int pos, const int *pos_dev, float *hidden) {
+/* The launches of one decode layer, op by op; positions come from pos_dev
+ * when not NULL. */
+/* q, k, v: one launch per distinct dtype, RMSNorm fused into the x staging;
+ * RoPE of q and k and the K/V cache append fused into the epilogue
+ * (engine.c:356-392 in one pass) */
+static int op_qkv(gq_ctx *c, int l, int pos, const int *pos_dev, float *hidden) {
   const gq_model &m = c->m;
   const gq_layer &L = c->layers[l];
-  Workspace &w = c->ws;
-  const int H = m.hidden, kvd = m.n_kv_heads * m.head_dim;
-  float *q = w.qkv, *k = w.qkv + H, *v = w.qkv + H + kvd;
-  int rc;
-  /* q, k, v: one launch per distinct dtype, RMSNorm fused into the x
-   * staging; RoPE of q and k and the K/V cache append fused into the
-   * epilogue (engine.c:356-392 in one pass) */
-  (void)k;
-  (void)v;
   const gq_weight *W[3] = {&L.wq, &L.wk, &L.wv};
-  float *Y[3] = {q, gq_hip_kv_k(c, l), gq_hip_kv_v(c, l)};
+  float *Y[3] = {c->ws.qkv, gq_hip_kv_k(c, l), gq_hip_kv_v(c, l)};
   const int kind[3] = {SEG_ROPE, SEG_ROPE_KV, SEG_KV};
   bool done[3] = {false, false, false};
   for (int i = 0; i < 3; i++) {
     if (done[i]) continue;
     MvArgs a{};
-    a.cols = H, a.x = hidden, a.norm_w = L.rms_att, a.eps = m.rms_eps;
+    a.cols = m.hidden, a.x = hidden, a.norm_w = L.rms_att, a.eps = m.rms_eps;
     a.rope = MvRope{c->rope, pos_dev, pos, m.head_dim, c->kv_max_seq};
-    double bytes = 4.0 * H;
+    double bytes = 4.0 * m.hidden;
     for (int j = i; j < 3; j++)
       if (!done[j] && W[j]->dtype == W[i]->dtype) {
         a.seg[a.nseg++] = MvSeg{(const uint8_t *)W[j]->data, Y[j], nullptr, W[j]->rows, kind[j]};
-        bytes += mv_bytes(*W[j], 0) - 4.0 * H;
+        bytes += mv_bytes(*W[j], 0) - 4.0 * m.hidden;
         done[j] = true;
       }
-    if ((rc = gq_launch_matvec(W[i]->dtype, MV_STORE, a, c->stream))) return rc;
-    mark(c, mv_class(W[i]->dtype), bytes);
+    const int rc = gq_launch_matvec(W[i]->dtype, MV_STORE, a, c->stream);
+    if (rc) return rc;
+    mark(c, PC_QKV, bytes);
   }
+  return 0;
+}
+
+static int op_attention(gq_ctx *c, int l, int pos, const int *pos_dev) {
+  const gq_model &m = c->m;
+  Workspace &w = c->ws;
+  const int kvd = m.n_kv_heads * m.head_dim;
   AttnArgs aa{};
-  aa.q = q, aa.k = gq_hip_kv_k(c, l), aa.v = gq_hip_kv_v(c, l);
+  aa.q = w.qkv, aa.k = gq_hip_kv_k(c, l), aa.v = gq_hip_kv_v(c, l);
   aa.part_o = w.part_o, aa.part_ml = w.part_ml, aa.out = w.attn;
   aa.pos_dev = pos_dev, aa.pos = pos;
   aa.n_heads = m.n_heads, aa.n_kv = m.n_kv_heads, aa.hd = m.head_dim, aa.max_seq = c->kv_max_seq;
   aa.nch = w.nch, aa.s_max = w.s_max, aa.scale = 1.0f / sqrtf((float)m.head_dim);
-  if ((rc = gq_launch_attention(aa, c->stream, nullptr))) return rc;
-  mark(c, 3, 2.0 * 4.0 * kvd * (double)(std::min(pos + 1, c->kv_max_seq)) + 8.0 * H);
-  /* o-proj + residual (in place on hidden) */
-  {
-    MvArgs a{};
-    a.seg[0] = MvSeg{(const uint8_t *)L.wo.data, hidden, hidden, L.wo.rows};
-    a.nseg = 1, a.cols = L.wo.cols, a.x = w.attn;
-    if ((rc = gq_launch_matvec(L.wo.dtype, MV_RESID, a, c->stream))) return rc;
-    mark(c, mv_class(L.wo.dtype), mv_bytes(L.wo, 1));
-  }
-  /* gate/up + SwiGLU, RMSNorm fused */
+  const int rc = gq_launch_attention(aa, c->stream, nullptr);
+  if (rc) return rc;
+  mark(c, PC_ATTN, 2.0 * 4.0 * kvd * (double)(std::min(pos + 1, c->kv_max_seq)) + 8.0 * m.hidden);
+  return 0;
+}
+
+/* o-proj + residual (in place on hidden) */
+static int op_o(gq_ctx *c, int l, float *hidden) {
+  const gq_layer &L = c->layers[l];
+  MvArgs a{};
+  a.seg[0] = MvSeg{(const uint8_t *)L.wo.data, hidden, hidden, L.wo.rows};
+  a.nseg = 1, a.cols = L.wo.cols, a.x = c->ws.attn;
+  const int rc = gq_launch_matvec(L.wo.dtype, MV_RESID, a, c->stream);
+  if (rc) return rc;
+  mark(c, PC_O, mv_bytes(L.wo, 1));
+  return 0;
+}
+
+/* gate/up + SwiGLU, RMSNorm fused */
+static int op_gate_up(gq_ctx *c, int l, float *hidden) {
+  const gq_model &m = c->m;
+  const gq_layer &L = c->layers[l];
+  Workspace &w = c->ws;
+  int rc;
   if (L.w_gate.dtype == L.w_up.dtype) {
     MvArgs a{};
     a.seg[0] = MvSeg{(const uint8_t *)L.w_gate.data, w.act, nullptr, L.w_gate.rows};
     a.seg[1] = MvSeg{(const uint8_t *)L.w_up.data, nullptr, nullptr, L.w_up.rows};
-    a.nseg = 2, a.cols = H, a.x = hidden, a.norm_w = L.rms_ffn, a.eps = m.rms_eps;
+    a.nseg = 2, a.cols = m.hidden, a.x = hidden, a.norm_w = L.rms_ffn, a.eps = m.rms_eps;
     if ((rc = gq_launch_matvec(L.w_gate.dtype, MV_SWIGLU, a, c->stream))) return rc;
-    mark(c, mv_class(L.w_gate.dtype), mv_bytes(L.w_gate, 0) + mv_bytes(L.w_up, 0) - 4.0 * H - 4.0 * m.ff);
-  } else {
-    for (int i = 0; i < 2; i++) {
-      const gq_weight &g = i ? L.w_up : L.w_gate;
-      MvArgs a{};
-      a.seg[0] = MvSeg{(const uint8_t *)g.data, i ? w.act2 : w.act, nullptr, g.rows};
-      a.nseg = 1, a.cols = H, a.x = hidden, a.norm_w = L.rms_ffn, a.eps = m.rms_eps;
-      if ((rc = gq_launch_matvec(g.dtype, MV_STORE, a, c->stream))) return rc;
-      mark(c, mv_class(g.dtype), mv_bytes(g, 0));
-    }
-    if ((rc = gq_launch_silu_mul(w.act, w.act2, m.ff, c->stream))) return rc;
-    mark(c, 5, 12.0 * m.ff);
+    mark(c, PC_GATE_UP, mv_bytes(L.w_gate, 0) + mv_bytes(L.w_up, 0) - 4.0 * m.hidden - 4.0 * m.ff);
+    return 0;
   }
-  /* down + residual (in place on hidden) */
-  {
+  for (int i = 0; i < 2; i++) {
+    const gq_weight &g = i ? L.w_up : L.w_gate;
     MvArgs a{};
-    a.seg[0] = MvSeg{(const uint8_t *)L.w_down.data, hidden, hidden, L.w_down.rows};
-    a.nseg = 1, a.cols = L.w_down.cols, a.x = w.act;
-    if ((rc = gq_launch_matvec(L.w_down.dtype, MV_RESID, a, c->stream))) return rc;
-    mark(c, mv_class(L.w_down.dtype), mv_bytes(L.w_down, 1));
+    a.seg[0] = MvSeg{(const uint8_t *)g.data, i ? w.act2 : w.act, nullptr, g.rows};
+    a.nseg = 1, a.cols = m.hidden, a.x = hidden, a.norm_w = L.rms_ffn, a.eps = m.rms_eps;
+    if ((rc = gq_launch_matvec(g.dtype, MV_STORE, a, c->stream))) return rc;
+    mark(c, PC_GATE_UP, mv_bytes(g, 0));
   }
+  if ((rc = gq_launch_silu_mul(w.act, w.act2, m.ff, c->stream))) return rc;
+  mark(c, PC_GATE_UP, 12.0 * m.ff);
   return 0;
+}
+
+/* down + residual (in place on hidden) */
+static int op_down(gq_ctx *c, int l, float *hidden) {
+  const gq_layer &L = c->layers[l];
+  MvArgs a{};
+  a.seg[0] = MvSeg{(const uint8_t *)L.w_down.data, hidden, hidden, L.w_down.rows};
+  a.nseg = 1, a.cols = L.w_down.cols, a.x = c->ws.act;
+  const int rc = gq_launch_matvec(L.w_down.dtype, MV_RESID, a, c->stream);
+  if (rc) return rc;
+  mark(c, PC_DOWN, mv_bytes(L.w_down, 1));
+  return 0;
+}
+
+/* final RMSNorm fused into the LM head */
+static int op_lm_head(gq_ctx *c, float *hidden) {
+  const gq_model &m = c->m;
+  MvArgs a{};
+  a.seg[0] = MvSeg{(const uint8_t *)m.lm_head.data, c->ws.logits, nullptr, m.lm_head.rows};
+  a.nseg = 1, a.cols = m.hidden, a.x = hidden, a.norm_w = m.rms_final, a.eps = m.rms_eps;
+  const int rc = gq_launch_matvec(m.lm_head.dtype, MV_STORE, a, c->stream);
+  if (rc) return rc;
+  mark(c, PC_LM_HEAD, mv_bytes(m.lm_head, 0));
+  return 0;
+}
+
+static int run_layer(gq_ctx *c, int l, int pos, const int *pos_dev, float *hidden) {
+  int rc;
+  if ((rc = op_qkv(c, l, pos, pos_dev, hidden))) return rc;
+  if ((rc = op_attention(c, l, pos, pos_dev))) return rc;
+  if ((rc = op_o(c, l, hidden))) return rc;
+  if ((rc = op_gate_up(c, l, hidden))) return rc;
+  return op_down(c, l, hidden);
 }
 
 /* embedding -> layers -> final RMSNorm + LM head -> argmax.  Eager form
@@ -712,23 +754,19 @@ static int run_step(gq_ctx *c, int token, int pos, bool device_state, float *hid
   const int *pos_dev = device_state ? w.d_pos : nullptr;
   if ((rc = gq_launch_embed(m.embed.dtype, m.embed.data, m.hidden, tok_dev, token, w.hidden, c->stream)))
     return rc;
-  mark(c, 5, 4.0 * m.hidden);
+  mark(c, PC_OTHER, 4.0 * m.hidden);
   for (int l = 0; l < m.n_layers; l++) {
     if ((rc = run_layer(c, l, pos, pos_dev, w.hidden))) return rc;
     if (hidden_per_layer)
       HIPCHK(c, hipMemcpyAsync(hidden_per_layer + (size_t)l * m.hidden, w.hidden, sizeof(float) * m.hidden,
                                hipMemcpyDeviceToHost, c->stream));
   }
-  MvArgs a{};
-  a.seg[0] = MvSeg{(const uint8_t *)m.lm_head.data, w.logits, nullptr, m.lm_head.rows};
-  a.nseg = 1, a.cols = m.hidden, a.x = w.hidden, a.norm_w = m.rms_final, a.eps = m.rms_eps;
-  if ((rc = gq_launch_matvec(m.lm_head.dtype, MV_STORE, a, c->stream))) return rc;
-  mark(c, mv_class(m.lm_head.dtype), mv_bytes(m.lm_head, 0));
+  if ((rc = op_lm_head(c, w.hidden))) return rc;
   if ((rc = gq_launch_argmax(w.logits, m.vocab, w.amax, w.amax_blocks, w.d_token,
                              device_state ? w.d_tokens : nullptr, device_state ? w.d_step : nullptr,
                              device_state ? w.d_pos : nullptr, c->stream)))
     return rc;
-  mark(c, 5, 4.0 * m.vocab);
+  mark(c, PC_OTHER, 4.0 * m.vocab);
   return 0;
 }
 
@@ -873,6 +911,35 @@ extern "C" int gq_hip_profile_step(gq_ctx *c, int token, int pos, double ms[GQ_N
   return 0;
 }
 
+extern "C" float gq_hip_time_op(gq_ctx *c, int op, int pos, int n_iter) {
+  if (!c || n_iter <= 0 || op < 0 || op > PC_LM_HEAD) return -1.f;
+  if (check_pos(c, pos, 1)) return -1.f;
+  hipEvent_t e0, e1;
+  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return -1.f;
+  float *h = c->ws.hidden;
+  int rc = 0;
+  (void)hipEventRecord(e0, c->stream);
+  for (int i = 0; i < n_iter && !rc; i++) {
+    const int l = i % c->m.n_layers; /* every layer's weights: no cache reuse */
+    switch (op) {
+    case PC_QKV: rc = op_qkv(c, l, pos, nullptr, h); break;
+    case PC_ATTN: rc = op_attention(c, l, pos, nullptr); break;
+    case PC_O: rc = op_o(c, l, h); break;
+    case PC_GATE_UP: rc = op_gate_up(c, l, h); break;
+    case PC_DOWN: rc = op_down(c, l, h); break;
+    default: rc = op_lm_head(c, h); break;
+    }
+  }
+  (void)hipEventRecord(e1, c->stream);
+  (void)hipEventSynchronize(e1);
+  float t = 0.f;
+  (void)hipEventElapsedTime(&t, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (rc) return fail(c, rc, "time_op launch failed"), -1.f;
+  return t / n_iter;
+}
+
 extern "C" float gq_hip_time_matvec(gq_ctx *c, int dtype, const void *const *w_devs, int n_w, int rows,
                                     int cols, const float *x, float *y, int n_iter) {
   if (!c || !w_devs || n_w <= 0 || n_iter <= 0) return -1.f;
@@ -1009,6 +1076,12 @@ extern "C" int gq_hip_argmax_dev(gq_ctx *c, const float *x, int n, int *out_inde
   (void)hipStreamSynchronize(c->stream);
   gq_hip_free(c, scratch);
   return rc ? fail(c, rc, "argmax") : 0;
+}
+
+extern "C" int gq_hip_copy_dev(gq_ctx *c, void *dst, const void *src, size_t bytes) {
+  if (!c || !dst || !src) return -1;
+  const int rc = gq_launch_copy(dst, src, bytes, c->n_cu, c->stream);
+  return rc ? fail(c, rc, "copy: sizes and pointers must be multiples of 16 bytes") : 0;
 }
 
 extern "C" int gq_hip_silu_mul_dev(gq_ctx *c, float *gate, const float *up, int n) {

@@ -72,6 +72,7 @@ def _load():
         "gq_hip_time_matvec": (C.c_float, [_vp, C.c_int, C.POINTER(_vp), C.c_int, C.c_int,
                                            C.c_int, _vp, _vp, C.c_int]),
         "gq_hip_set_matvec_path": (C.c_int, [C.c_int]),
+        "gq_hip_time_op": (C.c_float, [_vp, C.c_int, C.c_int, C.c_int]),
         "gq_hip_time_attention": (C.c_float, [_vp, C.c_int, C.c_int, _vp, _vp, C.c_int]),
         "gq_hip_rmsnorm_dev": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, C.c_float]),
         "gq_hip_rope_append_dev": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp]),
@@ -80,6 +81,7 @@ def _load():
         "gq_hip_embed_dev": (C.c_int, [_vp, C.c_int, _vp, C.c_int, C.c_int, _vp]),
         "gq_hip_argmax_dev": (C.c_int, [_vp, _vp, C.c_int, _vp]),
         "gq_hip_silu_mul_dev": (C.c_int, [_vp, _vp, _vp, C.c_int]),
+        "gq_hip_copy_dev": (C.c_int, [_vp, _vp, _vp, C.c_size_t]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -89,8 +91,8 @@ def _load():
 
 
 lib, EXPORTS = _load()
-NCLASS = 6
-CLASS_NAMES = ("q4_k_matvec", "q6_k_matvec", "q8_0_matvec", "attention", "rope_append", "other")
+NCLASS = 7
+CLASS_NAMES = ("qkv", "attention", "o_proj", "gate_up", "down", "lm_head", "other")
 MATVEC_PATHS = ("register", "lds", "wave", "ring", "auto")
 
 
@@ -387,6 +389,14 @@ class DeviceModel:
                                               out.ctypes.data_as(C.POINTER(C.c_int32)), C.byref(ms)),
                        "decode_loop")
         return out, ms.value
+
+    def time_op(self, op, pos, n_iter=64):
+        """Average ms of one op (a CLASS_NAMES entry other than "other")
+        launched n_iter times back to back over the layers."""
+        ms = lib.gq_hip_time_op(self.ctx.h, CLASS_NAMES.index(op), pos, n_iter)
+        if ms < 0:
+            self.ctx.raise_last("time_op")
+        return float(ms)
 
     def profile_step(self, token, pos):
         ms = (C.c_double * NCLASS)()

@@ -184,14 +184,22 @@ int gq_hip_decode_loop(gq_ctx *ctx, int token, int pos, int n_steps, int use_gra
                        int32_t *tokens_out, float *ms);
 
 /* ------------------------------------------------------- measurement
- * Runs one eager decode step with HIP events around every kernel launch and
- * accumulates per-kernel-class device time and launch counts.  Classes:
- * 0 Q4_K matvec, 1 Q6_K matvec, 2 Q8_0 matvec, 3 attention (partial+merge),
- * 4 RoPE+append, 5 other (embedding, argmax).  Per-class algorithmic bytes
- * are accumulated in bytes[]. */
-#define GQ_NCLASS 6
+ * Runs one eager decode step with HIP events after every kernel launch and
+ * accumulates per-class device time and launch counts.  Classes by role:
+ * 0 q/k/v projections (RMSNorm, RoPE and K/V append fused), 1 attention
+ * (partial + merge), 2 o-projection + residual, 3 gate/up + SwiGLU, 4 down
+ * projection + residual, 5 final RMSNorm + LM head, 6 other (embedding,
+ * argmax).  Per-class algorithmic bytes (weights, activations in and out,
+ * KV read) are accumulated in bytes[]. */
+#define GQ_NCLASS 7
 int gq_hip_profile_step(gq_ctx *ctx, int token, int pos, double ms[GQ_NCLASS],
                         int launches[GQ_NCLASS], double bytes[GQ_NCLASS]);
+/* Average device time (ms) of one op (a GQ_NCLASS class index 0..5) of the
+ * bound model, launched n_iter times back to back on the context stream
+ * (layer i % n_layers for launch i, so no two consecutive launches share
+ * weights) between two HIP events.  The ops write their usual outputs (the
+ * q/k/v op appends K/V at pos; o and down add into the hidden state). */
+float gq_hip_time_op(gq_ctx *ctx, int op, int pos, int n_iter);
 /* Average device time (ms) of n back-to-back launches of one matvec, timed
  * with HIP events on the context stream; rotating over n_w weight buffers
  * (to defeat the MALL) with per-buffer outputs. */
@@ -234,6 +242,10 @@ int gq_hip_embed_dev(gq_ctx *ctx, int dtype, const void *table, int hidden, int 
                      float *out);
 int gq_hip_argmax_dev(gq_ctx *ctx, const float *x, int n, int *out_index_dev);
 int gq_hip_silu_mul_dev(gq_ctx *ctx, float *gate, const float *up, int n);
+/* Device-to-device copy by a plain streaming kernel (bytes and both pointers
+ * multiples of 16), asynchronous.  No reference counterpart: the known-size
+ * workload that scales the HBM byte counters of the profiles. */
+int gq_hip_copy_dev(gq_ctx *ctx, void *dst, const void *src, size_t bytes);
 
 #ifdef __cplusplus
 }

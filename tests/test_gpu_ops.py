@@ -134,3 +134,15 @@ def test_silu_mul(ctx, orc):
     gg = g.copy()
     orc.lib.orc_silu(fptr(gg), n)
     assert rel_l2(gb.download(), gg * u) < 1e-6
+
+
+def test_copy_kernel(ctx):
+    """gq_hip_copy_dev: the plain copy used to scale the HBM byte counters."""
+    import guanaco_amd.hip as H
+    n = (3 << 20) + 48
+    src = ctx.upload(np.arange(n // 4, dtype=np.float32))
+    dst = ctx.alloc(n)
+    assert H.lib.gq_hip_copy_dev(ctx.h, dst.ptr, src.ptr, n) == 0
+    assert np.array_equal(dst.download(count=n // 4), np.arange(n // 4, dtype=np.float32))
+    assert H.lib.gq_hip_copy_dev(ctx.h, dst.ptr, src.ptr, 8) == -1  # not a multiple of 16
+    src.free(), dst.free()
