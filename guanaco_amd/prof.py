@@ -5,13 +5,30 @@
         the reference that scales the FETCH_SIZE / WRITE_SIZE counters into
         HBM bytes (expected per dispatch: mib MiB read and mib MiB written).
 
+    python3 -m guanaco_amd.prof configs
+        the benchmark configs other than the headline one, with synthetic
+        inputs generated on the device: (1) one Q4_K 4096x4096 matvec
+        rotating over 48 matrices (> the 256 MB MALL); (2) TinyLlama-shape
+        greedy decode, 128 steps from a 512-position KV prefix; (4) split-K
+        attention per layer at 8192 / 16384 / 32768 positions on the 8B shape
+        (cycling over the 32 layers' caches) and a .lctx restore of a
+        4096-token prefix (1 GiB of K/V) from pinned host memory.  Prints one
+        JSON line per result.
+
 The decode workload itself is ``python3 bench.py --eager`` (one kernel launch
 per op, so per-dispatch counters map onto ops).
 """
 import argparse
+import ctypes as C
+import json
+import os
+import tempfile
 import time
 
+import numpy as np
+
 from . import hip as H
+from . import spec as S
 
 
 def run_copy(mib, iters):
@@ -30,15 +47,119 @@ def run_copy(mib, iters):
     ctx.close()
 
 
+def emit(**kw):
+    print(json.dumps(kw), flush=True)
+
+
+def config1(ctx, nbuf=48, iters=96):
+    rows = cols = 4096
+    bufs = [ctx.synth_quant(S.Q4_K, rows, cols, 1000 + i) for i in range(nbuf)]
+    x = ctx.synth_normal(cols, 5)
+    y = ctx.alloc(4 * rows * nbuf)
+    arr = (C.c_void_p * nbuf)(*[b.ptr for b in bufs])
+    H.lib.gq_hip_time_matvec(ctx.h, S.Q4_K, arr, nbuf, rows, cols, x.ptr, y.ptr, 8)
+    ms = H.lib.gq_hip_time_matvec(ctx.h, S.Q4_K, arr, nbuf, rows, cols, x.ptr, y.ptr, iters)
+    alg = S.qbytes(S.Q4_K, rows, cols) + 4 * rows + 4 * cols
+    emit(config=1, what="Q4_K matvec 4096x4096, 48 rotating matrices", us_per_launch=round(ms * 1e3, 2),
+         algorithmic_bytes=alg, GB_per_s=round(alg / ms / 1e6, 1))
+    for b in bufs:
+        b.free()
+    x.free(), y.free()
+
+
+def config2(ctx):
+    spec, pre, n = S.TINYLLAMA, 512, 128
+    dm = H.DeviceModel(ctx, spec, 640, prefill=pre)
+    ctx.sync()
+    dm.decode_loop(1, pre, 8, use_graph=True)
+    ctx.sync()
+    t0 = time.perf_counter()
+    toks, dev_ms = dm.decode_loop(1, pre, n, use_graph=True)
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    emit(config=2, what="TinyLlama-shape greedy decode, 128 steps from pos 512 (graph replay)",
+         tok_per_s=round(n / wall, 1), ref_definition_tok_per_s=round((n - 1) / wall, 1),
+         ms_per_token=round(wall * 1e3 / n, 4), weight_bytes_per_token=spec.weight_bytes_per_token(),
+         first_tokens=[int(t) for t in toks[:8]])
+
+
+def config4(ctx):
+    spec = S.LLAMA8B
+    top = 32768
+    dm = H.DeviceModel(ctx, spec, top + 64, prefill=top)
+    ctx.sync()
+    q = ctx.synth_normal(spec.n_heads * spec.head_dim, 3)
+    out = ctx.alloc(4 * spec.n_heads * spec.head_dim)
+    for L in (8192, 16384, 32768):
+        H.lib.gq_hip_time_attention(ctx.h, 0, L - 1, q.ptr, out.ptr, 8)
+        ms = H.lib.gq_hip_time_attention(ctx.h, 0, L - 1, q.ptr, out.ptr, 64)
+        alg = 2 * spec.n_kv_heads * L * spec.head_dim * 4
+        emit(config=4, what=f"split-K GQA attention per layer, {L} positions (partial + merge)",
+             us_per_layer=round(ms * 1e3, 2), kv_bytes=alg, GB_per_s=round(alg / ms / 1e6, 1))
+    q.free(), out.free()
+
+
+def config4_restore():
+    ctx = H.Context(0)
+    L, nkv, hd, ms_ = 32, 8, 128, 4096
+    ctx.kv_init(L, nkv, hd, ms_, 500000.0)
+    ctx.kv_prefill_synth(11, 12, ms_)
+    before = [ctx.kv_read_layer(l) for l in (0, L - 1)]
+    fd, path = tempfile.mkstemp(suffix=".lctx")
+    os.close(fd)
+    try:
+        ctx.check(ctx.lctx_save(path, ms_), "lctx_save")
+        size = os.path.getsize(path)
+        img = H.lib.gq_hip_host_alloc_pinned(size)
+        if not img:
+            raise H.HipError("pinned allocation failed")
+        with open(path, "rb") as f:
+            f.readinto((C.c_char * size).from_address(img))
+        ctx.kv_prefill_synth(99, 98, ms_)  # overwrite the cache before restoring
+        times = []
+        for _ in range(3):
+            rc, pos, ms = ctx.lctx_restore_image(img, size)
+            ctx.check(rc, "lctx_restore_image")
+            times.append(ms)
+        after = [ctx.kv_read_layer(l) for l in (0, L - 1)]
+        exact = all(np.array_equal(a[i].view(np.uint32), b[i].view(np.uint32))
+                    for a, b in zip(before, after) for i in (0, 1))
+        kv_bytes = 2 * L * nkv * ms_ * hd * 4
+        best = min(times)
+        emit(config=4, what=".lctx restore, 4096-token prefix (max_seq 4096) from pinned host memory",
+             file_bytes=size, kv_bytes=kv_bytes, ms=round(best, 3), GB_per_s=round(kv_bytes / best / 1e6, 1),
+             bit_exact_layers_0_and_31=exact, restored_pos=pos)
+        H.lib.gq_hip_host_free_pinned(img)
+    finally:
+        os.unlink(path)
+        ctx.close()
+
+
+def run_configs():
+    ctx = H.Context(0)
+    config1(ctx)
+    ctx.close()
+    ctx = H.Context(0)
+    config2(ctx)
+    ctx.close()
+    ctx = H.Context(0)
+    config4(ctx)
+    ctx.close()
+    config4_restore()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     sub = ap.add_subparsers(dest="cmd", required=True)
     c = sub.add_parser("copy")
     c.add_argument("--mib", type=int, default=256)
     c.add_argument("--iters", type=int, default=20)
+    sub.add_parser("configs")
     a = ap.parse_args()
     if a.cmd == "copy":
         run_copy(a.mib, a.iters)
+    elif a.cmd == "configs":
+        run_configs()
 
 
 if __name__ == "__main__":
