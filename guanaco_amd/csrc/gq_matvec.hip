@@ -951,6 +951,7 @@ struct MwPlan {
   int rowbytes;
   int slot;     /* LDS bytes per ring slot */
   int ns;       /* ring slots per wave */
+  int pre;      /* groups issued before x is waited for */
   int x_off;    /* LDS offset of staged x (the last slot row) */
   int nw_off;   /* LDS offset of the staged norm weight */
   int total;    /* output rows */
@@ -1035,8 +1036,12 @@ __global__ __launch_bounds__(kMaxWaves * GQ_WAVE) void mvw_kernel(MvArgs a, MwPl
         if (lane < hd - o) dma4(crow + o + lane, __builtin_amdgcn_readfirstlane(base + 4u * o));
     }
   }
+  /* pl.pre of the first ns-1 groups go out before x is waited for, the rest
+   * after x is in registers (x queues behind whatever is issued before it
+   * across the whole device) */
   int pend = 0; /* this wave's DMA instructions of the groups after the current one */
-  for (int k = 0; k < ns - 1 && k < mygroups; k++) {
+  const int npre = min(min(pl.pre, ns - 1), mygroups);
+  for (int k = 0; k < npre; k++) {
     issue_group<MODE, RW>(a, pl, gw + k * W, ring + k * row, rr + 4 * k, lane);
     pend += group_count<MODE, RW>(a, pl, gw + k * W);
   }
@@ -1067,6 +1072,10 @@ __global__ __launch_bounds__(kMaxWaves * GQ_WAVE) void mvw_kernel(MvArgs a, MwPl
   for (int i = 0; i < TPW; i++)
     T::load_x(xs[i], lds + pl.x_off, a.norm_w ? lds + pl.nw_off : nullptr, min(i * BPT + bt, nb - 1), part);
   __syncthreads(); /* the last slot row is free from here on */
+  for (int k = npre; k < ns - 1 && k < mygroups; k++) {
+    issue_group<MODE, RW>(a, pl, gw + k * W, ring + k * row, rr + 4 * k, lane);
+    pend += group_count<MODE, RW>(a, pl, gw + k * W);
+  }
 
   int slot = 0; /* j % ns */
   for (int j = 0; j < mygroups; j++) {
@@ -1372,6 +1381,7 @@ int launch_lds(const MvArgs &a, int total, hipStream_t s) {
 
 int g_mw_rw = 4;   /* rows per group of the wave-private kernel */
 int g_mw_waves = 0; /* waves per workgroup of the wave-private kernel (0: chosen per shape) */
+int g_mw_pre = -1;  /* groups issued before x is waited for (-1: all ns-1) */
 
 template <int DT, int MODE, int TPW>
 int launch_w_rw(int rw, const MvArgs &a, const MwPlan &pl, int grid, int nwv, size_t lds, hipStream_t s) {
@@ -1421,6 +1431,7 @@ int launch_w(const MvArgs &a, int total, hipStream_t s) {
   const int ns = std::min(kMaxNS, (int)(kMaxDynLdsW / ((size_t)nwv * pl.slot)));
   if (ns < 3 || nwv * pl.slot < xneed) return 1;
   pl.ns = ns;
+  pl.pre = g_mw_pre < 0 ? ns - 1 : g_mw_pre;
   pl.x_off = (ns - 1) * nwv * pl.slot;
   pl.nw_off = pl.x_off + a.cols * 4;
   const size_t lds = (size_t)ns * nwv * pl.slot;
@@ -1460,7 +1471,7 @@ int launch_reg(const MvArgs &a, int total, hipStream_t s) {
   pl.nw_off = xb;
   pl.x_off = xb * (a.norm_w ? 2 : 1); /* parked outputs after x and the norm weight */
   pl.slot = mg + 2;                    /* parked groups per wave (+ the unrolled tail) */
-  pl.ns = 0;
+  pl.ns = 0, pl.pre = 0;
   const size_t lds = (size_t)pl.x_off + (size_t)nw * pl.slot * per * 4;
   if (lds > kMaxDynLdsW) return 1;
   static bool attr_set = false;
@@ -1542,6 +1553,8 @@ void gq_matvec_set_cus(int n_cu) {
    * workgroup (GQ_MV_WAVES, 4..16; 0 = chosen per shape) */
   if (const char *e = getenv("GQ_MV_RW")) g_mw_rw = atoi(e) >= 4 ? 4 : 2;
   if (const char *e = getenv("GQ_MV_WAVES")) g_mw_waves = std::max(atoi(e), 0);
+  /* GQ_MV_XPRE: groups each wave issues before x is waited for (-1 = all) */
+  if (const char *e = getenv("GQ_MV_XPRE")) g_mw_pre = atoi(e);
   /* LDS-streamed kernel: bytes of weights per stage (GQ_MV_STAGE_BYTES, at
    * most 40 KB) and workgroups per CU (GQ_MV_LDS_WG, 0 = as many as LDS
    * allows) */
