@@ -101,6 +101,13 @@ int gq_launch_argmax(const float *x, int n, float *scratch, int nblk, int *out_i
 int gq_argmax_blocks(int n);
 int gq_launch_silu_mul(float *gate, const float *up, int n, hipStream_t s);
 int gq_launch_copy(void *dst, const void *src, size_t bytes, int n_cu, hipStream_t s);
+
+/* ---- prefill chunk ---------------------------------------------------
+ * Y[T][N] = X[T][K] . W^T on the bf16 matrix cores (W: N rows of Q4_K,
+ * X fp32 row-major); MV_STORE or MV_RESID (Y = R + X W^T, R may alias Y).
+ * Needs N % 128 == 0 and K % 256 == 0. */
+int gq_launch_prefill_gemm(int mode, const float *X, const void *W, float *Y, const float *R, int T, int N, int K,
+                           hipStream_t s);
 int gq_launch_synth_quant(void *dev, int dtype, int rows, int cols, uint64_t seed, hipStream_t s);
 int gq_launch_synth_normal(float *dev, size_t n, uint64_t seed, int norm_weight, hipStream_t s);
 int gq_launch_synth_kv(float *slab, int n_layers, int n_kv, int hd, int max_seq, int n_pos,

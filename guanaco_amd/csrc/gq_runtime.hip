@@ -1078,6 +1078,15 @@ extern "C" int gq_hip_argmax_dev(gq_ctx *c, const float *x, int n, int *out_inde
   return rc ? fail(c, rc, "argmax") : 0;
 }
 
+extern "C" int gq_hip_prefill_gemm_dev(gq_ctx *c, int dtype, int mode, const void *w, int n, int k,
+                                       const float *x, int t, float *y, const float *r) {
+  if (!c || !w || !x || !y || t <= 0) return -1;
+  if (dtype != GQ_Q4_K) return fail(c, -1, "prefill GEMM: Q4_K weights only");
+  if (k % 256) return fail(c, -2, "prefill GEMM: cols must be a multiple of 256");
+  const int rc = gq_launch_prefill_gemm(mode == 1 ? MV_RESID : MV_STORE, x, w, y, r, t, n, k, c->stream);
+  return rc ? fail(c, rc, "prefill GEMM launch (rows must be a multiple of 128)") : 0;
+}
+
 extern "C" int gq_hip_copy_dev(gq_ctx *c, void *dst, const void *src, size_t bytes) {
   if (!c || !dst || !src) return -1;
   const int rc = gq_launch_copy(dst, src, bytes, c->n_cu, c->stream);

@@ -82,6 +82,8 @@ def _load():
         "gq_hip_argmax_dev": (C.c_int, [_vp, _vp, C.c_int, _vp]),
         "gq_hip_silu_mul_dev": (C.c_int, [_vp, _vp, _vp, C.c_int]),
         "gq_hip_copy_dev": (C.c_int, [_vp, _vp, _vp, C.c_size_t]),
+        "gq_hip_prefill_gemm_dev": (C.c_int, [_vp, C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp,
+                                              C.c_int, _vp, _vp]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)

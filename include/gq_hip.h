@@ -242,6 +242,17 @@ int gq_hip_embed_dev(gq_ctx *ctx, int dtype, const void *table, int hidden, int 
                      float *out);
 int gq_hip_argmax_dev(gq_ctx *ctx, const float *x, int n, int *out_index_dev);
 int gq_hip_silu_mul_dev(gq_ctx *ctx, float *gate, const float *up, int n);
+/* ------------------------------------------------------- prefill chunk
+ * y[t][n] = sum_k x[t][k] w[n][k] for t < T tokens at once on the bf16
+ * matrix cores, fp32 accumulation: the projections of a prefill chunk, which
+ * the reference runs as T sequential matvecs (linear_dispatch,
+ * engine.c:119-152).  w: rows x cols Q4_K on the device (rows % 128 == 0,
+ * cols % 256 == 0); x: T x cols fp32, y: T x rows fp32, device pointers.
+ * mode 0 stores, mode 1 adds r (T x rows, may alias y).  x and the
+ * dequantized weights are rounded to bf16 (nearest even) before the
+ * products.  Asynchronous on the context stream. */
+int gq_hip_prefill_gemm_dev(gq_ctx *ctx, int dtype, int mode, const void *w, int rows, int cols,
+                            const float *x, int T, float *y, const float *r);
 /* Device-to-device copy by a plain streaming kernel (bytes and both pointers
  * multiples of 16), asynchronous.  No reference counterpart: the known-size
  * workload that scales the HBM byte counters of the profiles. */
