@@ -22,6 +22,8 @@
  * sum l_c e^(m_c-M).  The position count is read on the device, so the same
  * launch serves every step of a captured decode graph.
  */
+#include <algorithm>
+
 #include "gq_device.h"
 #include "gq_internal.h"
 
@@ -31,26 +33,30 @@ constexpr int kThreads = 256;
 
 __global__ __launch_bounds__(kThreads) void rope_append_kernel(RopeArgs a) {
 #pragma clang fp contract(off)
-  const int pos = a.pos_dev ? *a.pos_dev : a.pos;
+  /* token blockIdx.x of a chunk (0 for one token) */
+  const int tz = blockIdx.x;
+  const int pos = (a.pos_dev ? *a.pos_dev : a.pos) + tz;
   /* the host rejects positions outside the cache; this keeps a stray
    * device-side position from indexing past the table or the slab */
   if (pos < 0 || pos >= a.max_seq) return;
   const int half = a.hd >> 1;
   const int p = pos;
   const float2 *cs = a.cs + (size_t)pos * half;
+  float *q = a.q + (size_t)tz * a.q_stride;
+  const float *kin = a.k + (size_t)tz * a.k_stride, *vin = a.v + (size_t)tz * a.v_stride;
   const int nq = a.n_heads * half, nk = a.n_kv * half;
   for (int t = threadIdx.x; t < nq + nk; t += kThreads) {
     const bool isq = t < nq;
     const int u = isq ? t : t - nq;
     const int h = u / half, i = u - h * half;
     const float2 c = cs[i];
-    const float *src = isq ? a.q + (size_t)h * a.hd : a.k + (size_t)h * a.hd;
+    const float *src = isq ? q + (size_t)h * a.hd : kin + (size_t)h * a.hd;
     const float x0 = src[2 * i], x1 = src[2 * i + 1];
     const float y0 = x0 * c.x - x1 * c.y;
     const float y1 = x0 * c.y + x1 * c.x;
     if (isq) {
-      a.q[(size_t)h * a.hd + 2 * i] = y0;
-      a.q[(size_t)h * a.hd + 2 * i + 1] = y1;
+      q[(size_t)h * a.hd + 2 * i] = y0;
+      q[(size_t)h * a.hd + 2 * i + 1] = y1;
     } else {
       float *dst = a.kc + ((size_t)h * a.max_seq + p) * a.hd;
       dst[2 * i] = y0;
@@ -59,7 +65,7 @@ __global__ __launch_bounds__(kThreads) void rope_append_kernel(RopeArgs a) {
   }
   for (int t = threadIdx.x; t < a.n_kv * a.hd; t += kThreads) {
     const int h = t / a.hd, d = t - h * a.hd;
-    a.vc[((size_t)h * a.max_seq + p) * a.hd + d] = a.v[t];
+    a.vc[((size_t)h * a.max_seq + p) * a.hd + d] = vin[t];
   }
 }
 
@@ -82,9 +88,12 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(AttnArgs a) {
   __shared__ float ss[G][S];
   __shared__ float4 sr[NPG][G][DG];
 
-  const int g = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
+  const int g = blockIdx.x, c = blockIdx.y, tz = blockIdx.z, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int pos = a.pos_dev ? gld<int>(a.pos_dev) : a.pos;
+  /* token tz of a chunk (0 for one token): its query, partials, position */
+  const int pos = (a.pos_dev ? gld<int>(a.pos_dev) : a.pos) + tz;
+  const float *aq = a.q + (size_t)tz * a.q_stride;
+  float *part_o = a.part_o + (size_t)tz * a.po_stride, *part_ml = a.part_ml + (size_t)tz * a.pml_stride;
   const int L = min(pos + 1, a.max_seq);
   const int c0 = c * S;
   const int n = min(S, L - c0);
@@ -104,8 +113,8 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(AttnArgs a) {
   float4 qa[G], qb[G];
 #pragma unroll
   for (int h = 0; h < G; h++) {
-    qa[h] = gld<float4>(a.q + (size_t)(h0 + h) * HD + d0);
-    qb[h] = gld<float4>(a.q + (size_t)(h0 + h) * HD + d1);
+    qa[h] = gld<float4>(aq + (size_t)(h0 + h) * HD + d0);
+    qb[h] = gld<float4>(aq + (size_t)(h0 + h) * HD + d1);
   }
   float4 ka[KIT], kb[KIT];
 #pragma unroll
@@ -149,8 +158,8 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(AttnArgs a) {
     }
     l = gq_wave_sum(l);
     if (lane == 0) {
-      gst<float>(a.part_ml + (size_t)(h0 + h) * ml + 2 * c, m);
-      gst<float>(a.part_ml + (size_t)(h0 + h) * ml + 2 * c + 1, l);
+      gst<float>(part_ml + (size_t)(h0 + h) * ml + 2 * c, m);
+      gst<float>(part_ml + (size_t)(h0 + h) * ml + 2 * c + 1, l);
     }
   }
   __syncthreads();
@@ -184,7 +193,7 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(AttnArgs a) {
       const float4 u = sr[p][h][q];
       o.x += u.x, o.y += u.y, o.z += u.z, o.w += u.w;
     }
-    gst<float4>(a.part_o + ((size_t)(h0 + h) * a.nch + c) * HD + 4 * q, o);
+    gst<float4>(part_o + ((size_t)(h0 + h) * a.nch + c) * HD + 4 * q, o);
   }
 }
 
@@ -194,11 +203,11 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
   extern __shared__ float sw[]; /* [nch] weights e^(m_c - M), then l_c */
   __shared__ float red[kThreads / GQ_WAVE];
   __shared__ float sacc[kThreads / 32][32];
-  const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int pos = a.pos_dev ? gld<int>(a.pos_dev) : a.pos;
+  const int h = blockIdx.x, tz = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int pos = (a.pos_dev ? gld<int>(a.pos_dev) : a.pos) + tz;
   const int L = min(pos + 1, a.max_seq);
   const int nc = (L + kChunk - 1) / kChunk;
-  const float *ml = a.part_ml + (size_t)h * a.nch * 2;
+  const float *ml = a.part_ml + (size_t)tz * a.pml_stride + (size_t)h * a.nch * 2;
   float *sl = sw + a.nch;
   float m = -INFINITY;
   for (int c = tid; c < nc; c += kThreads) {
@@ -223,7 +232,7 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
   __syncthreads();
   const float Ls = (red[0] + red[1]) + (red[2] + red[3]);
   const int d = blockIdx.y * 32 + (tid & 31), cg = tid >> 5;
-  const float *o = a.part_o + (size_t)h * a.nch * a.hd + d;
+  const float *o = a.part_o + (size_t)tz * a.po_stride + (size_t)h * a.nch * a.hd + d;
   float acc = 0.f;
 #pragma unroll 8
   for (int c = cg; c < nc; c += kThreads / 32) acc = __builtin_fmaf(gld<float>(o + (size_t)c * a.hd), sw[c], acc);
@@ -233,14 +242,26 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
     float t = 0.f;
 #pragma unroll
     for (int k = 0; k < kThreads / 32; k++) t += sacc[k][tid];
-    gst<float>(a.out + (size_t)h * a.hd + d, t / Ls);
+    gst<float>(a.out + (size_t)tz * a.out_stride + (size_t)h * a.hd + d, t / Ls);
   }
 }
 
 template <int HD, int G>
 int launch_partial(const AttnArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL((attn_partial_kernel<HD, G>), dim3(a.n_kv, a.nch), dim3(kThreads), 0, s, a);
+  hipLaunchKernelGGL((attn_partial_kernel<HD, G>), dim3(a.n_kv, a.nch, std::max(a.ntok, 1)), dim3(kThreads), 0, s,
+                     a);
   return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+int launch_partial_any(const AttnArgs &a, hipStream_t s) {
+  const int G = a.n_heads / a.n_kv;
+  if (a.hd == 128 && G == 4) return launch_partial<128, 4>(a, s);
+  if (a.hd == 128 && G == 8) return launch_partial<128, 8>(a, s);
+  if (a.hd == 128 && G == 1) return launch_partial<128, 1>(a, s);
+  if (a.hd == 64 && G == 4) return launch_partial<64, 4>(a, s);
+  if (a.hd == 64 && G == 8) return launch_partial<64, 8>(a, s);
+  if (a.hd == 64 && G == 1) return launch_partial<64, 1>(a, s);
+  return -1;
 }
 
 } // namespace
@@ -258,15 +279,8 @@ int gq_attn_smax(int max_seq, int nch) {
 
 int gq_launch_attention(const AttnArgs &a, hipStream_t s, hipEvent_t mid) {
   if (a.n_kv <= 0 || a.n_heads % a.n_kv || a.nch != gq_attn_nch(a.n_kv, a.max_seq)) return -1;
-  if (a.hd % 32 || (size_t)a.nch * 2 * sizeof(float) > 32768) return -1;
-  const int G = a.n_heads / a.n_kv;
-  int rc = -1;
-  if (a.hd == 128 && G == 4) rc = launch_partial<128, 4>(a, s);
-  else if (a.hd == 128 && G == 8) rc = launch_partial<128, 8>(a, s);
-  else if (a.hd == 128 && G == 1) rc = launch_partial<128, 1>(a, s);
-  else if (a.hd == 64 && G == 4) rc = launch_partial<64, 4>(a, s);
-  else if (a.hd == 64 && G == 8) rc = launch_partial<64, 8>(a, s);
-  else if (a.hd == 64 && G == 1) rc = launch_partial<64, 1>(a, s);
+  if (a.hd % 32 || (size_t)a.nch * 2 * sizeof(float) > 32768 || a.ntok > 1) return -1;
+  const int rc = launch_partial_any(a, s);
   if (rc) return rc;
   if (mid) (void)hipEventRecord(mid, s);
   hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_heads, a.hd / 32), dim3(kThreads),
@@ -274,8 +288,21 @@ int gq_launch_attention(const AttnArgs &a, hipStream_t s, hipEvent_t mid) {
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
+int gq_launch_attention_chunk(const AttnArgs &a, hipStream_t s) {
+  if (a.n_kv <= 0 || a.n_heads % a.n_kv || a.ntok < 1 || a.hd % 32 || a.pos < 0) return -1;
+  if (a.pos + a.ntok > a.max_seq || a.nch != (a.pos + a.ntok + kChunk - 1) / kChunk) return -1;
+  if ((size_t)a.nch * 2 * sizeof(float) > 32768 || a.po_stride < (size_t)a.n_heads * a.nch * a.hd ||
+      a.pml_stride < (size_t)a.n_heads * a.nch * 2)
+    return -1;
+  const int rc = launch_partial_any(a, s);
+  if (rc) return rc;
+  hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_heads, a.hd / 32, a.ntok), dim3(kThreads),
+                     (size_t)a.nch * 2 * sizeof(float), s, a);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
 int gq_launch_rope_append(const RopeArgs &a, hipStream_t s) {
-  if ((a.hd & 1) || a.n_kv <= 0) return -1;
-  hipLaunchKernelGGL(rope_append_kernel, dim3(1), dim3(kThreads), 0, s, a);
+  if ((a.hd & 1) || a.n_kv <= 0 || a.ntok < 0) return -1;
+  hipLaunchKernelGGL(rope_append_kernel, dim3(std::max(a.ntok, 1)), dim3(kThreads), 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }

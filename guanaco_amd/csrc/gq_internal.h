@@ -72,10 +72,18 @@ struct AttnArgs {
   int pos;
   int n_heads, n_kv, hd, max_seq, nch, s_max;
   float scale;
+  /* a chunk of ntok query tokens at positions pos .. pos + ntok - 1 (causal:
+   * token t attends to 0 .. pos + t); per-token strides in floats.  Decode
+   * launches leave these zero (one token). */
+  int ntok, q_stride, out_stride;
+  size_t po_stride, pml_stride;
 };
 int gq_attn_nch(int n_kv, int max_seq);
 int gq_attn_smax(int max_seq, int nch);
 int gq_launch_attention(const AttnArgs &a, hipStream_t s, hipEvent_t mid);
+/* The chunk form: a.ntok tokens, a.nch = chunks of the longest row
+ * (ceil((pos + ntok) / 128)), partial buffers of ntok * stride floats. */
+int gq_launch_attention_chunk(const AttnArgs &a, hipStream_t s);
 
 struct RopeArgs {
   float *q;
@@ -85,6 +93,9 @@ struct RopeArgs {
   const int *pos_dev;
   int pos;
   int n_heads, n_kv, hd, max_seq;
+  /* ntok tokens at pos .. pos + ntok - 1 (0 or 1: one); per-token strides in
+   * floats of q, k, v */
+  int ntok, q_stride, k_stride, v_stride;
 };
 int gq_launch_rope_append(const RopeArgs &a, hipStream_t s);
 
@@ -103,11 +114,17 @@ int gq_launch_silu_mul(float *gate, const float *up, int n, hipStream_t s);
 int gq_launch_copy(void *dst, const void *src, size_t bytes, int n_cu, hipStream_t s);
 
 /* ---- prefill chunk ---------------------------------------------------
- * Y[T][N] = X[T][K] . W^T on the bf16 matrix cores (W: N rows of Q4_K,
- * X fp32 row-major); MV_STORE or MV_RESID (Y = R + X W^T, R may alias Y).
- * Needs N % 128 == 0 and K % 256 == 0. */
-int gq_launch_prefill_gemm(int mode, const float *X, const void *W, float *Y, const float *R, int T, int N, int K,
+ * Y[T][N] = X[T][K] . W^T on the bf16 matrix cores (W: N rows of Q4_K or
+ * Q6_K, X fp32 row-major); MV_STORE or MV_RESID (Y = R + X W^T, R may alias
+ * Y).  Needs N % 128 == 0 and K % 256 == 0. */
+int gq_launch_prefill_gemm(int dtype, int mode, const float *X, const void *W, float *Y, const float *R, int T,
+                           int N, int K, hipStream_t s);
+/* RMSNorm of `rows` consecutive rows of dim floats, one workgroup per row */
+int gq_launch_rmsnorm_rows(const float *x, const float *w, float *out, int dim, int rows, float eps,
                            hipStream_t s);
+/* embedding rows of tokens[0..n) (device array) into out (n x hidden) */
+int gq_launch_embed_rows(int dtype, const void *table, int hidden, const int *tokens_dev, int n, float *out,
+                         hipStream_t s);
 int gq_launch_synth_quant(void *dev, int dtype, int rows, int cols, uint64_t seed, hipStream_t s);
 int gq_launch_synth_normal(float *dev, size_t n, uint64_t seed, int norm_weight, hipStream_t s);
 int gq_launch_synth_kv(float *slab, int n_layers, int n_kv, int hd, int max_seq, int n_pos,

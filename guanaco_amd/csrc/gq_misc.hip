@@ -14,11 +14,13 @@ namespace {
 constexpr int kThreads = 256;
 
 /* out = w * (x * 1/sqrt(mean(x^2) + eps)) (kernels_cpu.c:199-265); one
- * workgroup, sum of squares in a fixed tree order. */
+ * workgroup per row (blockIdx.x), sum of squares in a fixed tree order. */
 __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *x, const float *w, float *out,
                                                           int dim, float eps) {
   __shared__ float red[kThreads / GQ_WAVE];
   const int tid = threadIdx.x;
+  x += (size_t)blockIdx.x * dim;
+  out += (size_t)blockIdx.x * dim;
   float ss = 0.f;
   for (int i = tid; i < dim; i += kThreads) ss = __builtin_fmaf(x[i], x[i], ss);
   ss = gq_wave_sum(ss);
@@ -32,11 +34,14 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *x, const
 }
 
 /* Embedding row of `token` (engine.c:214-283): F32 copy, Q8_0 q*scale,
- * Q4_K (d*sc)*q - dmin*m with separate roundings. */
+ * Q4_K (d*sc)*q - dmin*m with separate roundings.  With tokens != NULL,
+ * workgroup b writes the row of tokens[b] to out + b * hidden. */
 __global__ __launch_bounds__(kThreads) void embed_kernel(int dtype, const uint8_t *table, int hidden,
-                                                        const int *token_dev, int token, float *out) {
+                                                        const int *token_dev, int token, const int *tokens,
+                                                        float *out) {
 #pragma clang fp contract(off)
-  const int tok = token_dev ? *token_dev : token;
+  const int tok = tokens ? tokens[blockIdx.x] : token_dev ? *token_dev : token;
+  out += (size_t)blockIdx.x * hidden;
   for (int e = threadIdx.x; e < hidden; e += kThreads) {
     float v;
     if (dtype == GQ_F32) {
@@ -175,7 +180,13 @@ __global__ void synth_kv_kernel(float *slab, int n_kv, int hd, int max_seq, int 
 } // namespace
 
 int gq_launch_rmsnorm(const float *x, const float *w, float *out, int dim, float eps, hipStream_t s) {
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(kThreads), 0, s, x, w, out, dim, eps);
+  return gq_launch_rmsnorm_rows(x, w, out, dim, 1, eps, s);
+}
+
+int gq_launch_rmsnorm_rows(const float *x, const float *w, float *out, int dim, int rows, float eps,
+                           hipStream_t s) {
+  if (rows <= 0 || dim <= 0) return -1;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, s, x, w, out, dim, eps);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
@@ -183,7 +194,15 @@ int gq_launch_embed(int dtype, const void *table, int hidden, const int *token_d
                     float *out, hipStream_t s) {
   if (dtype != GQ_F32 && dtype != GQ_Q8_0 && dtype != GQ_Q4_K) return -1;
   hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(kThreads), 0, s, dtype, (const uint8_t *)table,
-                     hidden, token_dev, token, out);
+                     hidden, token_dev, token, (const int *)nullptr, out);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+int gq_launch_embed_rows(int dtype, const void *table, int hidden, const int *tokens_dev, int n, float *out,
+                         hipStream_t s) {
+  if ((dtype != GQ_F32 && dtype != GQ_Q8_0 && dtype != GQ_Q4_K) || !tokens_dev || n <= 0) return -1;
+  hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(kThreads), 0, s, dtype, (const uint8_t *)table, hidden,
+                     (const int *)nullptr, 0, tokens_dev, out);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 

@@ -35,6 +35,21 @@ struct Workspace {
   size_t part_cap = 0, part_ml_cap = 0; /* floats in part_o / part_ml */
 };
 
+/* Prefill-chunk activations, T x width row-major, allocated on first use
+ * for up to `cap` tokens; attention partials grow with the context. */
+struct PrefillWs {
+  int cap = 0;
+  float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr;
+  float *g = nullptr, *u = nullptr, *po = nullptr, *pml = nullptr;
+  int *tok = nullptr;
+  size_t po_cap = 0, pml_cap = 0;
+};
+
+/* tokens per prefill chunk */
+constexpr int kPrefillChunk = 512;
+/* bytes of attention partials one chunk launch may use */
+constexpr size_t kPrefillPartBytes = (size_t)64 << 20;
+
 } // namespace
 
 struct gq_ctx {
@@ -57,6 +72,7 @@ struct gq_ctx {
   gq_model m{};
   std::vector<gq_layer> layers;
   Workspace ws;
+  PrefillWs pf;
   /* graph */
   hipGraph_t graph = nullptr;
   hipGraphExec_t gexec = nullptr;
@@ -883,6 +899,154 @@ extern "C" int gq_hip_decode_loop(gq_ctx *c, int token, int pos, int n_steps, in
   return 0;
 }
 
+/* ------------------------------------------------------------ prefill
+ * forward(model, kv, scr, tokens, n, pos) for n > 1 (engine.c:559-595 with
+ * transformer_layer's T-token path, engine.c:352-509): chunks of up to 512
+ * tokens; per layer and chunk one GEMM launch per projection on the matrix
+ * cores, RoPE + append of every token of the chunk, then causal attention
+ * (token t sees positions 0 .. pos + t). */
+static int pf_ensure(gq_ctx *c, float *&p, size_t &cap, size_t n) {
+  if (cap >= n && p) return 0;
+  if (p) gq_hip_free(c, p);
+  p = (float *)dev_alloc(c, sizeof(float) * n);
+  if (!p) return -4;
+  cap = n;
+  return 0;
+}
+
+static int pf_alloc(gq_ctx *c) {
+  PrefillWs &w = c->pf;
+  if (w.cap) return 0;
+  const gq_model &m = c->m;
+  const size_t T = kPrefillChunk, H = m.hidden, F = m.ff, kvd = (size_t)m.n_kv_heads * m.head_dim;
+  float **bufs[8] = {&w.x, &w.xn, &w.q, &w.att, &w.k, &w.v, &w.g, &w.u};
+  const size_t n[8] = {T * H, T * H, T * H, T * H, T * kvd, T * kvd, T * F, T * F};
+  for (int i = 0; i < 8; i++)
+    if (!(*bufs[i] = (float *)dev_alloc(c, sizeof(float) * n[i]))) return -4;
+  if (!(w.tok = (int *)dev_alloc(c, sizeof(int) * T))) return -4;
+  w.cap = kPrefillChunk;
+  return 0;
+}
+
+/* y (T x rows) = x (T x cols) W^T, or y += with resid: the bf16 GEMM for
+ * Q4_K / Q6_K weights of 128-row multiples, else T device matvecs */
+static int pf_proj(gq_ctx *c, const gq_weight &w, const float *x, float *y, int T, bool resid) {
+  if ((w.dtype == GQ_Q4_K || w.dtype == GQ_Q6_K) && w.rows % 128 == 0 && w.cols % 256 == 0)
+    return gq_launch_prefill_gemm(w.dtype, resid ? MV_RESID : MV_STORE, x, w.data, y, resid ? y : nullptr, T,
+                                  w.rows, w.cols, c->stream);
+  for (int t = 0; t < T; t++) {
+    MvArgs a{};
+    float *yt = y + (size_t)t * w.rows;
+    a.seg[0] = MvSeg{(const uint8_t *)w.data, yt, resid ? yt : nullptr, w.rows};
+    a.nseg = 1, a.cols = w.cols, a.x = x + (size_t)t * w.cols;
+    const int rc = gq_launch_matvec(w.dtype, resid ? MV_RESID : MV_STORE, a, c->stream);
+    if (rc) return rc;
+  }
+  return 0;
+}
+
+/* RoPE + append of T tokens at pos..pos+T-1 (q: T x n_heads*hd in place,
+ * k/v: T x n_kv*hd), then causal attention into out (T x n_heads*hd), in
+ * token sub-batches that keep the partials under kPrefillPartBytes */
+static int pf_attention(gq_ctx *c, int layer, int pos, int T, int n_heads, float *q, const float *k, const float *v,
+                        float *out) {
+  const int hd = c->kv_hd, kvd = c->kv_heads * hd, qd = n_heads * hd;
+  RopeArgs ra{q, k, v, gq_hip_kv_k(c, layer), gq_hip_kv_v(c, layer), c->rope, nullptr, pos,
+              n_heads, c->kv_heads, hd, c->kv_max_seq, T, qd, kvd, kvd};
+  int rc = gq_launch_rope_append(ra, c->stream);
+  if (rc) return rc;
+  PrefillWs &w = c->pf;
+  for (int t0 = 0; t0 < T;) {
+    const int nch_all = (pos + T + 127) / 128;
+    const size_t per_tok = (size_t)n_heads * nch_all * (hd + 2) * sizeof(float);
+    const int nt = std::max(1, std::min(T - t0, (int)(kPrefillPartBytes / per_tok)));
+    AttnArgs aa{};
+    aa.pos = pos + t0, aa.ntok = nt;
+    aa.nch = (pos + t0 + nt + 127) / 128;
+    aa.po_stride = (size_t)n_heads * aa.nch * hd, aa.pml_stride = (size_t)n_heads * aa.nch * 2;
+    if ((rc = pf_ensure(c, w.po, w.po_cap, aa.po_stride * nt)) ||
+        (rc = pf_ensure(c, w.pml, w.pml_cap, aa.pml_stride * nt)))
+      return rc;
+    aa.q = q + (size_t)t0 * qd, aa.q_stride = qd;
+    aa.k = gq_hip_kv_k(c, layer), aa.v = gq_hip_kv_v(c, layer);
+    aa.part_o = w.po, aa.part_ml = w.pml;
+    aa.out = out + (size_t)t0 * qd, aa.out_stride = qd;
+    aa.n_heads = n_heads, aa.n_kv = c->kv_heads, aa.hd = hd, aa.max_seq = c->kv_max_seq;
+    aa.s_max = gq_attn_smax(c->kv_max_seq, aa.nch), aa.scale = 1.0f / sqrtf((float)hd);
+    if ((rc = gq_launch_attention_chunk(aa, c->stream))) return rc;
+    t0 += nt;
+  }
+  return 0;
+}
+
+static int pf_layer(gq_ctx *c, int l, int pos, int T) {
+  const gq_model &m = c->m;
+  const gq_layer &L = c->layers[l];
+  PrefillWs &w = c->pf;
+  int rc;
+  if ((rc = gq_launch_rmsnorm_rows(w.x, L.rms_att, w.xn, m.hidden, T, m.rms_eps, c->stream)) ||
+      (rc = pf_proj(c, L.wq, w.xn, w.q, T, false)) || (rc = pf_proj(c, L.wk, w.xn, w.k, T, false)) ||
+      (rc = pf_proj(c, L.wv, w.xn, w.v, T, false)) ||
+      (rc = pf_attention(c, l, pos, T, m.n_heads, w.q, w.k, w.v, w.att)) ||
+      (rc = pf_proj(c, L.wo, w.att, w.x, T, true)) ||
+      (rc = gq_launch_rmsnorm_rows(w.x, L.rms_ffn, w.xn, m.hidden, T, m.rms_eps, c->stream)) ||
+      (rc = pf_proj(c, L.w_gate, w.xn, w.g, T, false)) || (rc = pf_proj(c, L.w_up, w.xn, w.u, T, false)) ||
+      (rc = gq_launch_silu_mul(w.g, w.u, T * m.ff, c->stream)) || (rc = pf_proj(c, L.w_down, w.g, w.x, T, true)))
+    return rc;
+  return 0;
+}
+
+extern "C" int gq_hip_prefill(gq_ctx *c, const int32_t *tokens, int n_tokens, int pos, float *logits,
+                              float *hidden_last, float *ms) {
+  if (!c || !tokens || n_tokens <= 0) return fail(c, -1, "prefill: bad argument");
+  int rc = check_pos(c, pos, n_tokens);
+  if (rc) return rc;
+  const gq_model &m = c->m;
+  for (int i = 0; i < n_tokens; i++)
+    if (tokens[i] < 0 || tokens[i] >= m.vocab) return fail(c, -1, "prefill: token %d out of range", tokens[i]);
+  if ((rc = pf_alloc(c))) return rc;
+  PrefillWs &w = c->pf;
+  Workspace &ws = c->ws;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (ms) {
+    HIPCHK(c, hipEventCreate(&e0));
+    HIPCHK(c, hipEventCreate(&e1));
+    HIPCHK(c, hipEventRecord(e0, c->stream));
+  }
+  int T = 0;
+  for (int t0 = 0; t0 < n_tokens; t0 += T) {
+    T = std::min(kPrefillChunk, n_tokens - t0);
+    HIPCHK(c, hipMemcpyAsync(w.tok, tokens + t0, sizeof(int) * T, hipMemcpyHostToDevice, c->stream));
+    if ((rc = gq_launch_embed_rows(m.embed.dtype, m.embed.data, m.hidden, w.tok, T, w.x, c->stream)))
+      return fail(c, rc, "prefill: embed");
+    for (int l = 0; l < m.n_layers; l++)
+      if ((rc = pf_layer(c, l, pos + t0, T))) return fail(c, rc, "prefill: layer %d launch failed", l);
+  }
+  /* last token: final RMSNorm + LM head + argmax as in a decode step */
+  HIPCHK(c, hipMemcpyAsync(ws.hidden, w.x + (size_t)(T - 1) * m.hidden, sizeof(float) * m.hidden,
+                           hipMemcpyDeviceToDevice, c->stream));
+  if ((rc = op_lm_head(c, ws.hidden)) ||
+      (rc = gq_launch_argmax(ws.logits, m.vocab, ws.amax, ws.amax_blocks, ws.d_token, nullptr, nullptr, nullptr,
+                             c->stream)))
+    return fail(c, rc, "prefill: lm head");
+  if (ms) HIPCHK(c, hipEventRecord(e1, c->stream));
+  int next = -1;
+  HIPCHK(c, hipMemcpyAsync(&next, ws.d_token, sizeof(int), hipMemcpyDeviceToHost, c->stream));
+  if (logits)
+    HIPCHK(c, hipMemcpyAsync(logits, ws.logits, sizeof(float) * m.vocab, hipMemcpyDeviceToHost, c->stream));
+  if (hidden_last)
+    HIPCHK(c, hipMemcpyAsync(hidden_last, ws.hidden, sizeof(float) * m.hidden, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  if (ms) {
+    float t = 0.f;
+    (void)hipEventElapsedTime(&t, e0, e1);
+    *ms = t;
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+  }
+  return next;
+}
+
 /* ------------------------------------------------------------ measurement */
 extern "C" int gq_hip_profile_step(gq_ctx *c, int token, int pos, double ms[GQ_NCLASS],
                                    int launches[GQ_NCLASS], double bytes[GQ_NCLASS]) {
@@ -1062,6 +1226,16 @@ extern "C" int gq_hip_attention_dev(gq_ctx *c, int layer, int pos, int n_heads, 
   return gq_launch_attention(aa, c->stream, nullptr) ? fail(c, -1, "attention launch (unsupported head_dim/group?)") : 0;
 }
 
+extern "C" int gq_hip_prefill_attention_dev(gq_ctx *c, int layer, int pos, int T, int n_heads, float *q,
+                                            const float *k, const float *v, float *out) {
+  if (!c || !c->kslab || !q || !k || !v || !out || layer < 0 || layer >= c->kv_layers || T <= 0 ||
+      n_heads <= 0 || n_heads % c->kv_heads)
+    return fail(c, -1, "prefill attention: bad argument");
+  if (pos < 0 || pos + T > c->kv_max_seq) return fail(c, -5, "prefill attention: positions outside the cache");
+  const int rc = pf_attention(c, layer, pos, T, n_heads, q, k, v, out);
+  return rc ? fail(c, rc, "prefill attention launch (unsupported head_dim/group?)") : 0;
+}
+
 extern "C" int gq_hip_embed_dev(gq_ctx *c, int dtype, const void *table, int hidden, int token, float *out) {
   if (!c || !table || !out || hidden <= 0 || token < 0) return -1;
   return gq_launch_embed(dtype, table, hidden, nullptr, token, out, c->stream) ? fail(c, -1, "embed") : 0;
@@ -1081,9 +1255,9 @@ extern "C" int gq_hip_argmax_dev(gq_ctx *c, const float *x, int n, int *out_inde
 extern "C" int gq_hip_prefill_gemm_dev(gq_ctx *c, int dtype, int mode, const void *w, int n, int k,
                                        const float *x, int t, float *y, const float *r) {
   if (!c || !w || !x || !y || t <= 0) return -1;
-  if (dtype != GQ_Q4_K) return fail(c, -1, "prefill GEMM: Q4_K weights only");
+  if (dtype != GQ_Q4_K && dtype != GQ_Q6_K) return fail(c, -1, "prefill GEMM: Q4_K or Q6_K weights only");
   if (k % 256) return fail(c, -2, "prefill GEMM: cols must be a multiple of 256");
-  const int rc = gq_launch_prefill_gemm(mode == 1 ? MV_RESID : MV_STORE, x, w, y, r, t, n, k, c->stream);
+  const int rc = gq_launch_prefill_gemm(dtype, mode == 1 ? MV_RESID : MV_STORE, x, w, y, r, t, n, k, c->stream);
   return rc ? fail(c, rc, "prefill GEMM launch (rows must be a multiple of 128)") : 0;
 }
 

@@ -84,6 +84,10 @@ def _load():
         "gq_hip_copy_dev": (C.c_int, [_vp, _vp, _vp, C.c_size_t]),
         "gq_hip_prefill_gemm_dev": (C.c_int, [_vp, C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp,
                                               C.c_int, _vp, _vp]),
+        "gq_hip_prefill_attention_dev": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp,
+                                                   _vp, _vp]),
+        "gq_hip_prefill": (C.c_int, [_vp, C.POINTER(C.c_int32), C.c_int, C.c_int, _fp, _fp,
+                                     C.POINTER(C.c_float)]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -307,6 +311,10 @@ class Context:
     def attention_dev(self, layer, pos, n_heads, q_buf, out_buf):
         return lib.gq_hip_attention_dev(self.h, layer, pos, n_heads, q_buf.ptr, out_buf.ptr)
 
+    def prefill_attention_dev(self, layer, pos, T, n_heads, q_buf, k_buf, v_buf, out_buf):
+        return lib.gq_hip_prefill_attention_dev(self.h, layer, pos, T, n_heads, q_buf.ptr, k_buf.ptr,
+                                                v_buf.ptr, out_buf.ptr)
+
     # ---- sessions ----
     def lctx_save(self, path, current_pos, tokens=None):
         toks = np.ascontiguousarray(tokens if tokens is not None else [], np.int32)
@@ -383,6 +391,21 @@ class DeviceModel:
         if tok < 0:
             self.ctx.raise_last("forward_token", tok)
         return tok, logits, (hid.reshape(s.n_layers, s.hidden) if want_hidden else None)
+
+    def prefill(self, tokens, pos, want_logits=True, want_hidden=False):
+        """forward() over a prompt: returns (next greedy token, logits of the
+        last token, its hidden state before the final norm, device ms)."""
+        s = self.spec
+        toks = np.ascontiguousarray(tokens, np.int32)
+        logits = np.empty(s.vocab, np.float32) if want_logits else None
+        hid = np.empty(s.hidden, np.float32) if want_hidden else None
+        ms = C.c_float(0)
+        tok = lib.gq_hip_prefill(self.ctx.h, toks.ctypes.data_as(C.POINTER(C.c_int32)), toks.size, pos,
+                                 _f(logits) if want_logits else None, _f(hid) if want_hidden else None,
+                                 C.byref(ms))
+        if tok < 0:
+            self.ctx.raise_last("prefill", tok)
+        return tok, logits, hid, ms.value
 
     def decode_loop(self, token, pos, n_steps, use_graph=True):
         out = np.zeros(n_steps, np.int32)

@@ -15,6 +15,13 @@
         4096-token prefix (1 GiB of K/V) from pinned host memory.  Prints one
         JSON line per result.
 
+    python3 -m guanaco_amd.prof config5
+        the prefill chunk on the 8B shape: the bf16-MFMA GEMM of 512 tokens
+        against each projection shape (4096x4096, 1024x4096, 14336x4096 and
+        the 4096x14336 down projection, Q4_K and Q6_K), RoPE + append +
+        causal attention of the 512 tokens, and forward() of a 512-token
+        prompt through the whole 32-layer model.
+
 The decode workload itself is ``python3 bench.py --eager`` (one kernel launch
 per op, so per-dispatch counters map onto ops).
 """
@@ -135,6 +142,64 @@ def config4_restore():
         ctx.close()
 
 
+def config5(ctx, T=512, iters=20):
+    spec = S.LLAMA8B
+    H_, F = spec.hidden, spec.ff
+    shapes = [("q/o", H_, H_), ("k/v", spec.n_kv_heads * spec.head_dim, H_), ("gate/up", F, H_), ("down", H_, F)]
+    for dt, name in ((S.Q4_K, "Q4_K"), (S.Q6_K, "Q6_K")):
+        for what, N, K in shapes:
+            w = ctx.synth_quant(dt, N, K, 77 + N + K)
+            x = ctx.synth_normal(T * K, 5)
+            y = ctx.alloc(4 * T * N)
+
+            def go():
+                ctx.check(H.lib.gq_hip_prefill_gemm_dev(ctx.h, dt, 0, w.ptr, N, K, x.ptr, T, y.ptr, None), "gemm")
+            go()
+            ctx.sync()
+            t0 = time.perf_counter()
+            for _ in range(iters):
+                go()
+            ctx.sync()
+            dt_s = (time.perf_counter() - t0) / iters
+            flop = 2.0 * T * N * K
+            emit(config=5, what=f"prefill GEMM {name} {what}: {T} tokens x {N}x{K}", us_per_launch=round(dt_s * 1e6, 2),
+                 gflop=round(flop / 1e9, 2), TFLOP_per_s=round(flop / dt_s / 1e12, 1),
+                 weight_bytes=S.qbytes(dt, N, K))
+            w.free(), x.free(), y.free()
+    # RoPE + append + causal attention of T tokens from position 0
+    nh, nkv, hd = spec.n_heads, spec.n_kv_heads, spec.head_dim
+    ctx.kv_init(1, nkv, hd, T + 128, spec.rope_theta)
+    q, k, v = ctx.synth_normal(T * nh * hd, 1), ctx.synth_normal(T * nkv * hd, 2), ctx.synth_normal(T * nkv * hd, 3)
+    o = ctx.alloc(4 * T * nh * hd)
+    ctx.check(ctx.prefill_attention_dev(0, 0, T, nh, q, k, v, o), "prefill attention")
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        ctx.check(ctx.prefill_attention_dev(0, 0, T, nh, q, k, v, o), "prefill attention")
+    ctx.sync()
+    dt_s = (time.perf_counter() - t0) / iters
+    flop = 4.0 * nh * hd * T * (T + 1) / 2  # q.k and p.v over the causal triangle
+    emit(config=5, what=f"RoPE + append + causal attention, {T} tokens, 32 heads / 8 KV heads, hd 128",
+         us_per_layer=round(dt_s * 1e6, 2), gflop=round(flop / 1e9, 3), TFLOP_per_s=round(flop / dt_s / 1e12, 2))
+    for b in (q, k, v, o):
+        b.free()
+    ctx.close()
+    # forward() over a T-token prompt through the whole model
+    ctx = H.Context(0)
+    dm = H.DeviceModel(ctx, spec, T + 128)
+    toks = np.random.default_rng(5).integers(0, spec.vocab, T).astype(np.int32)
+    dm.prefill(toks, 0, want_logits=False)
+    best = None
+    for _ in range(3):
+        t0 = time.perf_counter()
+        nxt, _, _, dev_ms = dm.prefill(toks, 0, want_logits=False)
+        wall = time.perf_counter() - t0
+        best = wall if best is None else min(best, wall)
+    emit(config=5, what=f"forward() of a {T}-token prompt, 8B shape, 32 layers (prefill)", ms=round(best * 1e3, 3),
+         device_ms=round(dev_ms, 3), tok_per_s=round(T / best, 1), next_token=int(nxt))
+    ctx.close()
+
+
 def run_configs():
     ctx = H.Context(0)
     config1(ctx)
@@ -155,11 +220,14 @@ def main():
     c.add_argument("--mib", type=int, default=256)
     c.add_argument("--iters", type=int, default=20)
     sub.add_parser("configs")
+    sub.add_parser("config5")
     a = ap.parse_args()
     if a.cmd == "copy":
         run_copy(a.mib, a.iters)
     elif a.cmd == "configs":
         run_configs()
+    elif a.cmd == "config5":
+        config5(H.Context(0))
 
 
 if __name__ == "__main__":

@@ -246,13 +246,31 @@ int gq_hip_silu_mul_dev(gq_ctx *ctx, float *gate, const float *up, int n);
  * y[t][n] = sum_k x[t][k] w[n][k] for t < T tokens at once on the bf16
  * matrix cores, fp32 accumulation: the projections of a prefill chunk, which
  * the reference runs as T sequential matvecs (linear_dispatch,
- * engine.c:119-152).  w: rows x cols Q4_K on the device (rows % 128 == 0,
- * cols % 256 == 0); x: T x cols fp32, y: T x rows fp32, device pointers.
- * mode 0 stores, mode 1 adds r (T x rows, may alias y).  x and the
- * dequantized weights are rounded to bf16 (nearest even) before the
- * products.  Asynchronous on the context stream. */
+ * engine.c:119-152).  w: rows x cols Q4_K or Q6_K on the device
+ * (rows % 128 == 0, cols % 256 == 0); x: T x cols fp32, y: T x rows fp32,
+ * device pointers.  mode 0 stores, mode 1 adds r (T x rows, may alias y).
+ * x and the dequantized weights are rounded to bf16 (nearest even) before
+ * the products.  Asynchronous on the context stream. */
 int gq_hip_prefill_gemm_dev(gq_ctx *ctx, int dtype, int mode, const void *w, int rows, int cols,
                             const float *x, int T, float *y, const float *r);
+/* Steps 4-10 of transformer_layer for T tokens at pos .. pos+T-1
+ * (engine.c:372-509): RoPE of q (T x n_heads*hd, in place) and k
+ * (T x n_kv*hd), append of every token's k and v to the cache of `layer`,
+ * then causal attention, token t over positions 0 .. pos+t, into out
+ * (T x n_heads*hd).  Device pointers, asynchronous; -5 when pos+T passes
+ * the cache. */
+int gq_hip_prefill_attention_dev(gq_ctx *ctx, int layer, int pos, int T, int n_heads, float *q,
+                                 const float *k, const float *v, float *out);
+/* forward(model, kv, scr, tokens, n_tokens, pos) of the bound model
+ * (engine.c:559-595): the whole prompt through every layer in chunks of
+ * up to 512 tokens, filling the device KV cache at pos .. pos+n_tokens-1;
+ * the slot of gpu_prefill (gpu_prefill.h:13-20).  tokens and the optional
+ * outputs are host pointers: logits (vocab floats) and hidden_last (the
+ * last token's final hidden state before the final RMSNorm) of the last
+ * token, ms the device time.  Returns the greedy next token (>= 0) or a
+ * negative error (-5: positions outside the cache). */
+int gq_hip_prefill(gq_ctx *ctx, const int32_t *tokens, int n_tokens, int pos, float *logits,
+                   float *hidden_last, float *ms);
 /* Device-to-device copy by a plain streaming kernel (bytes and both pointers
  * multiples of 16), asynchronous.  No reference counterpart: the known-size
  * workload that scales the HBM byte counters of the profiles. */

@@ -1,20 +1,33 @@
-"""Prefill-chunk GEMM (config 5): Y = X W^T for T tokens on the bf16 matrix
-cores.  Two references on the same seeded inputs:
+"""The prefill chunk (config 5) on the GPU.
+
+GEMM, Y = X W^T for T tokens on the bf16 matrix cores; two references on the
+same seeded inputs:
 
 * exact-input reference: X and the dequantized weights rounded to bf16 the
-  way the kernel rounds them (dequant w = d sc q - dmin m rounded once to
-  fp32, then to bf16 nearest-even), products and sums in fp64.  Only the
-  kernel's fp32 accumulation order differs: tolerance 1e-5 relative L2.
-  This is what pins indexing, operand layouts and the Q4_K decode.
+  way the kernel rounds them (Q4_K: w = d sc q - dmin m rounded once to fp32;
+  Q6_K: w = (d sc) q, exact in fp32; then bf16 nearest-even), products and
+  sums in fp64.  Only the kernel's fp32 accumulation order differs:
+  tolerance 1e-5 relative L2.  This pins indexing, operand layouts and the
+  block decodes.
 * full-precision reference: fp64 GEMM of the fp32 X and the exactly
   dequantized weights (what the reference's T sequential fp32 matvecs
   approximate, engine.c:119-152).  bf16 inputs cost ~2^-9 relative per
-  product: tolerance 1e-2 relative L2 (observed ~3e-3)."""
+  product: tolerance 1e-2 relative L2 (observed ~3e-3).
+
+RoPE + append + causal attention of T tokens: the cache rows bit-exact with
+the oracle's RoPE, each token's attention bit-identical to the decode kernel
+at its position (the same arithmetic) and within 1e-5 of the oracle.
+
+Whole-model prefill (forward() over a prompt, engine.c:559-595) against T
+sequential oracle steps (bit-exact with the reference's forward()): the
+projections see bf16 inputs, so the last token's logits and the new cache
+rows are held to 3e-2 relative L2 (observed about 5e-3) and the next greedy
+token must agree."""
 import numpy as np
 import pytest
 
 from guanaco_amd import spec as S
-from util import dequant_q4k_f64, rel_l2
+from util import bits, dequant_q4k_f64, dequant_q6k_f64, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -54,21 +67,33 @@ SHAPES = [(64, 128, 256), (100, 256, 512), (512, 1024, 4096), (130, 384, 1024)]
 @pytest.mark.parametrize("T,N,K", SHAPES)
 @pytest.mark.parametrize("mode", [0, 1])
 def test_prefill_gemm(ctx, orc, T, N, K, mode):
+    _gemm_case(ctx, orc, S.Q4_K, T, N, K, mode)
+
+
+@pytest.mark.parametrize("T,N,K", [(64, 128, 256), (100, 256, 512), (512, 1024, 4096), (77, 384, 1536)])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_prefill_gemm_q6k(ctx, orc, T, N, K, mode):
+    _gemm_case(ctx, orc, S.Q6_K, T, N, K, mode)
+
+
+def _gemm_case(ctx, orc, dtype, T, N, K, mode):
     import guanaco_amd.hip as H
-    seed = (T << 20) ^ (N << 8) ^ K
-    w = orc.synth_quant(S.Q4_K, seed, N, K)
+    seed = (T << 20) ^ (N << 8) ^ K ^ (dtype << 28)
+    w = orc.synth_quant(dtype, seed, N, K)
     x = orc.synth_normal(seed + 1, T * K).reshape(T, K)
     r = orc.synth_normal(seed + 2, T * N).reshape(T, N)
     wd, xd = ctx.upload_weight(w), ctx.upload(x)
     yd = ctx.upload(r) if mode == 1 else ctx.alloc(4 * T * N)
-    rc = H.lib.gq_hip_prefill_gemm_dev(ctx.h, S.Q4_K, mode, wd, N, K, xd.ptr, T, yd.ptr,
+    rc = H.lib.gq_hip_prefill_gemm_dev(ctx.h, dtype, mode, wd, N, K, xd.ptr, T, yd.ptr,
                                        yd.ptr if mode == 1 else None)
     assert rc == 0
     y = yd.download(count=T * N).reshape(T, N)
     base = r.astype(np.float64) if mode == 1 else 0.0
-    exact_in = bf16_round(x).astype(np.float64) @ bf16_round(q4k_dequant_kernel_order(w, N, K)).astype(np.float64).T
+    wf = dequant_q4k_f64(w, N, K) if dtype == S.Q4_K else dequant_q6k_f64(w, N, K)
+    wk = q4k_dequant_kernel_order(w, N, K) if dtype == S.Q4_K else wf.astype(np.float32)
+    exact_in = bf16_round(x).astype(np.float64) @ bf16_round(wk).astype(np.float64).T
     assert rel_l2(y, base + exact_in) < 1e-5
-    full = x.astype(np.float64) @ dequant_q4k_f64(w, N, K).T
+    full = x.astype(np.float64) @ wf.T
     e = rel_l2(y - base, full)
     assert e < 1e-2, e
     H.lib.gq_hip_free(ctx.h, wd)
@@ -80,5 +105,107 @@ def test_prefill_gemm_rejects_bad_shapes(ctx):
     buf = ctx.alloc(1 << 20)
     assert H.lib.gq_hip_prefill_gemm_dev(ctx.h, S.Q4_K, 0, buf.ptr, 100, 256, buf.ptr, 4, buf.ptr, None) != 0
     assert H.lib.gq_hip_prefill_gemm_dev(ctx.h, S.Q4_K, 0, buf.ptr, 128, 300, buf.ptr, 4, buf.ptr, None) != 0
-    assert H.lib.gq_hip_prefill_gemm_dev(ctx.h, S.Q6_K, 0, buf.ptr, 128, 256, buf.ptr, 4, buf.ptr, None) != 0
+    assert H.lib.gq_hip_prefill_gemm_dev(ctx.h, S.Q8_0, 0, buf.ptr, 128, 256, buf.ptr, 4, buf.ptr, None) != 0
     buf.free()
+
+
+@pytest.mark.parametrize("nh,nkv,hd,pre,T,ms", [
+    (32, 8, 128, 0, 512, 640),     # config 5: a 512-token chunk from position 0
+    (32, 8, 128, 300, 200, 640),   # after a cached prefix, chunk boundary inside
+    (32, 4, 64, 5, 130, 160),      # TinyLlama shape, ends near the cache end
+    (8, 8, 64, 0, 3, 16),          # G = 1, three tokens
+])
+def test_prefill_attention(ctx, orc, nh, nkv, hd, pre, T, ms):
+    from oracle import HostKV, fptr
+    theta = 500000.0
+    ctx.kv_init(1, nkv, hd, ms, theta)
+    seed_k, seed_v = 0x5EED + pre, 0xFEED + T
+    if pre:
+        ctx.kv_prefill_synth(seed_k, seed_v, pre)
+    rng = np.random.default_rng(T * 1000 + pre)
+    q = rng.standard_normal((T, nh * hd)).astype(np.float32)
+    k = rng.standard_normal((T, nkv * hd)).astype(np.float32)
+    v = rng.standard_normal((T, nkv * hd)).astype(np.float32)
+    qb, kb, vb, ob = ctx.upload(q), ctx.upload(k), ctx.upload(v), ctx.alloc(4 * T * nh * hd)
+    assert ctx.prefill_attention_dev(0, pre, T, nh, qb, kb, vb, ob) == 0
+    out = ob.download(count=T * nh * hd).reshape(T, nh * hd)
+    qr = qb.download(count=T * nh * hd).reshape(T, nh * hd)
+    # RoPE and the appended rows bit-exact with the oracle
+    kv = HostKV(1, nkv, hd, ms)
+    for arr, seed in ((kv.k, seed_k), (kv.v, seed_v)):
+        orc.lib.orc_synth_kv(seed, fptr(arr), 1, nkv, hd, ms, pre)
+    kr = np.empty_like(k)
+    for t in range(T):
+        q2, k2 = orc.rope(q[t], k[t], nh, nkv, hd, pre + t, theta)
+        assert np.array_equal(bits(qr[t]), bits(q2)), t
+        kr[t] = k2
+    kvk, kvv = kv.k.reshape(nkv, ms, hd), kv.v.reshape(nkv, ms, hd)
+    kvk[:, pre:pre + T] = kr.reshape(T, nkv, hd).transpose(1, 0, 2)
+    kvv[:, pre:pre + T] = v.reshape(T, nkv, hd).transpose(1, 0, 2)
+    dk, dv = ctx.kv_read_layer(0)
+    assert np.array_equal(bits(dk), bits(kv.k)) and np.array_equal(bits(dv), bits(kv.v))
+    # each token: the decode kernel at its position bit for bit, the oracle to 1e-5
+    q1, o1 = ctx.alloc(4 * nh * hd), ctx.alloc(4 * nh * hd)
+    for t in sorted({0, 1, T // 2, T - 2, T - 1} & set(range(T))):
+        q1.upload(qr[t])
+        assert ctx.attention_dev(0, pre + t, nh, q1, o1) == 0
+        assert np.array_equal(bits(o1.download()), bits(out[t])), t
+        ref = orc.attention(qr[t], kv, 0, nh, pre + t)
+        assert rel_l2(out[t], ref) < 1e-5, t
+    for b in (qb, kb, vb, ob, q1, o1):
+        b.free()
+
+
+def test_prefill_attention_rejects_bad_positions(ctx):
+    ctx.kv_init(1, 2, 64, 32, 500000.0)
+    b = ctx.alloc(4 * 40 * 8 * 64)
+    assert ctx.prefill_attention_dev(0, 30, 3, 8, b, b, b, b) == -5
+    assert ctx.prefill_attention_dev(0, -1, 3, 8, b, b, b, b) == -5
+    assert ctx.prefill_attention_dev(0, 0, 0, 8, b, b, b, b) == -1
+    assert ctx.prefill_attention_dev(0, 0, 3, 7, b, b, b, b) == -1
+    b.free()
+
+
+PF_TOL = 3e-2
+
+
+@pytest.mark.parametrize("pre,T,ms", [(0, 48, 64), (24, 39, 64), (0, 600, 640)])
+def test_prefill_model_vs_oracle(ctx, orc, pre, T, ms):
+    """forward() over a T-token prompt at pos `pre` (the reference's own
+    prefill call, generate.c:200-226), then one decode step from it."""
+    import guanaco_amd.hip as H
+    from oracle import HostModel
+    from guanaco_amd.synth import tensor_seed
+    spec = S.TINY_TEST
+    hm = HostModel(orc, spec, ms)
+    dm = H.DeviceModel(ctx, spec, ms, prefill=pre)
+    kv = hm.new_kv()
+    if pre:
+        kv.prefill(orc, spec, pre)
+    rng = np.random.default_rng(T + pre)
+    toks = rng.integers(0, spec.vocab, T).astype(np.int32)
+    nxt, lg, hid, ms_dev = dm.prefill(toks, pre, want_hidden=True)
+    for t in range(T):
+        t_cpu, lc, _ = hm.forward(kv, int(toks[t]), pre + t)
+    assert rel_l2(lg, lc) < PF_TOL
+    assert nxt == t_cpu
+    for l in range(spec.n_layers):
+        dk, dv = ctx.kv_read_layer(l)
+        for d, h in ((dk, kv.view("k")[l]), (dv, kv.view("v")[l])):
+            d = d.reshape(h.shape)
+            assert np.array_equal(d[:, :pre], h[:, :pre])          # the cached prefix untouched
+            assert rel_l2(d[:, pre:pre + T], h[:, pre:pre + T]) < PF_TOL
+    # decode continues from the prefilled cache
+    t_gpu, lg2, _ = dm.forward(nxt, pre + T)
+    t_cpu2, lc2, _ = hm.forward(kv, t_cpu, pre + T)
+    assert rel_l2(lg2, lc2) < PF_TOL and t_gpu == t_cpu2
+    print(f"prefill T={T} pre={pre}: logits rel {rel_l2(lg, lc):.2e}, device {ms_dev:.3f} ms")
+
+
+def test_prefill_model_rejects_bad_input(ctx):
+    import guanaco_amd.hip as H
+    dm = H.DeviceModel(ctx, S.TINY_TEST, 64)
+    with pytest.raises(H.HipError):
+        dm.prefill(np.arange(10, dtype=np.int32), 60)      # past the cache
+    with pytest.raises(H.HipError):
+        dm.prefill(np.array([1, 2, 5000], np.int32), 0)    # token out of range
