@@ -242,7 +242,11 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
     float t = 0.f;
 #pragma unroll
     for (int k = 0; k < kThreads / 32; k++) t += sacc[k][tid];
-    gst<float>(a.out + (size_t)tz * a.out_stride + (size_t)h * a.hd + d, t / Ls);
+    const size_t o = (size_t)tz * a.out_stride + (size_t)h * a.hd + d;
+    if (a.out16)
+      gst<unsigned short>(a.out16 + o, __builtin_bit_cast(unsigned short, (__bf16)(t / Ls)));
+    else
+      gst<float>(a.out + o, t / Ls);
   }
 }
 

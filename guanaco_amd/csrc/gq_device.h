@@ -181,4 +181,58 @@ __device__ __forceinline__ gq_f32x2 gq_nib2f(uint32_t w) {
   return __builtin_amdgcn_cvt_pk_f32_fp8((int)w, HI);
 }
 
+/* Direct global -> LDS copies (no VGPRs): 16 or 4 bytes per lane, lane i at
+ * lds_addr + 16 i (or 4 i).  They are issued from inline assembly on purpose:
+ * the compiler's wait-count pass treats a visible LDS-DMA load as a write to
+ * every LDS location and would put s_waitcnt vmcnt(0) in front of each LDS
+ * read of a pipelined loop, draining the stages in flight.  Completion is
+ * tracked by hand (wait_vmcnt + barrier).  VMEM loads retire in order, so the
+ * compiler's own waits for other loads can only wait longer than needed,
+ * never less.  The LDS address goes in M0 (the "{m0}" operand: the compiler
+ * writes M0). */
+__device__ __forceinline__ void dma16(const void *src, uint32_t lds_addr) {
+  asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(lds_addr));
+}
+
+__device__ __forceinline__ void dma4(const void *src, uint32_t lds_addr) {
+  asm volatile("global_load_lds_dword %0, off" : : "v"(src), "{m0}"(lds_addr));
+}
+
+/* s_waitcnt vmcnt(n) with the other counters left alone (vmcnt(0) for n > 63). */
+__device__ __forceinline__ void wait_vmcnt(int n) {
+#define GQ_W(N)                                                                                   \
+  case N: __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | (7 << 4) | (15 << 8)); break;
+  switch (n) {
+    GQ_W(0) GQ_W(1) GQ_W(2) GQ_W(3) GQ_W(4) GQ_W(5) GQ_W(6) GQ_W(7) GQ_W(8) GQ_W(9) GQ_W(10)
+    GQ_W(11) GQ_W(12) GQ_W(13) GQ_W(14) GQ_W(15) GQ_W(16) GQ_W(17) GQ_W(18) GQ_W(19) GQ_W(20)
+    GQ_W(21) GQ_W(22) GQ_W(23) GQ_W(24) GQ_W(25) GQ_W(26) GQ_W(27) GQ_W(28) GQ_W(29) GQ_W(30)
+    GQ_W(31) GQ_W(32) GQ_W(33) GQ_W(34) GQ_W(35) GQ_W(36) GQ_W(37) GQ_W(38) GQ_W(39) GQ_W(40)
+    GQ_W(41) GQ_W(42) GQ_W(43) GQ_W(44) GQ_W(45) GQ_W(46) GQ_W(47) GQ_W(48) GQ_W(49) GQ_W(50)
+    GQ_W(51) GQ_W(52) GQ_W(53) GQ_W(54) GQ_W(55) GQ_W(56) GQ_W(57) GQ_W(58) GQ_W(59) GQ_W(60)
+    GQ_W(61) GQ_W(62) GQ_W(63)
+  default: __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); break; /* vmcnt(0) */
+  }
+#undef GQ_W
+}
+
+/* s_waitcnt vmcnt(N) for a compile-time N */
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_c() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+/* vmcnt(min(ahead, A) * NPS): ahead groups of NPS loads may stay in flight */
+template <int NPS, int A>
+__device__ __forceinline__ void wait_groups(int ahead) {
+  if constexpr (A == 0) {
+    wait_vmcnt_c<0>();
+  } else {
+    if (ahead >= A)
+      wait_vmcnt_c<A * NPS>();
+    else
+      wait_groups<NPS, A - 1>(ahead);
+  }
+}
+
 #endif

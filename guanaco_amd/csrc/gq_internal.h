@@ -77,6 +77,7 @@ struct AttnArgs {
    * launches leave these zero (one token). */
   int ntok, q_stride, out_stride;
   size_t po_stride, pml_stride;
+  __bf16 *out16; /* chunk form: bf16 output (stride out_stride) instead of out */
 };
 int gq_attn_nch(int n_kv, int max_seq);
 int gq_attn_smax(int max_seq, int nch);
@@ -114,14 +115,28 @@ int gq_launch_silu_mul(float *gate, const float *up, int n, hipStream_t s);
 int gq_launch_copy(void *dst, const void *src, size_t bytes, int n_cu, hipStream_t s);
 
 /* ---- prefill chunk ---------------------------------------------------
- * Y[T][N] = X[T][K] . W^T on the bf16 matrix cores (W: N rows of Q4_K or
- * Q6_K, X fp32 row-major); MV_STORE or MV_RESID (Y = R + X W^T, R may alias
- * Y).  Needs N % 128 == 0 and K % 256 == 0. */
-int gq_launch_prefill_gemm(int dtype, int mode, const float *X, const void *W, float *Y, const float *R, int T,
-                           int N, int K, hipStream_t s);
-/* RMSNorm of `rows` consecutive rows of dim floats, one workgroup per row */
+ * Y[T][rows] = X[T][K] . W^T on the bf16 matrix cores for up to three weight
+ * segments in one launch (each rows % 128 == 0, Q4_K, or Q6_K with
+ * K % 512 == 0), X bf16 row-major.  MV_STORE writes y, MV_RESID adds into
+ * y; MV_SWIGLU takes gate (seg 0) and up (seg 1) of equal rows
+ * (rows % 64 == 0) and writes act[T][rows] = bf16(silu(gate) * up). */
+struct PgSeg {
+  const uint8_t *w;
+  float *y;
+  int rows, dtype;
+};
+struct PgArgs {
+  const __bf16 *x;
+  __bf16 *act;
+  PgSeg seg[3];
+  int nseg, T, K;
+};
+int gq_launch_pgemm(int mode, const PgArgs &a, hipStream_t s);
+int gq_launch_to_bf16(const float *x, __bf16 *y, size_t n, hipStream_t s);
+/* RMSNorm of `rows` consecutive rows of dim floats, one workgroup per row;
+ * out16 != NULL writes bf16 there instead of fp32 to out */
 int gq_launch_rmsnorm_rows(const float *x, const float *w, float *out, int dim, int rows, float eps,
-                           hipStream_t s);
+                           hipStream_t s, __bf16 *out16 = nullptr);
 /* embedding rows of tokens[0..n) (device array) into out (n x hidden) */
 int gq_launch_embed_rows(int dtype, const void *table, int hidden, const int *tokens_dev, int n, float *out,
                          hipStream_t s);

@@ -690,17 +690,8 @@ __device__ __forceinline__ int copy_count(int nbytes, int wave, int nwv = kWaves
   return wave < ng ? (ng - wave + nwv - 1) / nwv : 0;
 }
 
-/* The DMA loads are issued from inline assembly on purpose: the compiler's
- * wait-count pass treats a visible LDS-DMA load as a write to every LDS
- * location and would put s_waitcnt vmcnt(0) in front of each LDS read of the
- * compute loop, draining the stages in flight.  Completion is tracked by hand
- * (wait_vmcnt + barrier).  VMEM loads retire in order, so the compiler's own
- * waits for other loads can only wait longer than needed, never less.  The
- * LDS address goes in M0 (the "{m0}" operand: the compiler writes M0). */
-__device__ __forceinline__ void dma16(const uint8_t *src, uint32_t lds_addr) {
-  asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(lds_addr));
-}
-
+/* Rows [src, src + nbytes) into LDS at dst by 16-byte DMA (dma16), 1 KB per
+ * wave instruction, instructions dealt round-robin over nwv waves. */
 __device__ __forceinline__ void copy_range(const uint8_t *src, int nbytes, GQ_LDS uint8_t *dst, int wave,
                                            int lane, int nwv = kWaves) {
   const int nchunk = nbytes / 16, ng = (nchunk + 63) / 64;
@@ -712,10 +703,6 @@ __device__ __forceinline__ void copy_range(const uint8_t *src, int nbytes, GQ_LD
   }
 }
 
-/* One dword per lane into LDS (the residual rows of a stage). */
-__device__ __forceinline__ void dma4(const float *src, uint32_t lds_addr) {
-  asm volatile("global_load_lds_dword %0, off" : : "v"(src), "{m0}"(lds_addr));
-}
 
 /* Stage `g`'s rows: global rows [g*rs, g*rs+rs) (clamped to the end of their
  * segment), or for MV_SWIGLU gate and up rows [g*rs/2, g*rs/2 + rs/2); for
@@ -746,22 +733,6 @@ __device__ __forceinline__ int issue_stage(const MvArgs &a, const MvPlan &pl, in
   return c;
 }
 
-/* s_waitcnt vmcnt(n) with the other counters left alone (vmcnt(0) for n > 63). */
-__device__ __forceinline__ void wait_vmcnt(int n) {
-#define GQ_W(N)                                                                                   \
-  case N: __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | (7 << 4) | (15 << 8)); break;
-  switch (n) {
-    GQ_W(0) GQ_W(1) GQ_W(2) GQ_W(3) GQ_W(4) GQ_W(5) GQ_W(6) GQ_W(7) GQ_W(8) GQ_W(9) GQ_W(10)
-    GQ_W(11) GQ_W(12) GQ_W(13) GQ_W(14) GQ_W(15) GQ_W(16) GQ_W(17) GQ_W(18) GQ_W(19) GQ_W(20)
-    GQ_W(21) GQ_W(22) GQ_W(23) GQ_W(24) GQ_W(25) GQ_W(26) GQ_W(27) GQ_W(28) GQ_W(29) GQ_W(30)
-    GQ_W(31) GQ_W(32) GQ_W(33) GQ_W(34) GQ_W(35) GQ_W(36) GQ_W(37) GQ_W(38) GQ_W(39) GQ_W(40)
-    GQ_W(41) GQ_W(42) GQ_W(43) GQ_W(44) GQ_W(45) GQ_W(46) GQ_W(47) GQ_W(48) GQ_W(49) GQ_W(50)
-    GQ_W(51) GQ_W(52) GQ_W(53) GQ_W(54) GQ_W(55) GQ_W(56) GQ_W(57) GQ_W(58) GQ_W(59) GQ_W(60)
-    GQ_W(61) GQ_W(62) GQ_W(63)
-  default: __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); break; /* vmcnt(0) */
-  }
-#undef GQ_W
-}
 
 /* Store one finished output row `lr` of segment `s` (`s` is the same for the
  * whole stage: a stage never straddles segments).  No vector global loads

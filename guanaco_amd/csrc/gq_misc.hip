@@ -16,11 +16,12 @@ constexpr int kThreads = 256;
 /* out = w * (x * 1/sqrt(mean(x^2) + eps)) (kernels_cpu.c:199-265); one
  * workgroup per row (blockIdx.x), sum of squares in a fixed tree order. */
 __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *x, const float *w, float *out,
-                                                          int dim, float eps) {
+                                                          int dim, float eps, __bf16 *out16) {
   __shared__ float red[kThreads / GQ_WAVE];
   const int tid = threadIdx.x;
   x += (size_t)blockIdx.x * dim;
   out += (size_t)blockIdx.x * dim;
+  if (out16) out16 += (size_t)blockIdx.x * dim;
   float ss = 0.f;
   for (int i = tid; i < dim; i += kThreads) ss = __builtin_fmaf(x[i], x[i], ss);
   ss = gq_wave_sum(ss);
@@ -30,7 +31,13 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *x, const
   tot = tot / (float)dim;
   tot = tot + eps;
   const float r = 1.0f / sqrtf(tot);
-  for (int i = tid; i < dim; i += kThreads) out[i] = (w ? w[i] : 1.0f) * (x[i] * r);
+  for (int i = tid; i < dim; i += kThreads) {
+    const float v = (w ? w[i] : 1.0f) * (x[i] * r);
+    if (out16)
+      out16[i] = (__bf16)v;
+    else
+      out[i] = v;
+  }
 }
 
 /* Embedding row of `token` (engine.c:214-283): F32 copy, Q8_0 q*scale,
@@ -184,9 +191,9 @@ int gq_launch_rmsnorm(const float *x, const float *w, float *out, int dim, float
 }
 
 int gq_launch_rmsnorm_rows(const float *x, const float *w, float *out, int dim, int rows, float eps,
-                           hipStream_t s) {
+                           hipStream_t s, __bf16 *out16) {
   if (rows <= 0 || dim <= 0) return -1;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, s, x, w, out, dim, eps);
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, s, x, w, out, dim, eps, out16);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 

@@ -6,22 +6,34 @@
  * The reference computes a prefill projection as T sequential matvecs
  * (linear_dispatch, engine.c:119-152).  Here Y[T][N] = X[T][K] . W^T for
  * all T tokens in one launch, where W is N rows of Q4_K blocks
- * (quant_matvec_q4_k.c:9-16) or Q6_K blocks (quant_matvec_q6_k.c), X fp32
- * row-major.
+ * (quant_matvec_q4_k.c:9-16) or Q6_K blocks (quant_matvec_q6_k.c:5-12) and
+ * X is bf16 row-major (its producer rounds it: RMSNorm, the attention merge,
+ * the gate/up epilogue, or the fp32 -> bf16 pass of the op-level entry).
  *
- * Workgroup tile: 64 tokens x 128 weight rows, 4 waves in a 2 x 2 grid, each
- * wave 32 tokens x 64 rows = two 32x32 tiles of v_mfma_f32_32x32x16_bf16.
- * K advances 64 weights per step: one 32-byte quant chunk per row, i.e. two
- * Q4_K sub-blocks, or two 32-weight groups of a Q6_K half-block.  Per step
- * the workgroup converts its X tile to bf16 (round to nearest even) and
- * dequantizes its W tile into LDS (Q4_K: w = d sc q - dmin m in fp32, Q6_K:
- * w = (d sc) q, exact in fp32; then bf16); the next step's global loads are
- * in flight while the current step's MFMAs run (double-buffered LDS).
+ * Workgroup tile: 64 tokens x 128 weight rows, 4 waves; wave w owns rows
+ * 32w .. 32w+31 of the tile for all 64 tokens, i.e. two 32x32 tiles of
+ * v_mfma_f32_32x32x16_bf16.  K advances 64 weights per step: one Q4_K chunk
+ * of two sub-blocks, or two 32-weight groups of a Q6_K half-block.
+ *
+ * Every step's inputs stream into an LDS ring kRing - 1 steps ahead by direct
+ * global -> LDS DMA (no VGPRs, no VALU):
+ *   X  8 KB per step: each DMA instruction moves 8 tokens' whole 128-byte
+ *      k-slices (8 full cache lines), stored [token][k-octet] with the
+ *      octet position XOR-swizzled by (token / 2) % 8, so each MFMA A
+ *      operand (32 tokens, one octet) is a conflict-free ds_read_b128;
+ *   W  each wave's own 32 rows, raw block bytes (Q4_K: header + the 32 quant
+ *      bytes of the chunk; Q6_K: a dword-aligned window over ql, qh, scales
+ *      and d of the half-block).
+ * Each lane dequantizes exactly the 32 weights of its own B operands (its
+ * row, its k-octets), so a weight is converted once per token tile and never
+ * round-trips through LDS in bf16.  One barrier per step.
  *
  * MFMA operand layout (32x32x16, checked on the device): A[i][k] is element
  * k % 8 of lane i + 32 (k / 8); B[k][j] element k % 8 of lane j + 32 (k / 8);
  * D[i][j] element 4 (i / 8) + i % 4 of lane j + 32 ((i / 4) % 2).
  */
+#include <algorithm>
+
 #include "gq_device.h"
 #include "gq_internal.h"
 
@@ -32,228 +44,410 @@ typedef float gq_f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kPThreads = 256;
 constexpr int kBM = 64, kBN = 128, kBK = 64;
-constexpr int kLdK = kBK + 8; /* bf16 per LDS row: +8 staggers the banks */
+constexpr int kXBytes = kBM * kBK * 2; /* X bytes per step */
 
+typedef float gq_f2 __attribute__((ext_vector_type(2)));
+typedef __bf16 gq_bf2 __attribute__((ext_vector_type(2)));
+
+/* two floats to a bf16 pair, round to nearest even: one v_cvt_pk_bf16_f32 */
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  const __bf16 a = (__bf16)lo, b = (__bf16)hi; /* round to nearest even */
-  return (uint32_t)__builtin_bit_cast(unsigned short, a) | ((uint32_t)__builtin_bit_cast(unsigned short, b) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((gq_f2){lo, hi}, gq_bf2));
 }
 
-/* 16 bytes from a 2-byte-aligned address: five dword loads funnel-shifted
- * (the 4 bytes past the 16 stay inside the Q6_K block for every use here) */
-__device__ __forceinline__ uint4 gld16_a2(const uint8_t *p) {
-  typedef unsigned int N4 __attribute__((ext_vector_type(4), aligned(4)));
-  const uintptr_t a = (uintptr_t)p, b = a & ~(uintptr_t)3;
-  const N4 w = *(const GQ_GLOBAL N4 *)b;
-  const uint32_t e = *(const GQ_GLOBAL unsigned int *)(b + 16);
-  const uint32_t sh = (uint32_t)(a & 3u);
-  return make_uint4(__builtin_amdgcn_alignbyte(w.y, w.x, sh), __builtin_amdgcn_alignbyte(w.z, w.y, sh),
-                    __builtin_amdgcn_alignbyte(w.w, w.z, sh), __builtin_amdgcn_alignbyte(e, w.w, sh));
-}
-
-__device__ __forceinline__ uint32_t gld_u8(const uint8_t *p) { return *(const GQ_GLOBAL uint8_t *)p; }
-
-/* Per-thread W slice of one step: row tid / 2 of the tile, 16 weights of
- * each of the step's two 32-weight groups (half hf = tid & 1).  dequant()
- * returns them as bf16 pairs: lo[] for k = 16 hf + i, hq[] for
- * k = 32 + 16 hf + i. */
+/* Per-dtype W staging.  Lane (row r = lane % 32 of the wave's 32, h =
+ * lane / 32) builds B operands b[kk] = its row's weights k = 16 kk + 8 h + i
+ * (i < 8) of the step's 64. */
 template <int DT>
 struct PW;
 
+/* Q4_K: per row and step 48 bytes in LDS: the 16-byte block header, then
+ * the 32 quant bytes of chunk cc = s % 4 (weights 64 cc .. 64 cc + 63 of the
+ * super-block: sub-block 2cc in the low nibbles, 2cc+1 in the high ones). */
 template <>
 struct PW<GQ_Q4_K> {
   static constexpr int BB = 144;
-  struct Raw {
-    uint4 q, h;
+  static constexpr int kRowLds = 48;
+  static constexpr int kWaveLds = 2048; /* two 1-KB DMA instructions (96 pieces used) */
+  static constexpr int kDma = 2;        /* W DMA instructions per wave and step */
+  struct Plan {
+    uint32_t off[2]; /* per instruction: row * rowbytes + offset in the block */
+    bool qs[2];      /* quant bytes (move with the chunk) or header */
+    bool on[2];
   };
-  /* chunk cc = s % 4 of super-block s / 4: qs bytes 32 cc + 16 hf .. + 15 */
-  __device__ static void load(Raw &r, const uint8_t *blk, int cc, int hf) {
-    r.h = gld<uint4>(blk);
-    r.q = gld<uint4>(blk + 16 + 32 * cc + 16 * hf);
+  __device__ static void plan(Plan &p, int lane, uint32_t rowbytes) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int pc = 64 * i + lane, row = pc / 3, part = pc - 3 * row;
+      p.on[i] = pc < 96;
+      p.qs[i] = part != 0;
+      p.off[i] = (uint32_t)row * rowbytes + (part ? 16u * (uint32_t)part : 0u);
+    }
   }
-  /* sub-blocks 2cc (low nibbles) and 2cc+1 (high nibbles); scale/min decode
-   * as in the matvec (quant_matvec_q4_k.c:47-56) */
-  __device__ static void dequant(const Raw &st, int cc, uint32_t lo[8], uint32_t hq[8]) {
-    const float d = gq_h2f(st.h.x), dm = gq_h2f(st.h.x >> 16);
+  __device__ static void issue(const Plan &p, const uint8_t *w, int s, uint32_t lds) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const uint8_t *src = w + p.off[i] + (size_t)(s >> 2) * BB + (p.qs[i] ? 32 * (s & 3) : 0);
+      const uint32_t d = __builtin_amdgcn_readfirstlane(lds + 1024u * i);
+      if (p.on[i]) dma16(src, d);
+    }
+  }
+  /* scale/min decode as in the matvec (quant_matvec_q4_k.c:47-56); weight
+   * fp32(d sc q - dmin m) with one rounding (the fma), then bf16.  Nibbles go
+   * to float as OCP E4M3 (exactly q 2^-9), the 2^9 folded into d sc. */
+  struct Raw {
+    uint4 hd;
+    uint2 q0, q1;
+  };
+  __device__ static void read(Raw &w, const GQ_LDS uint8_t *ws, int lane, int s) {
+    const uint32_t r = (uint32_t)(lane & 31), h = (uint32_t)(lane >> 5);
+    (void)s;
+    w.hd = lld<uint4>(ws, r * kRowLds);
+    w.q0 = lld<uint2>(ws, r * kRowLds + 16u + 8u * h);
+    w.q1 = lld<uint2>(ws, r * kRowLds + 32u + 8u * h);
+  }
+  __device__ static void dequant(const Raw &rw, int s, gq_bf16x8 b[4]) {
+    const uint4 hd = rw.hd;
+    const uint2 q0 = rw.q0, q1 = rw.q1;
+    const int cc = s & 3;
+    const float d = gq_h2f(hd.x), dm = gq_h2f(hd.x >> 16);
     const uint32_t sh = 16u * (uint32_t)(cc & 1);
     const bool hi = cc >= 2;
-    const uint32_t y = st.h.y >> sh, z = st.h.z >> sh, w = st.h.w >> sh;
+    const uint32_t y = hd.y >> sh, z = hd.z >> sh, w = hd.w >> sh;
     const uint32_t mlo = hi ? 0x0f0fu : 0x3f3fu, mhi = hi ? 0x3030u : 0u;
     const uint32_t S = ((hi ? w : y) & mlo) | ((y >> 2) & mhi);
     const uint32_t M = ((hi ? (w >> 4) : z) & mlo) | ((z >> 2) & mhi);
     const float a0 = d * (float)(S & 0xffu), m0 = dm * (float)(M & 0xffu);
     const float a1 = d * (float)((S >> 8) & 0xffu), m1 = dm * (float)((M >> 8) & 0xffu);
-    const uint32_t qw[4] = {st.q.x, st.q.y, st.q.z, st.q.w};
+    const float A0 = a0 * 512.0f, A1 = a1 * 512.0f;
+    const uint32_t src[4][2] = {{q0.x, q0.y}, {q1.x, q1.y}, {q0.x >> 4, q0.y >> 4}, {q1.x >> 4, q1.y >> 4}};
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      float v[8];
+    for (int kk = 0; kk < 4; kk++) {
+      const float A = kk < 2 ? A0 : A1, m = kk < 2 ? m0 : m1;
+      uint32_t o[4];
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        v[j] = __builtin_fmaf(a0, (float)((qw[k] >> (8 * j)) & 15u), -m0);
-        v[4 + j] = __builtin_fmaf(a1, (float)((qw[k] >> (8 * j + 4)) & 15u), -m1);
+      for (int k = 0; k < 2; k++) {
+        const uint32_t n = src[kk][k] & 0x0f0f0f0fu;
+        const gq_f32x2 f0 = gq_nib2f<false>(n), f1 = gq_nib2f<true>(n);
+        o[2 * k] = pack_bf16x2(__builtin_fmaf(A, f0.x, -m), __builtin_fmaf(A, f0.y, -m));
+        o[2 * k + 1] = pack_bf16x2(__builtin_fmaf(A, f1.x, -m), __builtin_fmaf(A, f1.y, -m));
       }
-      lo[2 * k] = pack_bf16x2(v[0], v[1]), lo[2 * k + 1] = pack_bf16x2(v[2], v[3]);
-      hq[2 * k] = pack_bf16x2(v[4], v[5]), hq[2 * k + 1] = pack_bf16x2(v[6], v[7]);
+      b[kk] = __builtin_bit_cast(gq_bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
     }
   }
 };
 
-/* Q6_K block (quant_matvec_q6_k.c): ql[128], qh[64], int8 scales[16], fp16
- * d.  Weight 128 n + 32 g + l (half n, group g < 4, l < 32) has
- * q = (ql[64 n + 32 (g & 1) + l] >> 4 (g >> 1)) & 15
- *     | ((qh[32 n + l] >> 2 g) & 3) << 4,  minus 32,
- * scale scales[8 n + 2 g + l / 16].  Step chunk cc = 2 n + par holds groups
- * 2 par and 2 par + 1 of half n. */
+/* Q6_K (quant_matvec_q6_k.c:70-90): weight 128 n + 32 g + l (half n, group
+ * g < 4, l < 32) has q = (ql[64 n + 32 (g & 1) + l] >> 4 (g >> 1)) & 15
+ * | ((qh[32 n + l] >> 2 g) & 3) << 4, minus 32, scale scales[8 n + 2 g +
+ * l / 16]; w = (d sc) q, exact in fp32.  Step chunk cc = 2 n + par holds
+ * groups 2 par and 2 par + 1 of half n.  Blocks are 210 bytes, so only
+ * 2-byte aligned; rows are 4-byte aligned (cols % 512 == 0).  Per row and
+ * step 30 dwords of the block window aligned down to 4 bytes, in LDS as
+ *   ql[64 n - sh ..] 17 dwords | qh[32 n - sh ..] 9 | scales[8 n - sh ..] 3
+ *   | d 1,   sh = block offset & 3 (0 or 2). */
 template <>
 struct PW<GQ_Q6_K> {
   static constexpr int BB = 210;
-  struct Raw {
-    uint4 a, b, h;
-    uint32_t sd; /* scale of group 2par | scale of group 2par+1 << 8 | d << 16 */
+  static constexpr int kRowLds = 120;
+  static constexpr int kWaveLds = 15 * 256; /* 15 dword instructions */
+  static constexpr int kDma = 15;
+  struct Plan {
+    uint32_t off[15]; /* row * rowbytes + 4 * window dword (half 0) */
+    uint32_t dn[15];  /* extra bytes for half 1 */
   };
-  __device__ static void load(Raw &r, const uint8_t *blk, int cc, int hf) {
-    const int n = cc >> 1, par = cc & 1;
-    r.a = gld16_a2(blk + 64 * n + 16 * hf);
-    r.b = gld16_a2(blk + 64 * n + 32 + 16 * hf);
-    r.h = gld16_a2(blk + 128 + 32 * n + 16 * hf);
-    const uint8_t *sc = blk + 192 + 8 * n + 4 * par + hf;
-    r.sd = gld_u8(sc) | (gld_u8(sc + 2) << 8) | ((uint32_t)gld<uint16_t>(blk + 208) << 16);
+  __device__ static void plan(Plan &p, int lane, uint32_t rowbytes) {
+#pragma unroll
+    for (int i = 0; i < 15; i++) {
+      const int dw = 64 * i + lane, row = dw / 30, w = dw - 30 * row;
+      const int idx = w < 17 ? w : w < 26 ? 32 + (w - 17) : w < 29 ? 48 + (w - 26) : 52;
+      p.off[i] = (uint32_t)row * rowbytes + 4u * (uint32_t)idx;
+      p.dn[i] = w < 17 ? 64u : w < 26 ? 32u : w < 29 ? 8u : 0u;
+    }
   }
-  __device__ static void dequant(const Raw &st, int cc, uint32_t lo[8], uint32_t hq[8]) {
-    const uint32_t sa = 4u * (uint32_t)(cc & 1);
-    const float d = gq_h2f(st.sd >> 16);
-    const float a0 = d * (float)(int8_t)(st.sd & 0xffu), a1 = d * (float)(int8_t)((st.sd >> 8) & 0xffu);
-    const uint32_t A[4] = {st.a.x, st.a.y, st.a.z, st.a.w}, B[4] = {st.b.x, st.b.y, st.b.z, st.b.w};
-    const uint32_t H[4] = {st.h.x, st.h.y, st.h.z, st.h.w};
+  __device__ static void issue(const Plan &p, const uint8_t *w, int s, uint32_t lds) {
+    const size_t blk = ((size_t)(s >> 2) * BB) & ~(size_t)3;
+    const bool n1 = (s & 2) != 0;
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const uint32_t u0 = ((A[k] >> sa) & 0x0f0f0f0fu) | (((H[k] >> sa) & 0x03030303u) << 4);
-      const uint32_t u1 = ((B[k] >> sa) & 0x0f0f0f0fu) | (((H[k] >> (sa + 2)) & 0x03030303u) << 4);
-      float v[8];
+    for (int i = 0; i < 15; i++) {
+      const uint32_t d = __builtin_amdgcn_readfirstlane(lds + 256u * i);
+      dma4(w + blk + p.off[i] + (n1 ? p.dn[i] : 0u), d);
+    }
+  }
+  struct Raw {
+    uint2 P[4], H0, H1;
+    uint32_t sc, d;
+  };
+  __device__ static void read(Raw &w, const GQ_LDS uint8_t *ws, int lane, int s) {
+    const uint32_t r = (uint32_t)(lane & 31), h = (uint32_t)(lane >> 5);
+    const uint32_t sh = 2u * (uint32_t)((s >> 2) & 1), par = (uint32_t)(s & 1);
+    const uint32_t base = r * kRowLds + sh;
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        v[j] = a0 * (float)((int)((u0 >> (8 * j)) & 63u) - 32);
-        v[4 + j] = a1 * (float)((int)((u1 >> (8 * j)) & 63u) - 32);
+    for (int k = 0; k < 4; k++) w.P[k] = lld8_a2(ws, base + 16u * k + 8u * h);
+    w.H0 = lld8_a2(ws, base + 68u + 8u * h);
+    w.H1 = lld8_a2(ws, base + 84u + 8u * h);
+    w.sc = lld8_a2(ws, base + 104u + 4u * par).x;
+    w.d = lld<uint16_t>(ws, base + 116u);
+  }
+  __device__ static void dequant(const Raw &rw, int s, gq_bf16x8 b[4]) {
+    const uint32_t par = (uint32_t)(s & 1);
+    const uint2 *P = rw.P, H0 = rw.H0, H1 = rw.H1;
+    const uint32_t sc = rw.sc;
+    const float d = gq_h2f(rw.d);
+    const uint32_t sa = 4u * par;
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+      const uint2 Hq = (kk & 1) ? H1 : H0;
+      const uint32_t hs = sa + ((kk >= 2) ? 2u : 0u);
+      const float a = d * (float)(int8_t)((sc >> (8 * kk)) & 0xffu);
+      const float m = 32.0f * a;
+      const uint32_t pw[2] = {P[kk].x, P[kk].y}, hw[2] = {Hq.x, Hq.y};
+      uint32_t o[4];
+#pragma unroll
+      for (int k = 0; k < 2; k++) {
+        const uint32_t u = ((pw[k] >> sa) & 0x0f0f0f0fu) | (((hw[k] >> hs) & 0x03030303u) << 4);
+        const float v0 = __builtin_fmaf(a, (float)(u & 0xffu), -m);
+        const float v1 = __builtin_fmaf(a, (float)((u >> 8) & 0xffu), -m);
+        const float v2 = __builtin_fmaf(a, (float)((u >> 16) & 0xffu), -m);
+        const float v3 = __builtin_fmaf(a, (float)(u >> 24), -m);
+        o[2 * k] = pack_bf16x2(v0, v1);
+        o[2 * k + 1] = pack_bf16x2(v2, v3);
       }
-      lo[2 * k] = pack_bf16x2(v[0], v[1]), lo[2 * k + 1] = pack_bf16x2(v[2], v[3]);
-      hq[2 * k] = pack_bf16x2(v[4], v[5]), hq[2 * k + 1] = pack_bf16x2(v[6], v[7]);
+      b[kk] = __builtin_bit_cast(gq_bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
     }
   }
 };
 
-/* Per-step register staging: X (4 float4 per thread) and the W slice. */
 template <int DT>
-struct Stage {
-  float4 x[4];
-  typename PW<DT>::Raw w;
-};
-
-template <int DT>
-__device__ __forceinline__ void load_stage(Stage<DT> &st, const float *X, int T, int K, const uint8_t *W,
-                                           int t0, int n0, int s) {
-  const int tid = threadIdx.x;
-  /* X tile: 64 tokens x 64 fp32 = 1024 float4, 4 per thread */
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int f = tid + i * kPThreads, t = f >> 4, c = f & 15;
-    const int tt = min(t0 + t, T - 1);
-    st.x[i] = gld<float4>(X + (size_t)tt * K + s * kBK + 4 * c);
-  }
-  const int r = tid >> 1, hf = tid & 1;
-  const size_t rowbytes = (size_t)(K / 256) * PW<DT>::BB;
-  PW<DT>::load(st.w, W + (size_t)(n0 + r) * rowbytes + (size_t)(s >> 2) * PW<DT>::BB, s & 3, hf);
+constexpr int stage_bytes() {
+  return kXBytes + 4 * PW<DT>::kWaveLds;
 }
 
+/* Steps in the LDS ring: as deep as LDS and the 6-bit vmcnt allow (each
+ * wave keeps (ring - 2) steps of DMA instructions in flight while it waits) */
 template <int DT>
-__device__ __forceinline__ void store_stage(const Stage<DT> &st, GQ_LDS uint8_t *As, GQ_LDS uint8_t *Bs, int s) {
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int f = tid + i * kPThreads, t = f >> 4, c = f & 15;
-    uint2 v;
-    v.x = pack_bf16x2(st.x[i].x, st.x[i].y);
-    v.y = pack_bf16x2(st.x[i].z, st.x[i].w);
-    lst<uint2>(As, (uint32_t)(t * kLdK + 4 * c) * 2u, v);
-  }
-  const int r = tid >> 1, hf = tid & 1;
-  uint32_t lo[8], hq[8];
-  PW<DT>::dequant(st.w, s & 3, lo, hq);
-  /* weights 16 hf + i of the first group land at k 16 hf + i, those of the
-   * second at k 32 + 16 hf + i */
-  const uint32_t base = (uint32_t)(r * kLdK) * 2u;
-  lst<uint4>(Bs, base + (uint32_t)(16 * hf) * 2u, make_uint4(lo[0], lo[1], lo[2], lo[3]));
-  lst<uint4>(Bs, base + (uint32_t)(16 * hf + 8) * 2u, make_uint4(lo[4], lo[5], lo[6], lo[7]));
-  lst<uint4>(Bs, base + (uint32_t)(32 + 16 * hf) * 2u, make_uint4(hq[0], hq[1], hq[2], hq[3]));
-  lst<uint4>(Bs, base + (uint32_t)(32 + 16 * hf + 8) * 2u, make_uint4(hq[4], hq[5], hq[6], hq[7]));
+constexpr int ring() {
+  return DT == GQ_Q4_K ? 4 : 4;
 }
+template <int DT>
+constexpr int ring_bytes() {
+  return ring<DT>() * stage_bytes<DT>();
+}
+static_assert(ring<GQ_Q4_K>() >= 3 && ring<GQ_Q6_K>() >= 3, "the pipeline reads two slots");
+static_assert((ring<GQ_Q4_K>() - 2) * (2 + PW<GQ_Q4_K>::kDma) < 64, "vmcnt range");
+static_assert((ring<GQ_Q6_K>() - 2) * (2 + PW<GQ_Q6_K>::kDma) < 64, "vmcnt range");
 
-template <int DT, int MODE>
-__global__ __launch_bounds__(kPThreads) void prefill_gemm_kernel(const float *X, const uint8_t *W, float *Y,
-                                                                const float *R, int T, int N, int K) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2][(kBM + kBN) * kLdK * 2];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int n0 = blockIdx.x * kBN, t0 = blockIdx.y * kBM;
-  const int nsteps = K / kBK;
-  gq_f32x16 acc[2] = {};
-  Stage<DT> st;
-  load_stage<DT>(st, X, T, K, W, t0, n0, 0);
+/* One tile: tokens t0 .. t0+63 against this wave's 32 rows starting at w.
+ * acc[i] holds tokens t0 + 32 i + (D layout rows) for row (lane & 31). */
+template <int DT>
+__device__ __forceinline__ void tile_loop(const PgArgs &a, const uint8_t *w, uint32_t rowbytes, int t0,
+                                          GQ_LDS uint8_t *smem, gq_f32x16 acc[2]) {
+  constexpr int SB = stage_bytes<DT>();
+  constexpr int NPS = 2 + PW<DT>::kDma; /* DMA instructions per wave and step */
+  constexpr int kRing = ring<DT>();
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nsteps = a.K / kBK;
+  typename PW<DT>::Plan pl;
+  PW<DT>::plan(pl, lane, rowbytes);
+  const uint32_t sbase = (uint32_t)(uintptr_t)smem;
+  /* X DMA: instruction j of wave w covers tokens 8 (2w + j) + lane / 8; lane
+   * position q = lane % 8 of the token's LDS row fetches octet q ^ swz */
+  const __bf16 *xsrc[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int tl = 8 * (2 * wave + j) + (lane >> 3), q = lane & 7;
+    const int oct = q ^ ((tl >> 1) & 7);
+    xsrc[j] = a.x + (size_t)min(t0 + tl, a.T - 1) * a.K + 8 * oct;
+  }
+  auto issue = [&](int st) {
+    const uint32_t slot = sbase + (uint32_t)((st % kRing) * SB);
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+      dma16(xsrc[j] + st * kBK, __builtin_amdgcn_readfirstlane(slot + 1024u * (uint32_t)(2 * wave + j)));
+    PW<DT>::issue(pl, w, st, slot + kXBytes + (uint32_t)(wave * PW<DT>::kWaveLds));
+  };
+  for (int st = 0; st < kRing - 1 && st < nsteps; st++) issue(st);
+  acc[0] = gq_f32x16{};
+  acc[1] = gq_f32x16{};
+  const int h = lane >> 5, i32 = lane & 31;
+  /* Software pipeline: iteration s runs the MFMAs of step s with B operands
+   * dequantized in iteration s - 1 while it dequantizes step s + 1, so the
+   * VALU work overlaps the matrix core.  A wave's copies of a step have
+   * landed once only the copies of later steps remain in flight; the
+   * barrier extends that to every wave's copies and frees the slot read in
+   * iteration s - 1 for step s + kRing - 1. */
+  /* A operand addresses within a slot: token tl = 32 i + lane % 32, octet
+   * 2 kk + lane / 32, swizzled */
+  uint32_t aoff[4][2];
+#pragma unroll
+  for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int tl = 32 * i + i32, q = (2 * kk + h) ^ ((tl >> 1) & 7);
+      aoff[kk][i] = (uint32_t)((tl * 8 + q) * 16);
+    }
+  auto wslot = [&](int st) { return smem + (st % kRing) * SB + kXBytes + wave * PW<DT>::kWaveLds; };
+  gq_bf16x8 b[4], av[4][2];
+  typename PW<DT>::Raw raw;
+  wait_groups<NPS, kRing - 2>(nsteps - 1);
+  __syncthreads();
+  PW<DT>::read(raw, wslot(0), lane, 0);
+#pragma unroll
+  for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+    for (int i = 0; i < 2; i++) av[kk][i] = lld<gq_bf16x8>(smem, aoff[kk][i]);
+  PW<DT>::dequant(raw, 0, b);
   for (int s = 0; s < nsteps; s++) {
-    GQ_LDS uint8_t *As = (GQ_LDS uint8_t *)smem[s & 1];
-    GQ_LDS uint8_t *Bs = As + kBM * kLdK * 2;
-    store_stage<DT>(st, As, Bs, s);
+    if (s + 1 < nsteps) wait_groups<NPS, kRing - 3>(nsteps - 2 - s);
     __syncthreads();
-    if (s + 1 < nsteps) load_stage<DT>(st, X, T, K, W, t0, n0, s + 1);
+    if (s + kRing - 1 < nsteps) issue(s + kRing - 1);
+    /* LDS reads for step s + 1 first, so their latency hides behind the
+     * MFMAs of step s */
+    gq_bf16x8 an[4][2];
+    const bool more = s + 1 < nsteps;
+    if (more) {
+      const GQ_LDS uint8_t *xn = smem + ((s + 1) % kRing) * SB;
+      PW<DT>::read(raw, wslot(s + 1), lane, s + 1);
 #pragma unroll
-    for (int kk = 0; kk < kBK / 16; kk++) {
-      const uint32_t ko = (uint32_t)(16 * kk + 8 * (lane >> 5));
-      const gq_bf16x8 a = lld<gq_bf16x8>(As, ((uint32_t)(32 * wm + (lane & 31)) * kLdK + ko) * 2u);
+      for (int kk = 0; kk < 4; kk++)
 #pragma unroll
-      for (int j = 0; j < 2; j++) {
-        const gq_bf16x8 b = lld<gq_bf16x8>(Bs, ((uint32_t)(64 * wn + 32 * j + (lane & 31)) * kLdK + ko) * 2u);
-        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[j], 0, 0, 0);
-      }
+        for (int i = 0; i < 2; i++) an[kk][i] = lld<gq_bf16x8>(xn, aoff[kk][i]);
     }
-    /* the other buffer is written next step; this one only after a barrier */
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+      for (int i = 0; i < 2; i++) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[kk][i], b[kk], acc[i], 0, 0, 0);
+    if (more) {
+      PW<DT>::dequant(raw, s + 1, b);
+#pragma unroll
+      for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+        for (int i = 0; i < 2; i++) av[kk][i] = an[kk][i];
+    }
   }
-  /* D[i][j]: token t0 + 32 wm + i, row n0 + 64 wn + 32 jt + j */
-#pragma unroll
-  for (int jt = 0; jt < 2; jt++)
-#pragma unroll
-    for (int e = 0; e < 16; e++) {
-      const int i = (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-      const int t = t0 + 32 * wm + i, n = n0 + 64 * wn + 32 * jt + (lane & 31);
-      if (t < T) {
-        float v = acc[jt][e];
-        if (MODE == MV_RESID) v = gld<float>(R + (size_t)t * N + n) + v;
-        gst<float>(Y + (size_t)t * N + n, v);
-      }
-    }
 }
 
-} // namespace
+__device__ __forceinline__ int tile_token(int i, int e, int lane) {
+  return 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+}
 
-namespace {
-template <int DT>
-int launch_dt(int mode, const float *X, const void *W, float *Y, const float *R, int T, int N, int K,
-              hipStream_t s) {
-  const dim3 grid(N / kBN, (T + kBM - 1) / kBM), block(kPThreads);
-  if (mode == MV_RESID)
-    hipLaunchKernelGGL((prefill_gemm_kernel<DT, MV_RESID>), grid, block, 0, s, X, (const uint8_t *)W, Y, R, T, N,
-                       K);
-  else if (mode == MV_STORE)
-    hipLaunchKernelGGL((prefill_gemm_kernel<DT, MV_STORE>), grid, block, 0, s, X, (const uint8_t *)W, Y, R, T, N,
-                       K);
+/* Grid: x = row tiles over the segments (kBN rows each; MV_SWIGLU: 64 gate
+ * rows with the same 64 up rows), y = token tiles. */
+template <int MODE>
+__global__ __launch_bounds__(kPThreads) void pgemm_kernel(PgArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t pg_smem[];
+  GQ_LDS uint8_t *smem = (GQ_LDS uint8_t *)pg_smem;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int t0 = blockIdx.y * kBM;
+  int sg = 0, tb = blockIdx.x;
+  if (MODE != MV_SWIGLU)
+    while (sg + 1 < a.nseg && tb >= a.seg[sg].rows / kBN) tb -= a.seg[sg].rows / kBN, sg++;
+  /* this wave's weights: rows r0 .. r0 + 31 of segment ws */
+  int ws = sg, r0 = tb * kBN + 32 * wave;
+  if (MODE == MV_SWIGLU) ws = wave >> 1, r0 = tb * (kBN / 2) + 32 * (wave & 1);
+  const PgSeg &S = a.seg[ws];
+  const int dt = a.seg[sg].dtype;
+  const uint32_t rowbytes = (uint32_t)(a.K / 256) * (dt == GQ_Q4_K ? 144u : 210u);
+  const uint8_t *w = S.w + (size_t)r0 * rowbytes;
+  gq_f32x16 acc[2];
+  if (dt == GQ_Q4_K)
+    tile_loop<GQ_Q4_K>(a, w, rowbytes, t0, smem, acc);
   else
-    return -1;
+    tile_loop<GQ_Q6_K>(a, w, rowbytes, t0, smem, acc);
+  const int n = r0 + (lane & 31);
+  if (MODE != MV_SWIGLU) {
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int t = t0 + tile_token(i, e, lane);
+        if (t < a.T) {
+          float v = acc[i][e];
+          float *y = S.y + (size_t)t * S.rows + n;
+          if (MODE == MV_RESID) v = gld<float>(y) + v;
+          gst<float>(y, v);
+        }
+      }
+    return;
+  }
+  /* SwiGLU: the up waves (2, 3) hand their tiles to the gate waves (0, 1)
+   * through LDS; act = (g * sigmoid(g)) * u as silu_inplace then
+   * elemwise_mul (kernels_cpu.c:312-389), rounded to bf16 */
+  __syncthreads(); /* every wave is done reading the ring */
+  GQ_LDS float *xch = (GQ_LDS float *)smem;
+  if (wave >= 2) {
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) xch[(((wave - 2) * 2 + i) * 16 + e) * 64 + lane] = acc[i][e];
+  }
+  __syncthreads();
+  if (wave < 2) {
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int t = t0 + tile_token(i, e, lane);
+        const float g = acc[i][e], u = xch[((wave * 2 + i) * 16 + e) * 64 + lane];
+        const float sig = 1.0f / (1.0f + expf(0.0f - g));
+        const __bf16 v = (__bf16)((g * sig) * u);
+        if (t < a.T) gst<unsigned short>(a.act + (size_t)t * S.rows + n, __builtin_bit_cast(unsigned short, v));
+      }
+  }
+}
+
+__global__ void to_bf16_kernel(const float *x, __bf16 *y, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = (__bf16)x[i];
+}
+
+template <int MODE>
+int launch_mode(const PgArgs &a, int row_tiles, hipStream_t s) {
+  bool q6 = false;
+  for (int i = 0; i < a.nseg; i++) q6 |= a.seg[i].dtype == GQ_Q6_K;
+  bool q4 = false;
+  for (int i = 0; i < a.nseg; i++) q4 |= a.seg[i].dtype == GQ_Q4_K;
+  const size_t lds = std::max(q6 ? ring_bytes<GQ_Q6_K>() : 0, q4 ? ring_bytes<GQ_Q4_K>() : 0);
+  static bool attr_done = false;
+  if (!attr_done) {
+    (void)hipFuncSetAttribute((const void *)pgemm_kernel<MODE>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              std::max(ring_bytes<GQ_Q6_K>(), ring_bytes<GQ_Q4_K>()));
+    attr_done = true;
+  }
+  hipLaunchKernelGGL((pgemm_kernel<MODE>), dim3(row_tiles, (a.T + kBM - 1) / kBM), dim3(kPThreads), lds, s, a);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
+
 } // namespace
 
-int gq_launch_prefill_gemm(int dtype, int mode, const float *X, const void *W, float *Y, const float *R, int T,
-                           int N, int K, hipStream_t s) {
-  if (T <= 0 || N <= 0 || K <= 0 || N % kBN || K % 256 || (mode == MV_RESID && !R)) return -1;
-  if (dtype == GQ_Q4_K) return launch_dt<GQ_Q4_K>(mode, X, W, Y, R, T, N, K, s);
-  if (dtype == GQ_Q6_K) return launch_dt<GQ_Q6_K>(mode, X, W, Y, R, T, N, K, s);
+int gq_launch_pgemm(int mode, const PgArgs &a, hipStream_t s) {
+  if (a.T <= 0 || a.K <= 0 || a.K % 256 || a.nseg < 1 || a.nseg > 3 || !a.x) return -1;
+  int tiles = 0;
+  for (int i = 0; i < a.nseg; i++) {
+    const PgSeg &g = a.seg[i];
+    if (!g.w || g.rows <= 0) return -1;
+    if (g.dtype != GQ_Q4_K && g.dtype != GQ_Q6_K) return -1;
+    if (g.dtype == GQ_Q6_K && a.K % 512) return -2;
+    if (mode == MV_SWIGLU) {
+      if (g.rows % (kBN / 2) || g.dtype != a.seg[0].dtype || g.rows != a.seg[0].rows) return -1;
+    } else {
+      if (g.rows % kBN || !g.y) return -1;
+      tiles += g.rows / kBN;
+    }
+  }
+  /* the SwiGLU exchange (16 KB) reuses the ring, which is larger */
+  static_assert(ring_bytes<GQ_Q4_K>() >= 2 * 2 * 16 * 64 * 4 && ring_bytes<GQ_Q6_K>() >= 2 * 2 * 16 * 64 * 4,
+                "exchange fits the ring");
+  if (mode == MV_SWIGLU) {
+    if (a.nseg != 2 || !a.act) return -1;
+    return launch_mode<MV_SWIGLU>(a, a.seg[0].rows / (kBN / 2), s);
+  }
+  if (mode == MV_RESID) return launch_mode<MV_RESID>(a, tiles, s);
+  if (mode == MV_STORE) return launch_mode<MV_STORE>(a, tiles, s);
   return -1;
+}
+
+int gq_launch_to_bf16(const float *x, __bf16 *y, size_t n, hipStream_t s) {
+  if (!n) return 0;
+  hipLaunchKernelGGL(to_bf16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, y, n);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
 }

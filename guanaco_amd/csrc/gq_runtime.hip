@@ -39,10 +39,12 @@ struct Workspace {
  * for up to `cap` tokens; attention partials grow with the context. */
 struct PrefillWs {
   int cap = 0;
-  float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr;
-  float *g = nullptr, *u = nullptr, *po = nullptr, *pml = nullptr;
+  float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr; /* fp32: hidden, q/k/v for RoPE */
+  __bf16 *xn = nullptr, *att = nullptr, *act = nullptr;          /* bf16 GEMM inputs */
+  float *po = nullptr, *pml = nullptr;
+  __bf16 *xb = nullptr; /* op-level entry: bf16 copy of its fp32 x */
   int *tok = nullptr;
-  size_t po_cap = 0, pml_cap = 0;
+  size_t po_cap = 0, pml_cap = 0, xb_cap = 0;
 };
 
 /* tokens per prefill chunk */
@@ -905,10 +907,11 @@ extern "C" int gq_hip_decode_loop(gq_ctx *c, int token, int pos, int n_steps, in
  * tokens; per layer and chunk one GEMM launch per projection on the matrix
  * cores, RoPE + append of every token of the chunk, then causal attention
  * (token t sees positions 0 .. pos + t). */
-static int pf_ensure(gq_ctx *c, float *&p, size_t &cap, size_t n) {
+template <class T>
+static int pf_ensure(gq_ctx *c, T *&p, size_t &cap, size_t n) {
   if (cap >= n && p) return 0;
   if (p) gq_hip_free(c, p);
-  p = (float *)dev_alloc(c, sizeof(float) * n);
+  p = (T *)dev_alloc(c, sizeof(T) * n);
   if (!p) return -4;
   cap = n;
   return 0;
@@ -919,37 +922,42 @@ static int pf_alloc(gq_ctx *c) {
   if (w.cap) return 0;
   const gq_model &m = c->m;
   const size_t T = kPrefillChunk, H = m.hidden, F = m.ff, kvd = (size_t)m.n_kv_heads * m.head_dim;
-  float **bufs[8] = {&w.x, &w.xn, &w.q, &w.att, &w.k, &w.v, &w.g, &w.u};
-  const size_t n[8] = {T * H, T * H, T * H, T * H, T * kvd, T * kvd, T * F, T * F};
-  for (int i = 0; i < 8; i++)
-    if (!(*bufs[i] = (float *)dev_alloc(c, sizeof(float) * n[i]))) return -4;
+  float **f32[4] = {&w.x, &w.q, &w.k, &w.v};
+  const size_t nf[4] = {T * H, T * H, T * kvd, T * kvd};
+  for (int i = 0; i < 4; i++)
+    if (!(*f32[i] = (float *)dev_alloc(c, sizeof(float) * nf[i]))) return -4;
+  __bf16 **b16[3] = {&w.xn, &w.att, &w.act};
+  const size_t nb[3] = {T * H, T * H, T * F};
+  for (int i = 0; i < 3; i++)
+    if (!(*b16[i] = (__bf16 *)dev_alloc(c, sizeof(__bf16) * nb[i]))) return -4;
   if (!(w.tok = (int *)dev_alloc(c, sizeof(int) * T))) return -4;
   w.cap = kPrefillChunk;
   return 0;
 }
 
-/* y (T x rows) = x (T x cols) W^T, or y += with resid: the bf16 GEMM for
- * Q4_K / Q6_K weights of 128-row multiples, else T device matvecs */
-static int pf_proj(gq_ctx *c, const gq_weight &w, const float *x, float *y, int T, bool resid) {
-  if ((w.dtype == GQ_Q4_K || w.dtype == GQ_Q6_K) && w.rows % 128 == 0 && w.cols % 256 == 0)
-    return gq_launch_prefill_gemm(w.dtype, resid ? MV_RESID : MV_STORE, x, w.data, y, resid ? y : nullptr, T,
-                                  w.rows, w.cols, c->stream);
-  for (int t = 0; t < T; t++) {
-    MvArgs a{};
-    float *yt = y + (size_t)t * w.rows;
-    a.seg[0] = MvSeg{(const uint8_t *)w.data, yt, resid ? yt : nullptr, w.rows};
-    a.nseg = 1, a.cols = w.cols, a.x = x + (size_t)t * w.cols;
-    const int rc = gq_launch_matvec(w.dtype, resid ? MV_RESID : MV_STORE, a, c->stream);
-    if (rc) return rc;
-  }
-  return 0;
+/* The GEMM takes Q4_K rows in multiples of 128 and Q6_K rows likewise with
+ * cols % 512 == 0; a model with any other projection prefills token by
+ * token through the decode step instead. */
+static bool pf_gemm_ok(const gq_weight &w) {
+  return (w.dtype == GQ_Q4_K || (w.dtype == GQ_Q6_K && w.cols % 512 == 0)) && w.rows % 128 == 0 &&
+         w.cols % 256 == 0;
 }
+
+static bool pf_model_ok(const gq_ctx *c) {
+  for (const gq_layer &L : c->layers)
+    if (!pf_gemm_ok(L.wq) || !pf_gemm_ok(L.wk) || !pf_gemm_ok(L.wv) || !pf_gemm_ok(L.wo) || !pf_gemm_ok(L.w_gate) ||
+        !pf_gemm_ok(L.w_up) || !pf_gemm_ok(L.w_down) || L.w_gate.dtype != L.w_up.dtype)
+      return false;
+  return true;
+}
+
+static PgSeg pg_seg(const gq_weight &w, float *y) { return PgSeg{(const uint8_t *)w.data, y, w.rows, w.dtype}; }
 
 /* RoPE + append of T tokens at pos..pos+T-1 (q: T x n_heads*hd in place,
  * k/v: T x n_kv*hd), then causal attention into out (T x n_heads*hd), in
  * token sub-batches that keep the partials under kPrefillPartBytes */
 static int pf_attention(gq_ctx *c, int layer, int pos, int T, int n_heads, float *q, const float *k, const float *v,
-                        float *out) {
+                        float *out, __bf16 *out16) {
   const int hd = c->kv_hd, kvd = c->kv_heads * hd, qd = n_heads * hd;
   RopeArgs ra{q, k, v, gq_hip_kv_k(c, layer), gq_hip_kv_v(c, layer), c->rope, nullptr, pos,
               n_heads, c->kv_heads, hd, c->kv_max_seq, T, qd, kvd, kvd};
@@ -970,7 +978,8 @@ static int pf_attention(gq_ctx *c, int layer, int pos, int T, int n_heads, float
     aa.q = q + (size_t)t0 * qd, aa.q_stride = qd;
     aa.k = gq_hip_kv_k(c, layer), aa.v = gq_hip_kv_v(c, layer);
     aa.part_o = w.po, aa.part_ml = w.pml;
-    aa.out = out + (size_t)t0 * qd, aa.out_stride = qd;
+    aa.out = out ? out + (size_t)t0 * qd : nullptr, aa.out_stride = qd;
+    aa.out16 = out16 ? out16 + (size_t)t0 * qd : nullptr;
     aa.n_heads = n_heads, aa.n_kv = c->kv_heads, aa.hd = hd, aa.max_seq = c->kv_max_seq;
     aa.s_max = gq_attn_smax(c->kv_max_seq, aa.nch), aa.scale = 1.0f / sqrtf((float)hd);
     if ((rc = gq_launch_attention_chunk(aa, c->stream))) return rc;
@@ -979,19 +988,28 @@ static int pf_attention(gq_ctx *c, int layer, int pos, int T, int n_heads, float
   return 0;
 }
 
+/* one layer over the chunk (engine.c:352-554 with T tokens): 7 launches of
+ * the GEMM (q/k/v together, gate/up together with SwiGLU), RMSNorms writing
+ * bf16, RoPE + append + attention writing bf16 */
 static int pf_layer(gq_ctx *c, int l, int pos, int T) {
   const gq_model &m = c->m;
   const gq_layer &L = c->layers[l];
   PrefillWs &w = c->pf;
   int rc;
-  if ((rc = gq_launch_rmsnorm_rows(w.x, L.rms_att, w.xn, m.hidden, T, m.rms_eps, c->stream)) ||
-      (rc = pf_proj(c, L.wq, w.xn, w.q, T, false)) || (rc = pf_proj(c, L.wk, w.xn, w.k, T, false)) ||
-      (rc = pf_proj(c, L.wv, w.xn, w.v, T, false)) ||
-      (rc = pf_attention(c, l, pos, T, m.n_heads, w.q, w.k, w.v, w.att)) ||
-      (rc = pf_proj(c, L.wo, w.att, w.x, T, true)) ||
-      (rc = gq_launch_rmsnorm_rows(w.x, L.rms_ffn, w.xn, m.hidden, T, m.rms_eps, c->stream)) ||
-      (rc = pf_proj(c, L.w_gate, w.xn, w.g, T, false)) || (rc = pf_proj(c, L.w_up, w.xn, w.u, T, false)) ||
-      (rc = gq_launch_silu_mul(w.g, w.u, T * m.ff, c->stream)) || (rc = pf_proj(c, L.w_down, w.g, w.x, T, true)))
+  PgArgs qkv{}, o{}, gu{}, dn{};
+  qkv.T = o.T = gu.T = dn.T = T;
+  qkv.x = w.xn, qkv.K = m.hidden, qkv.nseg = 3;
+  qkv.seg[0] = pg_seg(L.wq, w.q), qkv.seg[1] = pg_seg(L.wk, w.k), qkv.seg[2] = pg_seg(L.wv, w.v);
+  o.x = w.att, o.K = m.hidden, o.nseg = 1, o.seg[0] = pg_seg(L.wo, w.x);
+  gu.x = w.xn, gu.K = m.hidden, gu.nseg = 2, gu.act = w.act;
+  gu.seg[0] = pg_seg(L.w_gate, nullptr), gu.seg[1] = pg_seg(L.w_up, nullptr);
+  dn.x = w.act, dn.K = m.ff, dn.nseg = 1, dn.seg[0] = pg_seg(L.w_down, w.x);
+  if ((rc = gq_launch_rmsnorm_rows(w.x, L.rms_att, nullptr, m.hidden, T, m.rms_eps, c->stream, w.xn)) ||
+      (rc = gq_launch_pgemm(MV_STORE, qkv, c->stream)) ||
+      (rc = pf_attention(c, l, pos, T, m.n_heads, w.q, w.k, w.v, nullptr, w.att)) ||
+      (rc = gq_launch_pgemm(MV_RESID, o, c->stream)) ||
+      (rc = gq_launch_rmsnorm_rows(w.x, L.rms_ffn, nullptr, m.hidden, T, m.rms_eps, c->stream, w.xn)) ||
+      (rc = gq_launch_pgemm(MV_SWIGLU, gu, c->stream)) || (rc = gq_launch_pgemm(MV_RESID, dn, c->stream)))
     return rc;
   return 0;
 }
@@ -1004,7 +1022,8 @@ extern "C" int gq_hip_prefill(gq_ctx *c, const int32_t *tokens, int n_tokens, in
   const gq_model &m = c->m;
   for (int i = 0; i < n_tokens; i++)
     if (tokens[i] < 0 || tokens[i] >= m.vocab) return fail(c, -1, "prefill: token %d out of range", tokens[i]);
-  if ((rc = pf_alloc(c))) return rc;
+  const bool gemm = pf_model_ok(c);
+  if (gemm && (rc = pf_alloc(c))) return rc;
   PrefillWs &w = c->pf;
   Workspace &ws = c->ws;
   hipEvent_t e0 = nullptr, e1 = nullptr;
@@ -1014,21 +1033,26 @@ extern "C" int gq_hip_prefill(gq_ctx *c, const int32_t *tokens, int n_tokens, in
     HIPCHK(c, hipEventRecord(e0, c->stream));
   }
   int T = 0;
-  for (int t0 = 0; t0 < n_tokens; t0 += T) {
-    T = std::min(kPrefillChunk, n_tokens - t0);
-    HIPCHK(c, hipMemcpyAsync(w.tok, tokens + t0, sizeof(int) * T, hipMemcpyHostToDevice, c->stream));
-    if ((rc = gq_launch_embed_rows(m.embed.dtype, m.embed.data, m.hidden, w.tok, T, w.x, c->stream)))
-      return fail(c, rc, "prefill: embed");
-    for (int l = 0; l < m.n_layers; l++)
-      if ((rc = pf_layer(c, l, pos + t0, T))) return fail(c, rc, "prefill: layer %d launch failed", l);
+  if (!gemm) { /* token by token through the decode step */
+    for (int t = 0; t < n_tokens; t++)
+      if ((rc = run_step(c, tokens[t], pos + t, false, nullptr))) return fail(c, rc, "prefill: step launch failed");
+  } else {
+    for (int t0 = 0; t0 < n_tokens; t0 += T) {
+      T = std::min(kPrefillChunk, n_tokens - t0);
+      HIPCHK(c, hipMemcpyAsync(w.tok, tokens + t0, sizeof(int) * T, hipMemcpyHostToDevice, c->stream));
+      if ((rc = gq_launch_embed_rows(m.embed.dtype, m.embed.data, m.hidden, w.tok, T, w.x, c->stream)))
+        return fail(c, rc, "prefill: embed");
+      for (int l = 0; l < m.n_layers; l++)
+        if ((rc = pf_layer(c, l, pos + t0, T))) return fail(c, rc, "prefill: layer %d launch failed", l);
+    }
+    /* last token: final RMSNorm + LM head + argmax as in a decode step */
+    HIPCHK(c, hipMemcpyAsync(ws.hidden, w.x + (size_t)(T - 1) * m.hidden, sizeof(float) * m.hidden,
+                             hipMemcpyDeviceToDevice, c->stream));
+    if ((rc = op_lm_head(c, ws.hidden)) ||
+        (rc = gq_launch_argmax(ws.logits, m.vocab, ws.amax, ws.amax_blocks, ws.d_token, nullptr, nullptr, nullptr,
+                               c->stream)))
+      return fail(c, rc, "prefill: lm head");
   }
-  /* last token: final RMSNorm + LM head + argmax as in a decode step */
-  HIPCHK(c, hipMemcpyAsync(ws.hidden, w.x + (size_t)(T - 1) * m.hidden, sizeof(float) * m.hidden,
-                           hipMemcpyDeviceToDevice, c->stream));
-  if ((rc = op_lm_head(c, ws.hidden)) ||
-      (rc = gq_launch_argmax(ws.logits, m.vocab, ws.amax, ws.amax_blocks, ws.d_token, nullptr, nullptr, nullptr,
-                             c->stream)))
-    return fail(c, rc, "prefill: lm head");
   if (ms) HIPCHK(c, hipEventRecord(e1, c->stream));
   int next = -1;
   HIPCHK(c, hipMemcpyAsync(&next, ws.d_token, sizeof(int), hipMemcpyDeviceToHost, c->stream));
@@ -1232,7 +1256,7 @@ extern "C" int gq_hip_prefill_attention_dev(gq_ctx *c, int layer, int pos, int T
       n_heads <= 0 || n_heads % c->kv_heads)
     return fail(c, -1, "prefill attention: bad argument");
   if (pos < 0 || pos + T > c->kv_max_seq) return fail(c, -5, "prefill attention: positions outside the cache");
-  const int rc = pf_attention(c, layer, pos, T, n_heads, q, k, v, out);
+  const int rc = pf_attention(c, layer, pos, T, n_heads, q, k, v, out, nullptr);
   return rc ? fail(c, rc, "prefill attention launch (unsupported head_dim/group?)") : 0;
 }
 
@@ -1252,13 +1276,43 @@ extern "C" int gq_hip_argmax_dev(gq_ctx *c, const float *x, int n, int *out_inde
   return rc ? fail(c, rc, "argmax") : 0;
 }
 
+/* fp32 x -> the bf16 copy the GEMM reads */
+static const __bf16 *pf_x16(gq_ctx *c, const float *x, size_t n) {
+  PrefillWs &w = c->pf;
+  if (pf_ensure(c, w.xb, w.xb_cap, n) || gq_launch_to_bf16(x, w.xb, n, c->stream)) return nullptr;
+  return w.xb;
+}
+
 extern "C" int gq_hip_prefill_gemm_dev(gq_ctx *c, int dtype, int mode, const void *w, int n, int k,
                                        const float *x, int t, float *y, const float *r) {
-  if (!c || !w || !x || !y || t <= 0) return -1;
+  if (!c || !w || !x || !y || t <= 0 || n <= 0 || k <= 0 || (mode == 1 && !r) || (mode != 0 && mode != 1))
+    return fail(c, -1, "prefill GEMM: bad argument");
   if (dtype != GQ_Q4_K && dtype != GQ_Q6_K) return fail(c, -1, "prefill GEMM: Q4_K or Q6_K weights only");
-  if (k % 256) return fail(c, -2, "prefill GEMM: cols must be a multiple of 256");
-  const int rc = gq_launch_prefill_gemm(dtype, mode == 1 ? MV_RESID : MV_STORE, x, w, y, r, t, n, k, c->stream);
-  return rc ? fail(c, rc, "prefill GEMM launch (rows must be a multiple of 128)") : 0;
+  if (k % 256 || (dtype == GQ_Q6_K && k % 512)) return fail(c, -2, "prefill GEMM: cols %% 256 (Q6_K: %% 512)");
+  if (n % 128) return fail(c, -1, "prefill GEMM: rows must be a multiple of 128");
+  PgArgs a{};
+  if (!(a.x = pf_x16(c, x, (size_t)t * k))) return fail(c, -4, "prefill GEMM: x conversion");
+  a.T = t, a.K = k, a.nseg = 1, a.seg[0] = PgSeg{(const uint8_t *)w, y, n, dtype};
+  if (mode == 1 && r != y)
+    HIPCHK(c, hipMemcpyAsync(y, r, sizeof(float) * (size_t)t * n, hipMemcpyDeviceToDevice, c->stream));
+  const int rc = gq_launch_pgemm(mode == 1 ? MV_RESID : MV_STORE, a, c->stream);
+  return rc ? fail(c, rc, "prefill GEMM launch") : 0;
+}
+
+extern "C" int gq_hip_prefill_gate_up_dev(gq_ctx *c, int dtype, const void *w_gate, const void *w_up, int n, int k,
+                                          const float *x, int t, uint16_t *act) {
+  if (!c || !w_gate || !w_up || !x || !act || t <= 0 || n <= 0 || k <= 0)
+    return fail(c, -1, "prefill gate/up: bad argument");
+  if (dtype != GQ_Q4_K && dtype != GQ_Q6_K) return fail(c, -1, "prefill gate/up: Q4_K or Q6_K weights only");
+  if (k % 256 || (dtype == GQ_Q6_K && k % 512)) return fail(c, -2, "prefill gate/up: cols %% 256 (Q6_K: %% 512)");
+  if (n % 64) return fail(c, -1, "prefill gate/up: rows must be a multiple of 64");
+  PgArgs a{};
+  if (!(a.x = pf_x16(c, x, (size_t)t * k))) return fail(c, -4, "prefill gate/up: x conversion");
+  a.T = t, a.K = k, a.nseg = 2, a.act = (__bf16 *)act;
+  a.seg[0] = PgSeg{(const uint8_t *)w_gate, nullptr, n, dtype};
+  a.seg[1] = PgSeg{(const uint8_t *)w_up, nullptr, n, dtype};
+  const int rc = gq_launch_pgemm(MV_SWIGLU, a, c->stream);
+  return rc ? fail(c, rc, "prefill gate/up launch") : 0;
 }
 
 extern "C" int gq_hip_copy_dev(gq_ctx *c, void *dst, const void *src, size_t bytes) {

@@ -84,6 +84,8 @@ def _load():
         "gq_hip_copy_dev": (C.c_int, [_vp, _vp, _vp, C.c_size_t]),
         "gq_hip_prefill_gemm_dev": (C.c_int, [_vp, C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp,
                                               C.c_int, _vp, _vp]),
+        "gq_hip_prefill_gate_up_dev": (C.c_int, [_vp, C.c_int, _vp, _vp, C.c_int, C.c_int, _vp, C.c_int,
+                                                 _vp]),
         "gq_hip_prefill_attention_dev": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp,
                                                    _vp, _vp]),
         "gq_hip_prefill": (C.c_int, [_vp, C.POINTER(C.c_int32), C.c_int, C.c_int, _fp, _fp,

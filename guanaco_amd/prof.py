@@ -15,6 +15,9 @@
         4096-token prefix (1 GiB of K/V) from pinned host memory.  Prints one
         JSON line per result.
 
+    python3 -m guanaco_amd.prof gemm --dtype 4 --rows 4096 --cols 4096 --tokens 512 --iters 20
+        one prefill GEMM shape launched back to back (for counter runs).
+
     python3 -m guanaco_amd.prof config5
         the prefill chunk on the 8B shape: the bf16-MFMA GEMM of 512 tokens
         against each projection shape (4096x4096, 1024x4096, 14336x4096 and
@@ -166,6 +169,25 @@ def config5(ctx, T=512, iters=20):
                  gflop=round(flop / 1e9, 2), TFLOP_per_s=round(flop / dt_s / 1e12, 1),
                  weight_bytes=S.qbytes(dt, N, K))
             w.free(), x.free(), y.free()
+    # gate and up in one launch with SwiGLU in the epilogue (the model's form)
+    wg, wu = ctx.synth_quant(S.Q4_K, F, H_, 91), ctx.synth_quant(S.Q4_K, F, H_, 92)
+    x = ctx.synth_normal(T * H_, 5)
+    act = ctx.alloc(2 * T * F)
+
+    def gu():
+        ctx.check(H.lib.gq_hip_prefill_gate_up_dev(ctx.h, S.Q4_K, wg.ptr, wu.ptr, F, H_, x.ptr, T, act.ptr), "gate/up")
+    gu()
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        gu()
+    ctx.sync()
+    dt_s = (time.perf_counter() - t0) / iters
+    flop = 2 * 2.0 * T * F * H_
+    emit(config=5, what=f"prefill gate+up+SwiGLU Q4_K: {T} tokens x 2x{F}x{H_} (incl. fp32->bf16 of x)",
+         us_per_launch=round(dt_s * 1e6, 2), gflop=round(flop / 1e9, 2), TFLOP_per_s=round(flop / dt_s / 1e12, 1))
+    for b in (wg, wu, x, act):
+        b.free()
     # RoPE + append + causal attention of T tokens from position 0
     nh, nkv, hd = spec.n_heads, spec.n_kv_heads, spec.head_dim
     ctx.kv_init(1, nkv, hd, T + 128, spec.rope_theta)
@@ -200,6 +222,24 @@ def config5(ctx, T=512, iters=20):
     ctx.close()
 
 
+def run_gemm(dtype, rows, cols, T, iters):
+    ctx = H.Context(0)
+    w = ctx.synth_quant(dtype, rows, cols, 7)
+    x = ctx.synth_normal(T * cols, 5)
+    y = ctx.alloc(4 * T * rows)
+    t0 = None
+    for i in range(iters + 1):
+        if i == 1:
+            ctx.sync()
+            t0 = time.perf_counter()
+        ctx.check(H.lib.gq_hip_prefill_gemm_dev(ctx.h, dtype, 0, w.ptr, rows, cols, x.ptr, T, y.ptr, None), "gemm")
+    ctx.sync()
+    dt = (time.perf_counter() - t0) / iters
+    emit(what=f"prefill GEMM dtype {dtype} {T} x {rows}x{cols}", us_per_launch=round(dt * 1e6, 2),
+         TFLOP_per_s=round(2.0 * T * rows * cols / dt / 1e12, 1))
+    ctx.close()
+
+
 def run_configs():
     ctx = H.Context(0)
     config1(ctx)
@@ -221,6 +261,12 @@ def main():
     c.add_argument("--iters", type=int, default=20)
     sub.add_parser("configs")
     sub.add_parser("config5")
+    g = sub.add_parser("gemm")
+    g.add_argument("--dtype", type=int, default=S.Q4_K)
+    g.add_argument("--rows", type=int, default=4096)
+    g.add_argument("--cols", type=int, default=4096)
+    g.add_argument("--tokens", type=int, default=512)
+    g.add_argument("--iters", type=int, default=20)
     a = ap.parse_args()
     if a.cmd == "copy":
         run_copy(a.mib, a.iters)
@@ -228,6 +274,8 @@ def main():
         run_configs()
     elif a.cmd == "config5":
         config5(H.Context(0))
+    elif a.cmd == "gemm":
+        run_gemm(a.dtype, a.rows, a.cols, a.tokens, a.iters)
 
 
 if __name__ == "__main__":

@@ -70,7 +70,8 @@ def test_prefill_gemm(ctx, orc, T, N, K, mode):
     _gemm_case(ctx, orc, S.Q4_K, T, N, K, mode)
 
 
-@pytest.mark.parametrize("T,N,K", [(64, 128, 256), (100, 256, 512), (512, 1024, 4096), (77, 384, 1536)])
+@pytest.mark.parametrize("T,N,K", [(64, 128, 512), (100, 256, 512), (512, 1024, 4096), (77, 384, 1536),
+                                   (33, 128, 3584)])
 @pytest.mark.parametrize("mode", [0, 1])
 def test_prefill_gemm_q6k(ctx, orc, T, N, K, mode):
     _gemm_case(ctx, orc, S.Q6_K, T, N, K, mode)
@@ -106,7 +107,44 @@ def test_prefill_gemm_rejects_bad_shapes(ctx):
     assert H.lib.gq_hip_prefill_gemm_dev(ctx.h, S.Q4_K, 0, buf.ptr, 100, 256, buf.ptr, 4, buf.ptr, None) != 0
     assert H.lib.gq_hip_prefill_gemm_dev(ctx.h, S.Q4_K, 0, buf.ptr, 128, 300, buf.ptr, 4, buf.ptr, None) != 0
     assert H.lib.gq_hip_prefill_gemm_dev(ctx.h, S.Q8_0, 0, buf.ptr, 128, 256, buf.ptr, 4, buf.ptr, None) != 0
+    assert H.lib.gq_hip_prefill_gemm_dev(ctx.h, S.Q6_K, 0, buf.ptr, 128, 256, buf.ptr, 4, buf.ptr, None) == -2
     buf.free()
+
+
+def silu_mul_f32(g, u):
+    g = g.astype(np.float32)
+    with np.errstate(over="ignore"):
+        sig = np.float32(1) / (np.float32(1) + np.exp(np.float32(0) - g))
+    return (g * sig) * u.astype(np.float32)
+
+
+@pytest.mark.parametrize("dtype,T,N,K", [(S.Q4_K, 512, 1024, 4096), (S.Q4_K, 70, 192, 512),
+                                         (S.Q6_K, 100, 256, 1024)])
+def test_prefill_gate_up_swiglu(ctx, orc, dtype, T, N, K):
+    """gate and up in one launch with SiLU(gate) * up in the epilogue
+    (kernels_cpu.c:312-389), bf16 out: against the exact-input reference
+    (bf16 operands, fp64 sums, the SwiGLU in fp32 and bf16 rounding as the
+    kernel does; only the accumulation order differs) and against fp64."""
+    import guanaco_amd.hip as H
+    seed = (T << 16) ^ (N << 4) ^ K
+    wg, wu = orc.synth_quant(dtype, seed, N, K), orc.synth_quant(dtype, seed + 1, N, K)
+    x = orc.synth_normal(seed + 2, T * K).reshape(T, K)
+    gd, ud, xd = ctx.upload_weight(wg), ctx.upload_weight(wu), ctx.upload(x)
+    act = ctx.alloc(2 * T * N)
+    assert H.lib.gq_hip_prefill_gate_up_dev(ctx.h, dtype, gd, ud, N, K, xd.ptr, T, act.ptr) == 0
+    a16 = act.download(np.uint16, count=T * N).reshape(T, N)
+    got = (a16.astype(np.uint32) << 16).view(np.float32)
+    deq = dequant_q4k_f64 if dtype == S.Q4_K else dequant_q6k_f64
+    kern = (lambda w: q4k_dequant_kernel_order(w, N, K)) if dtype == S.Q4_K else (lambda w: deq(w, N, K).astype(np.float32))
+    xb = bf16_round(x).astype(np.float64)
+    g = xb @ bf16_round(kern(wg)).astype(np.float64).T
+    u = xb @ bf16_round(kern(wu)).astype(np.float64).T
+    assert rel_l2(got, bf16_round(silu_mul_f32(g, u))) < 1e-3
+    g64, u64 = x.astype(np.float64) @ deq(wg, N, K).T, x.astype(np.float64) @ deq(wu, N, K).T
+    with np.errstate(over="ignore"):
+        assert rel_l2(got, g64 / (1 + np.exp(-g64)) * u64) < 2e-2
+    act.free(), xd.free()
+    H.lib.gq_hip_free(ctx.h, gd), H.lib.gq_hip_free(ctx.h, ud)
 
 
 @pytest.mark.parametrize("nh,nkv,hd,pre,T,ms", [
