@@ -88,12 +88,9 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(AttnArgs a) {
   __shared__ float ss[G][S];
   __shared__ float4 sr[NPG][G][DG];
 
-  const int g = blockIdx.x, c = blockIdx.y, tz = blockIdx.z, tid = threadIdx.x;
+  const int g = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  /* token tz of a chunk (0 for one token): its query, partials, position */
-  const int pos = (a.pos_dev ? gld<int>(a.pos_dev) : a.pos) + tz;
-  const float *aq = a.q + (size_t)tz * a.q_stride;
-  float *part_o = a.part_o + (size_t)tz * a.po_stride, *part_ml = a.part_ml + (size_t)tz * a.pml_stride;
+  const int pos = a.pos_dev ? gld<int>(a.pos_dev) : a.pos;
   const int L = min(pos + 1, a.max_seq);
   const int c0 = c * S;
   const int n = min(S, L - c0);
@@ -113,8 +110,8 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(AttnArgs a) {
   float4 qa[G], qb[G];
 #pragma unroll
   for (int h = 0; h < G; h++) {
-    qa[h] = gld<float4>(aq + (size_t)(h0 + h) * HD + d0);
-    qb[h] = gld<float4>(aq + (size_t)(h0 + h) * HD + d1);
+    qa[h] = gld<float4>(a.q + (size_t)(h0 + h) * HD + d0);
+    qb[h] = gld<float4>(a.q + (size_t)(h0 + h) * HD + d1);
   }
   float4 ka[KIT], kb[KIT];
 #pragma unroll
@@ -158,8 +155,8 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(AttnArgs a) {
     }
     l = gq_wave_sum(l);
     if (lane == 0) {
-      gst<float>(part_ml + (size_t)(h0 + h) * ml + 2 * c, m);
-      gst<float>(part_ml + (size_t)(h0 + h) * ml + 2 * c + 1, l);
+      gst<float>(a.part_ml + (size_t)(h0 + h) * ml + 2 * c, m);
+      gst<float>(a.part_ml + (size_t)(h0 + h) * ml + 2 * c + 1, l);
     }
   }
   __syncthreads();
@@ -193,7 +190,7 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(AttnArgs a) {
       const float4 u = sr[p][h][q];
       o.x += u.x, o.y += u.y, o.z += u.z, o.w += u.w;
     }
-    gst<float4>(part_o + ((size_t)(h0 + h) * a.nch + c) * HD + 4 * q, o);
+    gst<float4>(a.part_o + ((size_t)(h0 + h) * a.nch + c) * HD + 4 * q, o);
   }
 }
 
@@ -203,11 +200,11 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
   extern __shared__ float sw[]; /* [nch] weights e^(m_c - M), then l_c */
   __shared__ float red[kThreads / GQ_WAVE];
   __shared__ float sacc[kThreads / 32][32];
-  const int h = blockIdx.x, tz = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int pos = (a.pos_dev ? gld<int>(a.pos_dev) : a.pos) + tz;
+  const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int pos = a.pos_dev ? gld<int>(a.pos_dev) : a.pos;
   const int L = min(pos + 1, a.max_seq);
   const int nc = (L + kChunk - 1) / kChunk;
-  const float *ml = a.part_ml + (size_t)tz * a.pml_stride + (size_t)h * a.nch * 2;
+  const float *ml = a.part_ml + (size_t)h * a.nch * 2;
   float *sl = sw + a.nch;
   float m = -INFINITY;
   for (int c = tid; c < nc; c += kThreads) {
@@ -232,7 +229,7 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
   __syncthreads();
   const float Ls = (red[0] + red[1]) + (red[2] + red[3]);
   const int d = blockIdx.y * 32 + (tid & 31), cg = tid >> 5;
-  const float *o = a.part_o + (size_t)tz * a.po_stride + (size_t)h * a.nch * a.hd + d;
+  const float *o = a.part_o + (size_t)h * a.nch * a.hd + d;
   float acc = 0.f;
 #pragma unroll 8
   for (int c = cg; c < nc; c += kThreads / 32) acc = __builtin_fmaf(gld<float>(o + (size_t)c * a.hd), sw[c], acc);
@@ -242,30 +239,14 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
     float t = 0.f;
 #pragma unroll
     for (int k = 0; k < kThreads / 32; k++) t += sacc[k][tid];
-    const size_t o = (size_t)tz * a.out_stride + (size_t)h * a.hd + d;
-    if (a.out16)
-      gst<unsigned short>(a.out16 + o, __builtin_bit_cast(unsigned short, (__bf16)(t / Ls)));
-    else
-      gst<float>(a.out + o, t / Ls);
+    gst<float>(a.out + (size_t)h * a.hd + d, t / Ls);
   }
 }
 
 template <int HD, int G>
 int launch_partial(const AttnArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL((attn_partial_kernel<HD, G>), dim3(a.n_kv, a.nch, std::max(a.ntok, 1)), dim3(kThreads), 0, s,
-                     a);
+  hipLaunchKernelGGL((attn_partial_kernel<HD, G>), dim3(a.n_kv, a.nch), dim3(kThreads), 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : -4;
-}
-
-int launch_partial_any(const AttnArgs &a, hipStream_t s) {
-  const int G = a.n_heads / a.n_kv;
-  if (a.hd == 128 && G == 4) return launch_partial<128, 4>(a, s);
-  if (a.hd == 128 && G == 8) return launch_partial<128, 8>(a, s);
-  if (a.hd == 128 && G == 1) return launch_partial<128, 1>(a, s);
-  if (a.hd == 64 && G == 4) return launch_partial<64, 4>(a, s);
-  if (a.hd == 64 && G == 8) return launch_partial<64, 8>(a, s);
-  if (a.hd == 64 && G == 1) return launch_partial<64, 1>(a, s);
-  return -1;
 }
 
 } // namespace
@@ -283,8 +264,15 @@ int gq_attn_smax(int max_seq, int nch) {
 
 int gq_launch_attention(const AttnArgs &a, hipStream_t s, hipEvent_t mid) {
   if (a.n_kv <= 0 || a.n_heads % a.n_kv || a.nch != gq_attn_nch(a.n_kv, a.max_seq)) return -1;
-  if (a.hd % 32 || (size_t)a.nch * 2 * sizeof(float) > 32768 || a.ntok > 1) return -1;
-  const int rc = launch_partial_any(a, s);
+  if (a.hd % 32 || (size_t)a.nch * 2 * sizeof(float) > 32768) return -1;
+  const int G = a.n_heads / a.n_kv;
+  int rc = -1;
+  if (a.hd == 128 && G == 4) rc = launch_partial<128, 4>(a, s);
+  else if (a.hd == 128 && G == 8) rc = launch_partial<128, 8>(a, s);
+  else if (a.hd == 128 && G == 1) rc = launch_partial<128, 1>(a, s);
+  else if (a.hd == 64 && G == 4) rc = launch_partial<64, 4>(a, s);
+  else if (a.hd == 64 && G == 8) rc = launch_partial<64, 8>(a, s);
+  else if (a.hd == 64 && G == 1) rc = launch_partial<64, 1>(a, s);
   if (rc) return rc;
   if (mid) (void)hipEventRecord(mid, s);
   hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_heads, a.hd / 32), dim3(kThreads),
@@ -292,17 +280,179 @@ int gq_launch_attention(const AttnArgs &a, hipStream_t s, hipEvent_t mid) {
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
-int gq_launch_attention_chunk(const AttnArgs &a, hipStream_t s) {
-  if (a.n_kv <= 0 || a.n_heads % a.n_kv || a.ntok < 1 || a.hd % 32 || a.pos < 0) return -1;
-  if (a.pos + a.ntok > a.max_seq || a.nch != (a.pos + a.ntok + kChunk - 1) / kChunk) return -1;
-  if ((size_t)a.nch * 2 * sizeof(float) > 32768 || a.po_stride < (size_t)a.n_heads * a.nch * a.hd ||
-      a.pml_stride < (size_t)a.n_heads * a.nch * 2)
-    return -1;
-  const int rc = launch_partial_any(a, s);
-  if (rc) return rc;
-  hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_heads, a.hd / 32, a.ntok), dim3(kThreads),
-                     (size_t)a.nch * 2 * sizeof(float), s, a);
+namespace {
+
+typedef float gq_f32x4 __attribute__((ext_vector_type(4)));
+typedef float gq_f2a __attribute__((ext_vector_type(2)));
+typedef __bf16 gq_bf2a __attribute__((ext_vector_type(2)));
+
+/* Causal attention of a prefill chunk on the fp32 matrix cores
+ * (v_mfma_f32_16x16x4_f32), flash-attention style: one wave per 16 query
+ * rows = 16 / G tokens x the G query heads of KV head g (the heads that
+ * share K/V), streaming the keys 0 .. (last token's position) in blocks of
+ * 16 with an online softmax.  Per block:
+ *   S^T = K Q^T   D[key][row]: lane (c, j) = (lane % 16, lane / 16) holds
+ *                 row c, keys 4 j + i (i < 4); the head dimension is split
+ *                 into 4 lane groups (dims HD/4 j ..) so every MFMA step
+ *                 reads one K and one Q float per lane;
+ *   scale, mask keys past each row's position, running max / sum across
+ *   the 4 lanes of a row;
+ *   O += P V      A = P straight from the S^T layout (step i takes keys
+ *                 4 j + i), B = V rows; output tile d holds dims ND c + d,
+ *                 so a lane reads ND consecutive floats of each V row and
+ *                 holds ND consecutive output dims of rows 4 j + i.
+ * Same mathematics as the reference (engine.c:476-501: scores * 1/sqrt(hd),
+ * -inf past the query position, softmax, P V) in fp32 throughout; only the
+ * summation order differs. */
+template <int HD, int G>
+__global__ __launch_bounds__(64) void flash_prefill_kernel(AttnArgs a) {
+  constexpr int TPT = 16 / G; /* tokens per tile */
+  constexpr int NS = HD / 4;  /* QK^T MFMA steps */
+  constexpr int ND = HD / 16; /* output tiles over the head dimension */
+  const int lane = threadIdx.x, c = lane & 15, j = lane >> 4;
+  /* heavy (late) tiles first */
+  const int tile = gridDim.x - 1 - blockIdx.x, g = blockIdx.y;
+  const int t0 = tile * TPT;
+  const int last = min(t0 + TPT, a.ntok) - 1;
+  const int pmax = a.pos + last; /* last key any row of the tile needs */
+  /* B operand of S^T: row c's query, dims NS j .. NS j + NS - 1 */
+  const int qt = min(t0 + c / G, a.ntok - 1), qh = g * G + c % G;
+  float qv[NS];
+  {
+    const float *qp = a.q + (size_t)qt * a.q_stride + (size_t)qh * HD + NS * j;
+#pragma unroll
+    for (int s4 = 0; s4 < NS / 4; s4++) {
+      const float4 v = gld<float4>(qp + 4 * s4);
+      qv[4 * s4] = v.x, qv[4 * s4 + 1] = v.y, qv[4 * s4 + 2] = v.z, qv[4 * s4 + 3] = v.w;
+    }
+  }
+  const int cpos = a.pos + t0 + c / G; /* row c's position (S^T layout) */
+  const float *K = a.k + (size_t)g * a.max_seq * HD;
+  const float *V = a.v + (size_t)g * a.max_seq * HD;
+  float m = -INFINITY, l = 0.f;
+  gq_f32x4 o[ND];
+#pragma unroll
+  for (int d = 0; d < ND; d++) o[d] = gq_f32x4{0.f, 0.f, 0.f, 0.f};
+  const int nblk = pmax / 16 + 1;
+  /* K row key0 + c, dims NS j ..; V rows key0 + 4 j + i, dims ND c ..
+   * (rows past pmax are never weighted: zeroed so stale cache contents
+   * cannot leak in as 0 * inf).  Block b + 1 loads while block b computes. */
+  float kv[NS], vv[4][ND];
+  auto load = [&](int key0, float (&kq)[NS], float (&vq)[4][ND]) {
+    const float *kp = K + (size_t)min(key0 + c, a.max_seq - 1) * HD + NS * j;
+#pragma unroll
+    for (int s4 = 0; s4 < NS / 4; s4++) {
+      const float4 v = gld<float4>(kp + 4 * s4);
+      kq[4 * s4] = v.x, kq[4 * s4 + 1] = v.y, kq[4 * s4 + 2] = v.z, kq[4 * s4 + 3] = v.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int key = key0 + 4 * j + i;
+      const float *vp = V + (size_t)min(key, a.max_seq - 1) * HD + ND * c;
+#pragma unroll
+      for (int d4 = 0; d4 < ND / 4; d4++) {
+        float4 v = gld<float4>(vp + 4 * d4);
+        if (key > pmax) v = make_float4(0.f, 0.f, 0.f, 0.f);
+        vq[i][4 * d4] = v.x, vq[i][4 * d4 + 1] = v.y, vq[i][4 * d4 + 2] = v.z, vq[i][4 * d4 + 3] = v.w;
+      }
+    }
+  };
+  /* one key block: S^T (four independent MFMA chains), mask, online
+   * softmax, rescale, O += P V */
+  auto step = [&](int key0, const float (&kq)[NS], const float (&vq)[4][ND]) {
+    gq_f32x4 sp[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) sp[u] = gq_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NS; s++) sp[s & 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(kq[s], qv[s], sp[s & 3], 0, 0, 0);
+    const gq_f32x4 st = (sp[0] + sp[1]) + (sp[2] + sp[3]);
+    /* st[i] = q(row c) . k(key0 + 4 j + i) */
+    float sv[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) sv[i] = key0 + 4 * j + i <= cpos ? st[i] * a.scale : -INFINITY;
+    float mb = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
+    mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+    const float mn = fmaxf(m, mb); /* finite: key 0 is visible to every row */
+    const float alpha = __expf(m - mn);
+    float p[4], lb = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      p[i] = __expf(sv[i] - mn);
+      lb += p[i];
+    }
+    lb += __shfl_xor(lb, 16, 64);
+    lb += __shfl_xor(lb, 32, 64);
+    l = __builtin_fmaf(l, alpha, lb);
+    m = mn;
+    /* O rows 4 j + i take the rescale of row 4 j + i (held by lane 4 j + i) */
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float al = __shfl(alpha, 4 * j + i, 64);
+#pragma unroll
+      for (int d = 0; d < ND; d++) o[d][i] *= al;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int d = 0; d < ND; d++) o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[i], vq[i][d], o[d], 0, 0, 0);
+  };
+  /* two register buffers, block b + 1 loading while block b computes */
+  float k2[NS], v2[4][ND];
+  load(0, kv, vv);
+  for (int b = 0; b < nblk; b += 2) {
+    if (b + 1 < nblk) load(16 * (b + 1), k2, v2);
+    step(16 * b, kv, vv);
+    if (b + 1 >= nblk) break;
+    if (b + 2 < nblk) load(16 * (b + 2), kv, vv);
+    step(16 * (b + 1), k2, v2);
+  }
+  /* out[row] = O[row] / l[row]; row 4 j + i -> token t0 + row / G, head
+   * g G + row % G */
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int row = 4 * j + i, t = t0 + row / G, h = g * G + row % G;
+    const float inv = 1.0f / __shfl(l, row, 64);
+    if (t < a.ntok) {
+      const size_t base = (size_t)t * a.out_stride + (size_t)h * HD + ND * c;
+#pragma unroll
+      for (int d4 = 0; d4 < ND / 4; d4++) {
+        const float4 v = make_float4(o[4 * d4][i] * inv, o[4 * d4 + 1][i] * inv, o[4 * d4 + 2][i] * inv,
+                                     o[4 * d4 + 3][i] * inv);
+        if (a.out16) {
+          uint2 u;
+          u.x = __builtin_bit_cast(uint32_t, __builtin_convertvector((gq_f2a){v.x, v.y}, gq_bf2a));
+          u.y = __builtin_bit_cast(uint32_t, __builtin_convertvector((gq_f2a){v.z, v.w}, gq_bf2a));
+          gst<uint2>(a.out16 + base + 4 * d4, u);
+        } else {
+          gst<float4>(a.out + base + 4 * d4, v);
+        }
+      }
+    }
+  }
+}
+
+template <int HD, int G>
+int launch_flash(const AttnArgs &a, hipStream_t s) {
+  hipLaunchKernelGGL((flash_prefill_kernel<HD, G>), dim3((a.ntok + 16 / G - 1) / (16 / G), a.n_kv), dim3(64), 0, s,
+                     a);
   return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+} // namespace
+
+int gq_launch_flash_prefill(const AttnArgs &a, hipStream_t s) {
+  if (a.n_kv <= 0 || a.n_heads % a.n_kv || a.ntok < 1 || a.pos < 0 || a.pos + a.ntok > a.max_seq) return -1;
+  const int G = a.n_heads / a.n_kv;
+  if (a.hd == 128 && G == 4) return launch_flash<128, 4>(a, s);
+  if (a.hd == 128 && G == 8) return launch_flash<128, 8>(a, s);
+  if (a.hd == 128 && G == 1) return launch_flash<128, 1>(a, s);
+  if (a.hd == 128 && G == 2) return launch_flash<128, 2>(a, s);
+  if (a.hd == 64 && G == 4) return launch_flash<64, 4>(a, s);
+  if (a.hd == 64 && G == 8) return launch_flash<64, 8>(a, s);
+  if (a.hd == 64 && G == 1) return launch_flash<64, 1>(a, s);
+  if (a.hd == 64 && G == 2) return launch_flash<64, 2>(a, s);
+  return -1;
 }
 
 int gq_launch_rope_append(const RopeArgs &a, hipStream_t s) {

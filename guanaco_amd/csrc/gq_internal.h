@@ -72,19 +72,21 @@ struct AttnArgs {
   int pos;
   int n_heads, n_kv, hd, max_seq, nch, s_max;
   float scale;
-  /* a chunk of ntok query tokens at positions pos .. pos + ntok - 1 (causal:
-   * token t attends to 0 .. pos + t); per-token strides in floats.  Decode
-   * launches leave these zero (one token). */
+  /* the prefill form (gq_launch_flash_prefill): ntok query tokens at
+   * positions pos .. pos + ntok - 1, token t attending to 0 .. pos + t;
+   * per-token strides in elements; out16 != NULL writes bf16 there instead
+   * of fp32 to out.  Decode launches leave these zero. */
   int ntok, q_stride, out_stride;
-  size_t po_stride, pml_stride;
-  __bf16 *out16; /* chunk form: bf16 output (stride out_stride) instead of out */
+  __bf16 *out16;
 };
 int gq_attn_nch(int n_kv, int max_seq);
 int gq_attn_smax(int max_seq, int nch);
 int gq_launch_attention(const AttnArgs &a, hipStream_t s, hipEvent_t mid);
-/* The chunk form: a.ntok tokens, a.nch = chunks of the longest row
- * (ceil((pos + ntok) / 128)), partial buffers of ntok * stride floats. */
-int gq_launch_attention_chunk(const AttnArgs &a, hipStream_t s);
+/* Causal attention of a prefill chunk (a.ntok tokens at a.pos, their keys
+ * already appended) by the fp32-MFMA flash kernel: q, q_stride, k, v, out
+ * or out16, out_stride, pos, ntok, n_heads, n_kv, hd (64 or 128), max_seq
+ * and scale are used. */
+int gq_launch_flash_prefill(const AttnArgs &a, hipStream_t s);
 
 struct RopeArgs {
   float *q;

@@ -41,16 +41,13 @@ struct PrefillWs {
   int cap = 0;
   float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr; /* fp32: hidden, q/k/v for RoPE */
   __bf16 *xn = nullptr, *att = nullptr, *act = nullptr;          /* bf16 GEMM inputs */
-  float *po = nullptr, *pml = nullptr;
   __bf16 *xb = nullptr; /* op-level entry: bf16 copy of its fp32 x */
   int *tok = nullptr;
-  size_t po_cap = 0, pml_cap = 0, xb_cap = 0;
+  size_t xb_cap = 0;
 };
 
 /* tokens per prefill chunk */
 constexpr int kPrefillChunk = 512;
-/* bytes of attention partials one chunk launch may use */
-constexpr size_t kPrefillPartBytes = (size_t)64 << 20;
 
 } // namespace
 
@@ -954,8 +951,8 @@ static bool pf_model_ok(const gq_ctx *c) {
 static PgSeg pg_seg(const gq_weight &w, float *y) { return PgSeg{(const uint8_t *)w.data, y, w.rows, w.dtype}; }
 
 /* RoPE + append of T tokens at pos..pos+T-1 (q: T x n_heads*hd in place,
- * k/v: T x n_kv*hd), then causal attention into out (T x n_heads*hd), in
- * token sub-batches that keep the partials under kPrefillPartBytes */
+ * k/v: T x n_kv*hd), then causal attention of the T tokens into out (fp32)
+ * or out16 (bf16), T x n_heads*hd */
 static int pf_attention(gq_ctx *c, int layer, int pos, int T, int n_heads, float *q, const float *k, const float *v,
                         float *out, __bf16 *out16) {
   const int hd = c->kv_hd, kvd = c->kv_heads * hd, qd = n_heads * hd;
@@ -963,29 +960,12 @@ static int pf_attention(gq_ctx *c, int layer, int pos, int T, int n_heads, float
               n_heads, c->kv_heads, hd, c->kv_max_seq, T, qd, kvd, kvd};
   int rc = gq_launch_rope_append(ra, c->stream);
   if (rc) return rc;
-  PrefillWs &w = c->pf;
-  for (int t0 = 0; t0 < T;) {
-    const int nch_all = (pos + T + 127) / 128;
-    const size_t per_tok = (size_t)n_heads * nch_all * (hd + 2) * sizeof(float);
-    const int nt = std::max(1, std::min(T - t0, (int)(kPrefillPartBytes / per_tok)));
-    AttnArgs aa{};
-    aa.pos = pos + t0, aa.ntok = nt;
-    aa.nch = (pos + t0 + nt + 127) / 128;
-    aa.po_stride = (size_t)n_heads * aa.nch * hd, aa.pml_stride = (size_t)n_heads * aa.nch * 2;
-    if ((rc = pf_ensure(c, w.po, w.po_cap, aa.po_stride * nt)) ||
-        (rc = pf_ensure(c, w.pml, w.pml_cap, aa.pml_stride * nt)))
-      return rc;
-    aa.q = q + (size_t)t0 * qd, aa.q_stride = qd;
-    aa.k = gq_hip_kv_k(c, layer), aa.v = gq_hip_kv_v(c, layer);
-    aa.part_o = w.po, aa.part_ml = w.pml;
-    aa.out = out ? out + (size_t)t0 * qd : nullptr, aa.out_stride = qd;
-    aa.out16 = out16 ? out16 + (size_t)t0 * qd : nullptr;
-    aa.n_heads = n_heads, aa.n_kv = c->kv_heads, aa.hd = hd, aa.max_seq = c->kv_max_seq;
-    aa.s_max = gq_attn_smax(c->kv_max_seq, aa.nch), aa.scale = 1.0f / sqrtf((float)hd);
-    if ((rc = gq_launch_attention_chunk(aa, c->stream))) return rc;
-    t0 += nt;
-  }
-  return 0;
+  AttnArgs aa{};
+  aa.q = q, aa.q_stride = qd, aa.k = gq_hip_kv_k(c, layer), aa.v = gq_hip_kv_v(c, layer);
+  aa.out = out, aa.out16 = out16, aa.out_stride = qd, aa.pos = pos, aa.ntok = T;
+  aa.n_heads = n_heads, aa.n_kv = c->kv_heads, aa.hd = hd, aa.max_seq = c->kv_max_seq;
+  aa.scale = 1.0f / sqrtf((float)hd);
+  return gq_launch_flash_prefill(aa, c->stream);
 }
 
 /* one layer over the chunk (engine.c:352-554 with T tokens): 7 launches of

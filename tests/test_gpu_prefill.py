@@ -14,9 +14,9 @@ same seeded inputs:
   approximate, engine.c:119-152).  bf16 inputs cost ~2^-9 relative per
   product: tolerance 1e-2 relative L2 (observed ~3e-3).
 
-RoPE + append + causal attention of T tokens: the cache rows bit-exact with
-the oracle's RoPE, each token's attention bit-identical to the decode kernel
-at its position (the same arithmetic) and within 1e-5 of the oracle.
+RoPE + append + causal attention of T tokens (the fp32-MFMA flash kernel):
+the cache rows bit-exact with the oracle's RoPE, each token's attention
+within 1e-5 of the oracle and of the decode kernel at its position.
 
 Whole-model prefill (forward() over a prompt, engine.c:559-595) against T
 sequential oracle steps (bit-exact with the reference's forward()): the
@@ -149,9 +149,11 @@ def test_prefill_gate_up_swiglu(ctx, orc, dtype, T, N, K):
 
 @pytest.mark.parametrize("nh,nkv,hd,pre,T,ms", [
     (32, 8, 128, 0, 512, 640),     # config 5: a 512-token chunk from position 0
-    (32, 8, 128, 300, 200, 640),   # after a cached prefix, chunk boundary inside
-    (32, 4, 64, 5, 130, 160),      # TinyLlama shape, ends near the cache end
+    (32, 8, 128, 300, 200, 640),   # after a cached prefix
+    (32, 4, 64, 5, 130, 135),      # TinyLlama shape, ends at the cache end (max_seq % 16 != 0)
     (8, 8, 64, 0, 3, 16),          # G = 1, three tokens
+    (64, 8, 128, 7, 33, 64),       # G = 8, two tokens per tile
+    (16, 8, 64, 1, 21, 40),        # G = 2
 ])
 def test_prefill_attention(ctx, orc, nh, nkv, hd, pre, T, ms):
     from oracle import HostKV, fptr
@@ -182,14 +184,16 @@ def test_prefill_attention(ctx, orc, nh, nkv, hd, pre, T, ms):
     kvv[:, pre:pre + T] = v.reshape(T, nkv, hd).transpose(1, 0, 2)
     dk, dv = ctx.kv_read_layer(0)
     assert np.array_equal(bits(dk), bits(kv.k)) and np.array_equal(bits(dv), bits(kv.v))
-    # each token: the decode kernel at its position bit for bit, the oracle to 1e-5
+    # each token against the oracle (fp32 throughout, only the summation
+    # order differs) and against the decode kernel at its position
     q1, o1 = ctx.alloc(4 * nh * hd), ctx.alloc(4 * nh * hd)
-    for t in sorted({0, 1, T // 2, T - 2, T - 1} & set(range(T))):
-        q1.upload(qr[t])
-        assert ctx.attention_dev(0, pre + t, nh, q1, o1) == 0
-        assert np.array_equal(bits(o1.download()), bits(out[t])), t
+    for t in sorted({0, 1, 2, 15, 16, 17, T // 2, T - 2, T - 1} & set(range(T))):
         ref = orc.attention(qr[t], kv, 0, nh, pre + t)
         assert rel_l2(out[t], ref) < 1e-5, t
+        if nh // nkv in (1, 4, 8):  # the decode kernel's group sizes
+            q1.upload(qr[t])
+            assert ctx.attention_dev(0, pre + t, nh, q1, o1) == 0
+            assert rel_l2(out[t], o1.download()) < 1e-5, t
     for b in (qb, kb, vb, ob, q1, o1):
         b.free()
 
