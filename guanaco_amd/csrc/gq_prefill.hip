@@ -33,6 +33,7 @@
  * D[i][j] element 4 (i / 8) + i % 4 of lane j + 32 ((i / 4) % 2).
  */
 #include <algorithm>
+#include <cstdlib>
 
 #include "gq_device.h"
 #include "gq_internal.h"
@@ -217,44 +218,52 @@ struct PW<GQ_Q6_K> {
   }
 };
 
-template <int DT>
+/* KS = 1 or 2 K-splits per workgroup: with KS = 2, eight waves, the second
+ * four running the upper half of K for the same tile; their sums are added
+ * through LDS at the end.  Two waves per SIMD hide each other's LDS, DMA and
+ * MFMA latencies. */
+template <int DT, int KS>
 constexpr int stage_bytes() {
-  return kXBytes + 4 * PW<DT>::kWaveLds;
+  return KS * kXBytes + 4 * KS * PW<DT>::kWaveLds;
 }
 
 /* Steps in the LDS ring: as deep as LDS and the 6-bit vmcnt allow (each
  * wave keeps (ring - 2) steps of DMA instructions in flight while it waits) */
-template <int DT>
+template <int DT, int KS>
 constexpr int ring() {
-  return DT == GQ_Q4_K ? 4 : 4;
+  return KS == 1 ? 4 : (DT == GQ_Q4_K ? 4 : 3);
 }
-template <int DT>
+template <int DT, int KS>
 constexpr int ring_bytes() {
-  return ring<DT>() * stage_bytes<DT>();
+  return ring<DT, KS>() * stage_bytes<DT, KS>();
 }
-static_assert(ring<GQ_Q4_K>() >= 3 && ring<GQ_Q6_K>() >= 3, "the pipeline reads two slots");
-static_assert((ring<GQ_Q4_K>() - 2) * (2 + PW<GQ_Q4_K>::kDma) < 64, "vmcnt range");
-static_assert((ring<GQ_Q6_K>() - 2) * (2 + PW<GQ_Q6_K>::kDma) < 64, "vmcnt range");
+static_assert(ring<GQ_Q4_K, 2>() >= 3 && ring<GQ_Q6_K, 2>() >= 3, "the pipeline reads two slots");
+static_assert((4 - 2) * (2 + PW<GQ_Q4_K>::kDma) < 64 && (4 - 2) * (2 + PW<GQ_Q6_K>::kDma) < 64, "vmcnt range");
+static_assert(ring_bytes<GQ_Q4_K, 2>() <= 160 * 1024 && ring_bytes<GQ_Q6_K, 2>() <= 160 * 1024, "LDS");
 
-/* One tile: tokens t0 .. t0+63 against this wave's 32 rows starting at w.
- * acc[i] holds tokens t0 + 32 i + (D layout rows) for row (lane & 31). */
-template <int DT>
+/* One tile: tokens t0 .. t0+63 against this wave's 32 rows starting at w,
+ * K-split kh of KS.  acc[i] holds tokens t0 + 32 i + (D layout rows) for
+ * row (lane & 31). */
+template <int DT, int KS>
 __device__ __forceinline__ void tile_loop(const PgArgs &a, const uint8_t *w, uint32_t rowbytes, int t0,
                                           GQ_LDS uint8_t *smem, gq_f32x16 acc[2]) {
-  constexpr int SB = stage_bytes<DT>();
+  constexpr int SB = stage_bytes<DT, KS>();
   constexpr int NPS = 2 + PW<DT>::kDma; /* DMA instructions per wave and step */
-  constexpr int kRing = ring<DT>();
+  constexpr int kRing = ring<DT, KS>();
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nsteps = a.K / kBK;
+  const int kh = wave >> 2, rw = wave & 3;
+  const int ns = a.K / kBK / KS, s0 = kh * ns; /* this split's steps: s0 .. s0 + ns - 1 */
   typename PW<DT>::Plan pl;
   PW<DT>::plan(pl, lane, rowbytes);
   const uint32_t sbase = (uint32_t)(uintptr_t)smem;
-  /* X DMA: instruction j of wave w covers tokens 8 (2w + j) + lane / 8; lane
-   * position q = lane % 8 of the token's LDS row fetches octet q ^ swz */
+  const uint32_t xreg = (uint32_t)(kh * kXBytes), wreg = (uint32_t)(KS * kXBytes + wave * PW<DT>::kWaveLds);
+  /* X DMA: instruction j of wave rw covers tokens 8 (2 rw + j) + lane / 8;
+   * lane position q = lane % 8 of the token's LDS row fetches octet
+   * q ^ ((token / 2) % 8) */
   const __bf16 *xsrc[2];
 #pragma unroll
   for (int j = 0; j < 2; j++) {
-    const int tl = 8 * (2 * wave + j) + (lane >> 3), q = lane & 7;
+    const int tl = 8 * (2 * rw + j) + (lane >> 3), q = lane & 7;
     const int oct = q ^ ((tl >> 1) & 7);
     xsrc[j] = a.x + (size_t)min(t0 + tl, a.T - 1) * a.K + 8 * oct;
   }
@@ -262,10 +271,11 @@ __device__ __forceinline__ void tile_loop(const PgArgs &a, const uint8_t *w, uin
     const uint32_t slot = sbase + (uint32_t)((st % kRing) * SB);
 #pragma unroll
     for (int j = 0; j < 2; j++)
-      dma16(xsrc[j] + st * kBK, __builtin_amdgcn_readfirstlane(slot + 1024u * (uint32_t)(2 * wave + j)));
-    PW<DT>::issue(pl, w, st, slot + kXBytes + (uint32_t)(wave * PW<DT>::kWaveLds));
+      dma16(xsrc[j] + (s0 + st) * kBK,
+            __builtin_amdgcn_readfirstlane(slot + xreg + 1024u * (uint32_t)(2 * rw + j)));
+    PW<DT>::issue(pl, w, s0 + st, slot + wreg);
   };
-  for (int st = 0; st < kRing - 1 && st < nsteps; st++) issue(st);
+  for (int st = 0; st < kRing - 1 && st < ns; st++) issue(st);
   acc[0] = gq_f32x16{};
   acc[1] = gq_f32x16{};
   const int h = lane >> 5, i32 = lane & 31;
@@ -283,30 +293,30 @@ __device__ __forceinline__ void tile_loop(const PgArgs &a, const uint8_t *w, uin
 #pragma unroll
     for (int i = 0; i < 2; i++) {
       const int tl = 32 * i + i32, q = (2 * kk + h) ^ ((tl >> 1) & 7);
-      aoff[kk][i] = (uint32_t)((tl * 8 + q) * 16);
+      aoff[kk][i] = xreg + (uint32_t)((tl * 8 + q) * 16);
     }
-  auto wslot = [&](int st) { return smem + (st % kRing) * SB + kXBytes + wave * PW<DT>::kWaveLds; };
+  auto wslot = [&](int st) { return smem + (st % kRing) * SB + wreg; };
   gq_bf16x8 b[4], av[4][2];
   typename PW<DT>::Raw raw;
-  wait_groups<NPS, kRing - 2>(nsteps - 1);
+  wait_groups<NPS, kRing - 2>(ns - 1);
   __syncthreads();
-  PW<DT>::read(raw, wslot(0), lane, 0);
+  PW<DT>::read(raw, wslot(0), lane, s0);
 #pragma unroll
   for (int kk = 0; kk < 4; kk++)
 #pragma unroll
     for (int i = 0; i < 2; i++) av[kk][i] = lld<gq_bf16x8>(smem, aoff[kk][i]);
-  PW<DT>::dequant(raw, 0, b);
-  for (int s = 0; s < nsteps; s++) {
-    if (s + 1 < nsteps) wait_groups<NPS, kRing - 3>(nsteps - 2 - s);
+  PW<DT>::dequant(raw, s0, b);
+  for (int s = 0; s < ns; s++) {
+    if (s + 1 < ns) wait_groups<NPS, kRing - 3>(ns - 2 - s);
     __syncthreads();
-    if (s + kRing - 1 < nsteps) issue(s + kRing - 1);
+    if (s + kRing - 1 < ns) issue(s + kRing - 1);
     /* LDS reads for step s + 1 first, so their latency hides behind the
      * MFMAs of step s */
     gq_bf16x8 an[4][2];
-    const bool more = s + 1 < nsteps;
+    const bool more = s + 1 < ns;
     if (more) {
       const GQ_LDS uint8_t *xn = smem + ((s + 1) % kRing) * SB;
-      PW<DT>::read(raw, wslot(s + 1), lane, s + 1);
+      PW<DT>::read(raw, wslot(s + 1), lane, s0 + s + 1);
 #pragma unroll
       for (int kk = 0; kk < 4; kk++)
 #pragma unroll
@@ -317,7 +327,7 @@ __device__ __forceinline__ void tile_loop(const PgArgs &a, const uint8_t *w, uin
 #pragma unroll
       for (int i = 0; i < 2; i++) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[kk][i], b[kk], acc[i], 0, 0, 0);
     if (more) {
-      PW<DT>::dequant(raw, s + 1, b);
+      PW<DT>::dequant(raw, s0 + s + 1, b);
 #pragma unroll
       for (int kk = 0; kk < 4; kk++)
 #pragma unroll
@@ -331,63 +341,83 @@ __device__ __forceinline__ int tile_token(int i, int e, int lane) {
 }
 
 /* Grid: x = row tiles over the segments (kBN rows each; MV_SWIGLU: 64 gate
- * rows with the same 64 up rows), y = token tiles. */
-template <int MODE>
-__global__ __launch_bounds__(kPThreads) void pgemm_kernel(PgArgs a) {
+ * rows with the same 64 up rows), y = token tiles; 256 KS threads. */
+template <int MODE, int KS>
+__global__ __launch_bounds__(kPThreads * KS) void pgemm_kernel(PgArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t pg_smem[];
   GQ_LDS uint8_t *smem = (GQ_LDS uint8_t *)pg_smem;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kh = wave >> 2, rw = wave & 3;
   const int t0 = blockIdx.y * kBM;
   int sg = 0, tb = blockIdx.x;
   if (MODE != MV_SWIGLU)
     while (sg + 1 < a.nseg && tb >= a.seg[sg].rows / kBN) tb -= a.seg[sg].rows / kBN, sg++;
   /* this wave's weights: rows r0 .. r0 + 31 of segment ws */
-  int ws = sg, r0 = tb * kBN + 32 * wave;
-  if (MODE == MV_SWIGLU) ws = wave >> 1, r0 = tb * (kBN / 2) + 32 * (wave & 1);
+  int ws = sg, r0 = tb * kBN + 32 * rw;
+  if (MODE == MV_SWIGLU) ws = rw >> 1, r0 = tb * (kBN / 2) + 32 * (rw & 1);
   const PgSeg &S = a.seg[ws];
   const int dt = a.seg[sg].dtype;
   const uint32_t rowbytes = (uint32_t)(a.K / 256) * (dt == GQ_Q4_K ? 144u : 210u);
   const uint8_t *w = S.w + (size_t)r0 * rowbytes;
   gq_f32x16 acc[2];
   if (dt == GQ_Q4_K)
-    tile_loop<GQ_Q4_K>(a, w, rowbytes, t0, smem, acc);
+    tile_loop<GQ_Q4_K, KS>(a, w, rowbytes, t0, smem, acc);
   else
-    tile_loop<GQ_Q6_K>(a, w, rowbytes, t0, smem, acc);
+    tile_loop<GQ_Q6_K, KS>(a, w, rowbytes, t0, smem, acc);
+  GQ_LDS float *xk = (GQ_LDS float *)smem;
+  if (KS == 2) { /* add the upper K half (waves 4..7) into waves 0..3, in a fixed order */
+    __syncthreads(); /* every wave is done reading the ring */
+    if (kh == 1) {
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) xk[((rw * 2 + i) * 16 + e) * 64 + lane] = acc[i][e];
+    }
+    __syncthreads();
+    if (kh == 0) {
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[i][e] += xk[((rw * 2 + i) * 16 + e) * 64 + lane];
+    }
+  }
   const int n = r0 + (lane & 31);
   if (MODE != MV_SWIGLU) {
+    if (kh == 0) {
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+      for (int i = 0; i < 2; i++)
 #pragma unroll
-      for (int e = 0; e < 16; e++) {
-        const int t = t0 + tile_token(i, e, lane);
-        if (t < a.T) {
-          float v = acc[i][e];
-          float *y = S.y + (size_t)t * S.rows + n;
-          if (MODE == MV_RESID) v = gld<float>(y) + v;
-          gst<float>(y, v);
+        for (int e = 0; e < 16; e++) {
+          const int t = t0 + tile_token(i, e, lane);
+          if (t < a.T) {
+            float v = acc[i][e];
+            float *y = S.y + (size_t)t * S.rows + n;
+            if (MODE == MV_RESID) v = gld<float>(y) + v;
+            gst<float>(y, v);
+          }
         }
-      }
+    }
     return;
   }
-  /* SwiGLU: the up waves (2, 3) hand their tiles to the gate waves (0, 1)
-   * through LDS; act = (g * sigmoid(g)) * u as silu_inplace then
+  /* SwiGLU: the up waves (rw 2, 3) hand their tiles to the gate waves (rw 0,
+   * 1) through LDS; act = (g * sigmoid(g)) * u as silu_inplace then
    * elemwise_mul (kernels_cpu.c:312-389), rounded to bf16 */
-  __syncthreads(); /* every wave is done reading the ring */
-  GQ_LDS float *xch = (GQ_LDS float *)smem;
-  if (wave >= 2) {
+  __syncthreads(); /* the ring (and the K-half exchange) are free */
+  GQ_LDS float *xch = (GQ_LDS float *)(smem + (KS == 2 ? 4 * 2 * 16 * 64 * 4 : 0));
+  if (kh == 0 && rw >= 2) {
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
-      for (int e = 0; e < 16; e++) xch[(((wave - 2) * 2 + i) * 16 + e) * 64 + lane] = acc[i][e];
+      for (int e = 0; e < 16; e++) xch[(((rw - 2) * 2 + i) * 16 + e) * 64 + lane] = acc[i][e];
   }
   __syncthreads();
-  if (wave < 2) {
+  if (kh == 0 && rw < 2) {
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
       for (int e = 0; e < 16; e++) {
         const int t = t0 + tile_token(i, e, lane);
-        const float g = acc[i][e], u = xch[((wave * 2 + i) * 16 + e) * 64 + lane];
+        const float g = acc[i][e], u = xch[((rw * 2 + i) * 16 + e) * 64 + lane];
         const float sig = 1.0f / (1.0f + expf(0.0f - g));
         const __bf16 v = (__bf16)((g * sig) * u);
         if (t < a.T) gst<unsigned short>(a.act + (size_t)t * S.rows + n, __builtin_bit_cast(unsigned short, v));
@@ -400,21 +430,48 @@ __global__ void to_bf16_kernel(const float *x, __bf16 *y, size_t n) {
   if (i < n) y[i] = (__bf16)x[i];
 }
 
-template <int MODE>
-int launch_mode(const PgArgs &a, int row_tiles, hipStream_t s) {
-  bool q6 = false;
-  for (int i = 0; i < a.nseg; i++) q6 |= a.seg[i].dtype == GQ_Q6_K;
-  bool q4 = false;
-  for (int i = 0; i < a.nseg; i++) q4 |= a.seg[i].dtype == GQ_Q4_K;
-  const size_t lds = std::max(q6 ? ring_bytes<GQ_Q6_K>() : 0, q4 ? ring_bytes<GQ_Q4_K>() : 0);
+/* K-splits per workgroup: 2 when the grid has at most one workgroup per
+ * CU (a second wave per SIMD then comes from the split), 1 when it has
+ * more (two workgroups per CU already give two waves per SIMD);
+ * GQ_PG_KS=1 or 2 overrides, for timing */
+int pg_ks(int wgs) {
+  static const int forced = [] {
+    const char *e = getenv("GQ_PG_KS");
+    return e ? atoi(e) : 0;
+  }();
+  static const int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev))
+      return 256;
+    return n > 0 ? n : 256;
+  }();
+  if (forced == 1 || forced == 2) return forced;
+  return wgs <= cus ? 2 : 1;
+}
+
+template <int MODE, int KS>
+int launch_ks(const PgArgs &a, int row_tiles, size_t lds, hipStream_t s) {
   static bool attr_done = false;
   if (!attr_done) {
-    (void)hipFuncSetAttribute((const void *)pgemm_kernel<MODE>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              std::max(ring_bytes<GQ_Q6_K>(), ring_bytes<GQ_Q4_K>()));
+    (void)hipFuncSetAttribute((const void *)pgemm_kernel<MODE, KS>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              160 * 1024);
     attr_done = true;
   }
-  hipLaunchKernelGGL((pgemm_kernel<MODE>), dim3(row_tiles, (a.T + kBM - 1) / kBM), dim3(kPThreads), lds, s, a);
+  hipLaunchKernelGGL((pgemm_kernel<MODE, KS>), dim3(row_tiles, (a.T + kBM - 1) / kBM), dim3(kPThreads * KS), lds, s,
+                     a);
   return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+template <int MODE>
+int launch_mode(const PgArgs &a, int row_tiles, hipStream_t s) {
+  bool q4 = false, q6 = false;
+  for (int i = 0; i < a.nseg; i++) q4 |= a.seg[i].dtype == GQ_Q4_K, q6 |= a.seg[i].dtype == GQ_Q6_K;
+  if (pg_ks(row_tiles * ((a.T + kBM - 1) / kBM)) == 2 && (a.K / kBK) % 2 == 0) {
+    const size_t lds = std::max(q6 ? ring_bytes<GQ_Q6_K, 2>() : 0, q4 ? ring_bytes<GQ_Q4_K, 2>() : 0);
+    return launch_ks<MODE, 2>(a, row_tiles, lds, s);
+  }
+  const size_t lds = std::max(q6 ? ring_bytes<GQ_Q6_K, 1>() : 0, q4 ? ring_bytes<GQ_Q4_K, 1>() : 0);
+  return launch_ks<MODE, 1>(a, row_tiles, lds, s);
 }
 
 } // namespace
@@ -434,9 +491,12 @@ int gq_launch_pgemm(int mode, const PgArgs &a, hipStream_t s) {
       tiles += g.rows / kBN;
     }
   }
-  /* the SwiGLU exchange (16 KB) reuses the ring, which is larger */
-  static_assert(ring_bytes<GQ_Q4_K>() >= 2 * 2 * 16 * 64 * 4 && ring_bytes<GQ_Q6_K>() >= 2 * 2 * 16 * 64 * 4,
+  /* the K-half exchange (32 KB) and the SwiGLU exchange (16 KB) reuse the
+   * ring, which is larger */
+  static_assert(ring_bytes<GQ_Q4_K, 1>() >= 2 * 2 * 16 * 64 * 4 && ring_bytes<GQ_Q6_K, 1>() >= 2 * 2 * 16 * 64 * 4,
                 "exchange fits the ring");
+  static_assert(ring_bytes<GQ_Q4_K, 2>() >= 6 * 2 * 16 * 64 * 4 && ring_bytes<GQ_Q6_K, 2>() >= 6 * 2 * 16 * 64 * 4,
+                "exchanges fit the ring");
   if (mode == MV_SWIGLU) {
     if (a.nseg != 2 || !a.act) return -1;
     return launch_mode<MV_SWIGLU>(a, a.seg[0].rows / (kBN / 2), s);
