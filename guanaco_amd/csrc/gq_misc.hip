@@ -14,7 +14,12 @@ namespace {
 constexpr int kThreads = 256;
 
 /* out = w * (x * 1/sqrt(mean(x^2) + eps)) (kernels_cpu.c:199-265); one
- * workgroup per row (blockIdx.x), sum of squares in a fixed tree order. */
+ * workgroup per row (blockIdx.x), sum of squares in a fixed tree order.  A
+ * row of up to kNormVec * 4 * kThreads floats is read once into registers
+ * (float4 per thread and pass) when dim % 4 == 0 and rows are 16-byte
+ * aligned; other shapes take the scalar two-pass loop. */
+constexpr int kNormVec = 16;
+
 __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *x, const float *w, float *out,
                                                           int dim, float eps, __bf16 *out16) {
   __shared__ float red[kThreads / GQ_WAVE];
@@ -22,8 +27,23 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *x, const
   x += (size_t)blockIdx.x * dim;
   out += (size_t)blockIdx.x * dim;
   if (out16) out16 += (size_t)blockIdx.x * dim;
+  const bool vec = (dim & 3) == 0 && dim <= kNormVec * 4 * kThreads && (((uintptr_t)x | (uintptr_t)out) & 15) == 0 &&
+                   (!w || ((uintptr_t)w & 15) == 0) && (!out16 || ((uintptr_t)out16 & 7) == 0);
+  float4 xv[kNormVec];
   float ss = 0.f;
-  for (int i = tid; i < dim; i += kThreads) ss = __builtin_fmaf(x[i], x[i], ss);
+  if (vec) {
+#pragma unroll
+    for (int k = 0; k < kNormVec; k++) {
+      const int e = 4 * (tid + k * kThreads);
+      if (e < dim) {
+        xv[k] = gld<float4>(x + e);
+        ss = __builtin_fmaf(xv[k].x, xv[k].x, ss), ss = __builtin_fmaf(xv[k].y, xv[k].y, ss);
+        ss = __builtin_fmaf(xv[k].z, xv[k].z, ss), ss = __builtin_fmaf(xv[k].w, xv[k].w, ss);
+      }
+    }
+  } else {
+    for (int i = tid; i < dim; i += kThreads) ss = __builtin_fmaf(x[i], x[i], ss);
+  }
   ss = gq_wave_sum(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
@@ -31,6 +51,28 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *x, const
   tot = tot / (float)dim;
   tot = tot + eps;
   const float r = 1.0f / sqrtf(tot);
+  if (vec) {
+#pragma unroll
+    for (int k = 0; k < kNormVec; k++) {
+      const int e = 4 * (tid + k * kThreads);
+      if (e < dim) {
+        const float4 wv = w ? gld<float4>(w + e) : make_float4(1.f, 1.f, 1.f, 1.f);
+        const float4 v = make_float4(wv.x * (xv[k].x * r), wv.y * (xv[k].y * r), wv.z * (xv[k].z * r),
+                                     wv.w * (xv[k].w * r));
+        if (out16) {
+          uint2 u;
+          u.x = (uint32_t)__builtin_bit_cast(unsigned short, (__bf16)v.x) |
+                ((uint32_t)__builtin_bit_cast(unsigned short, (__bf16)v.y) << 16);
+          u.y = (uint32_t)__builtin_bit_cast(unsigned short, (__bf16)v.z) |
+                ((uint32_t)__builtin_bit_cast(unsigned short, (__bf16)v.w) << 16);
+          gst<uint2>(out16 + e, u);
+        } else {
+          gst<float4>(out + e, v);
+        }
+      }
+    }
+    return;
+  }
   for (int i = tid; i < dim; i += kThreads) {
     const float v = (w ? w[i] : 1.0f) * (x[i] * r);
     if (out16)
