@@ -8,11 +8,11 @@ KV cache are resident before the timed region.  Steps start at position
 
 Prints ONE JSON line.  value = tokens/s over exactly --steps tokens between
 two device synchronisations.  roofline = the dominant kernel (the fused
-gate/up + SwiGLU matvec, mvw_kernel<Q4_K, MV_SWIGLU>): its algorithmic bytes
+gate/up + SwiGLU matvec, mvl_kernel<Q4_K, MV_SWIGLU>): its algorithmic bytes
 per launch over its average duration, measured live with HIP events around
 64 back-to-back launches cycling over the 32 layers at the same position;
 traffic = its HBM bytes per launch from the committed rocprofv3 counter runs
-(profiles/mvw_gate_up_llama8b_hbm_traffic.md).  cpu_baseline =
+(profiles/mvl_gate_up_llama8b_hbm_traffic.md).  cpu_baseline =
 the reference's own CPU forward() (oracle/_ref/libref.so) timed on this
 host on a bounded sample, or the oracle port when the reference build is
 absent.
@@ -35,7 +35,7 @@ def log(msg):
 
 
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                            "mvw_gate_up_llama8b_hbm_traffic.md")
+                            "mvl_gate_up_llama8b_hbm_traffic.md")
 
 
 def measured_traffic():
@@ -131,7 +131,7 @@ def main():
     # per-kernel-class device time of one eager step at the first timed position
     prof = dm.profile_step(start_tok, CTX)
     # the dominant kernel: the fused gate/up + SwiGLU matvec (one launch per
-    # layer, mvw_kernel<Q4_K, MV_SWIGLU>); algorithmic bytes per launch =
+    # layer, mvl_kernel<Q4_K, MV_SWIGLU>); algorithmic bytes per launch =
     # 2 x 14336 x 4096 Q4_K weights (144 B per 256) + x, norm weight, output
     gu = prof["gate_up"]
     bytes_per_launch = gu["bytes"] / max(gu["launches"], 1)
@@ -170,7 +170,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(),
-                     "kernel": "mvw_kernel<Q4_K, MV_SWIGLU> (gate/up + SwiGLU, one launch per layer)",
+                     "kernel": "mvl_kernel<Q4_K, MV_SWIGLU> (gate/up + SwiGLU, one launch per layer)",
                      "avg_launch_ms": round(avg_ms, 5), "bytes_per_launch": int(bytes_per_launch)},
         "per_token": {"weight_bytes": weight_bytes, "kv_bytes_at_8192": kv_bytes,
                       "effective_GB_per_s": round((weight_bytes + kv_bytes) * tok_s / 1e9, 1),

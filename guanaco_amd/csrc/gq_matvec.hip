@@ -1485,9 +1485,10 @@ int launch_dm(const MvArgs &a, hipStream_t s) {
     const int rc = launch_reg<DT, MODE>(a, total, s);
     if (rc <= 0) return rc;
   }
-  /* auto: the wave-private ring for gate/up (measured fastest there), the
-   * split-K kernel for everything else */
-  if (g_use_lds == 2 || g_use_lds == 3 || (g_use_lds == 4 && MODE == MV_SWIGLU)) {
+  /* auto: the split-K kernel for every op (the wave-private ring is selected
+   * explicitly; it measured 5% slower than split-K for gate/up in the 8B
+   * decode step) */
+  if (g_use_lds == 2 || g_use_lds == 3) {
     const int rc = launch_w<DT, MODE>(a, total, s);
     if (rc <= 0) return rc;
   }
