@@ -84,14 +84,15 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *x, const
 
 /* Embedding row of `token` (engine.c:214-283): F32 copy, Q8_0 q*scale,
  * Q4_K (d*sc)*q - dmin*m with separate roundings.  With tokens != NULL,
- * workgroup b writes the row of tokens[b] to out + b * hidden. */
+ * row blockIdx.y holds tokens[blockIdx.y] (out + blockIdx.y * hidden);
+ * blockIdx.x covers 256-element slices of the row. */
 __global__ __launch_bounds__(kThreads) void embed_kernel(int dtype, const uint8_t *table, int hidden,
                                                         const int *token_dev, int token, const int *tokens,
                                                         float *out) {
 #pragma clang fp contract(off)
-  const int tok = tokens ? tokens[blockIdx.x] : token_dev ? *token_dev : token;
-  out += (size_t)blockIdx.x * hidden;
-  for (int e = threadIdx.x; e < hidden; e += kThreads) {
+  const int tok = tokens ? tokens[blockIdx.y] : token_dev ? *token_dev : token;
+  out += (size_t)blockIdx.y * hidden;
+  for (int e = blockIdx.x * kThreads + threadIdx.x; e < hidden; e += gridDim.x * kThreads) {
     float v;
     if (dtype == GQ_F32) {
       v = ((const float *)table)[(size_t)tok * hidden + e];
@@ -141,7 +142,7 @@ __device__ __forceinline__ void block_argmax(float &v, int &i) {
   for (int w = 1; w < kThreads / GQ_WAVE; w++) better(v, i, sv[w], si[w]);
 }
 
-constexpr int kArgmaxPerBlock = 4096;
+constexpr int kArgmaxPerBlock = 1024; /* 126 workgroups for a 128256-entry vocabulary */
 
 __global__ __launch_bounds__(kThreads) void argmax_stage1(const float *x, int n, float *scratch) {
   const int base = blockIdx.x * kArgmaxPerBlock;
@@ -242,16 +243,16 @@ int gq_launch_rmsnorm_rows(const float *x, const float *w, float *out, int dim, 
 int gq_launch_embed(int dtype, const void *table, int hidden, const int *token_dev, int token,
                     float *out, hipStream_t s) {
   if (dtype != GQ_F32 && dtype != GQ_Q8_0 && dtype != GQ_Q4_K) return -1;
-  hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(kThreads), 0, s, dtype, (const uint8_t *)table,
-                     hidden, token_dev, token, (const int *)nullptr, out);
+  hipLaunchKernelGGL(embed_kernel, dim3((hidden + kThreads - 1) / kThreads), dim3(kThreads), 0, s, dtype,
+                     (const uint8_t *)table, hidden, token_dev, token, (const int *)nullptr, out);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
 int gq_launch_embed_rows(int dtype, const void *table, int hidden, const int *tokens_dev, int n, float *out,
                          hipStream_t s) {
   if ((dtype != GQ_F32 && dtype != GQ_Q8_0 && dtype != GQ_Q4_K) || !tokens_dev || n <= 0) return -1;
-  hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(kThreads), 0, s, dtype, (const uint8_t *)table, hidden,
-                     (const int *)nullptr, 0, tokens_dev, out);
+  hipLaunchKernelGGL(embed_kernel, dim3((hidden + kThreads - 1) / kThreads, n), dim3(kThreads), 0, s, dtype,
+                     (const uint8_t *)table, hidden, (const int *)nullptr, 0, tokens_dev, out);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
