@@ -44,8 +44,13 @@ typedef __bf16 gq_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float gq_f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kPThreads = 256;
-constexpr int kBM = 64, kBN = 128, kBK = 64;
-constexpr int kXBytes = kBM * kBK * 2; /* X bytes per step */
+constexpr int kBN = 128, kBK = 64;
+/* TT 32-token MFMA tiles per wave (the token tile is 32 TT); X bytes per
+ * step of one K-split */
+template <int TT>
+constexpr int x_bytes() {
+  return 32 * TT * kBK * 2;
+}
 
 typedef float gq_f2 __attribute__((ext_vector_type(2)));
 typedef __bf16 gq_bf2 __attribute__((ext_vector_type(2)));
@@ -221,117 +226,139 @@ struct PW<GQ_Q6_K> {
 /* KS = 1 or 2 K-splits per workgroup: with KS = 2, eight waves, the second
  * four running the upper half of K for the same tile; their sums are added
  * through LDS at the end.  Two waves per SIMD hide each other's LDS, DMA and
- * MFMA latencies. */
-template <int DT, int KS>
+ * MFMA latencies.  TT = 2 or 4 token tiles per wave: each dequantized B
+ * operand feeds TT MFMAs. */
+template <int DT, int KS, int TT>
 constexpr int stage_bytes() {
-  return KS * kXBytes + 4 * KS * PW<DT>::kWaveLds;
+  return KS * x_bytes<TT>() + 4 * KS * PW<DT>::kWaveLds;
 }
 
-/* Steps in the LDS ring: as deep as LDS and the 6-bit vmcnt allow (each
- * wave keeps (ring - 2) steps of DMA instructions in flight while it waits) */
-template <int DT, int KS>
+/* Steps in the LDS ring: as deep as LDS (160 KB) and the 6-bit vmcnt allow
+ * (each wave keeps (ring - 2) steps of DMA instructions in flight while it
+ * waits), at least 3 (the pipeline reads two slots) */
+template <int DT, int KS, int TT>
 constexpr int ring() {
-  return KS == 1 ? 4 : (DT == GQ_Q4_K ? 4 : 3);
+  return std::min(4, (160 * 1024) / stage_bytes<DT, KS, TT>());
 }
-template <int DT, int KS>
+template <int DT, int KS, int TT>
 constexpr int ring_bytes() {
-  return ring<DT, KS>() * stage_bytes<DT, KS>();
+  return ring<DT, KS, TT>() * stage_bytes<DT, KS, TT>();
 }
-static_assert(ring<GQ_Q4_K, 2>() >= 3 && ring<GQ_Q6_K, 2>() >= 3, "the pipeline reads two slots");
-static_assert((4 - 2) * (2 + PW<GQ_Q4_K>::kDma) < 64 && (4 - 2) * (2 + PW<GQ_Q6_K>::kDma) < 64, "vmcnt range");
-static_assert(ring_bytes<GQ_Q4_K, 2>() <= 160 * 1024 && ring_bytes<GQ_Q6_K, 2>() <= 160 * 1024, "LDS");
+template <int DT, int KS, int TT>
+constexpr bool fits() {
+  return ring<DT, KS, TT>() >= 3 && (ring<DT, KS, TT>() - 2) * (TT + PW<DT>::kDma) < 64;
+}
+static_assert(fits<GQ_Q4_K, 1, 2>() && fits<GQ_Q4_K, 2, 2>() && fits<GQ_Q6_K, 1, 2>() && fits<GQ_Q6_K, 2, 2>() &&
+                  fits<GQ_Q4_K, 1, 4>() && fits<GQ_Q4_K, 2, 4>(),
+              "ring shapes");
 
-/* One tile: tokens t0 .. t0+63 against this wave's 32 rows starting at w,
- * K-split kh of KS.  acc[i] holds tokens t0 + 32 i + (D layout rows) for
- * row (lane & 31). */
-template <int DT, int KS>
+/* One tile: tokens t0 .. t0 + 32 TT - 1 against this wave's 32 rows starting
+ * at w, K-split kh of KS.  acc[i] holds tokens t0 + 32 i + (D layout rows)
+ * for row (lane & 31). */
+template <int DT, int KS, int TT>
 __device__ __forceinline__ void tile_loop(const PgArgs &a, const uint8_t *w, uint32_t rowbytes, int t0,
-                                          GQ_LDS uint8_t *smem, gq_f32x16 acc[2]) {
-  constexpr int SB = stage_bytes<DT, KS>();
-  constexpr int NPS = 2 + PW<DT>::kDma; /* DMA instructions per wave and step */
-  constexpr int kRing = ring<DT, KS>();
+                                          GQ_LDS uint8_t *smem, gq_f32x16 (&acc)[TT]) {
+  constexpr int SB = stage_bytes<DT, KS, TT>();
+  constexpr int XB = x_bytes<TT>();
+  constexpr int NPS = TT + PW<DT>::kDma; /* DMA instructions per wave and step */
+  constexpr int kRing = ring<DT, KS, TT>();
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kh = wave >> 2, rw = wave & 3;
   const int ns = a.K / kBK / KS, s0 = kh * ns; /* this split's steps: s0 .. s0 + ns - 1 */
   typename PW<DT>::Plan pl;
   PW<DT>::plan(pl, lane, rowbytes);
   const uint32_t sbase = (uint32_t)(uintptr_t)smem;
-  const uint32_t xreg = (uint32_t)(kh * kXBytes), wreg = (uint32_t)(KS * kXBytes + wave * PW<DT>::kWaveLds);
-  /* X DMA: instruction j of wave rw covers tokens 8 (2 rw + j) + lane / 8;
+  const uint32_t xreg = (uint32_t)(kh * XB), wreg = (uint32_t)(KS * XB + wave * PW<DT>::kWaveLds);
+  /* X DMA: instruction j of wave rw covers tokens 8 (TT rw + j) + lane / 8;
    * lane position q = lane % 8 of the token's LDS row fetches octet
    * q ^ ((token / 2) % 8) */
-  const __bf16 *xsrc[2];
+  const __bf16 *xsrc[TT];
 #pragma unroll
-  for (int j = 0; j < 2; j++) {
-    const int tl = 8 * (2 * rw + j) + (lane >> 3), q = lane & 7;
+  for (int j = 0; j < TT; j++) {
+    const int tl = 8 * (TT * rw + j) + (lane >> 3), q = lane & 7;
     const int oct = q ^ ((tl >> 1) & 7);
     xsrc[j] = a.x + (size_t)min(t0 + tl, a.T - 1) * a.K + 8 * oct;
   }
   auto issue = [&](int st) {
     const uint32_t slot = sbase + (uint32_t)((st % kRing) * SB);
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+    for (int j = 0; j < TT; j++)
       dma16(xsrc[j] + (s0 + st) * kBK,
-            __builtin_amdgcn_readfirstlane(slot + xreg + 1024u * (uint32_t)(2 * rw + j)));
+            __builtin_amdgcn_readfirstlane(slot + xreg + 1024u * (uint32_t)(TT * rw + j)));
     PW<DT>::issue(pl, w, s0 + st, slot + wreg);
   };
   for (int st = 0; st < kRing - 1 && st < ns; st++) issue(st);
-  acc[0] = gq_f32x16{};
-  acc[1] = gq_f32x16{};
+#pragma unroll
+  for (int i = 0; i < TT; i++) acc[i] = gq_f32x16{};
   const int h = lane >> 5, i32 = lane & 31;
   /* Software pipeline: iteration s runs the MFMAs of step s with B operands
    * dequantized in iteration s - 1 while it dequantizes step s + 1, so the
    * VALU work overlaps the matrix core.  A wave's copies of a step have
    * landed once only the copies of later steps remain in flight; the
    * barrier extends that to every wave's copies and frees the slot read in
-   * iteration s - 1 for step s + kRing - 1. */
+   * iteration s - 1 for step s + kRing - 1.  With TT = 2 the A operands of
+   * step s + 1 are read during step s too; with TT = 4 (twice the A
+   * registers) they are read at the top of their own step. */
   /* A operand addresses within a slot: token tl = 32 i + lane % 32, octet
    * 2 kk + lane / 32, swizzled */
-  uint32_t aoff[4][2];
+  uint32_t aoff[4][TT];
 #pragma unroll
   for (int kk = 0; kk < 4; kk++)
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < TT; i++) {
       const int tl = 32 * i + i32, q = (2 * kk + h) ^ ((tl >> 1) & 7);
       aoff[kk][i] = xreg + (uint32_t)((tl * 8 + q) * 16);
     }
   auto wslot = [&](int st) { return smem + (st % kRing) * SB + wreg; };
-  gq_bf16x8 b[4], av[4][2];
+  gq_bf16x8 b[4], av[4][TT];
   typename PW<DT>::Raw raw;
   wait_groups<NPS, kRing - 2>(ns - 1);
   __syncthreads();
   PW<DT>::read(raw, wslot(0), lane, s0);
+  if (TT == 2) {
 #pragma unroll
-  for (int kk = 0; kk < 4; kk++)
+    for (int kk = 0; kk < 4; kk++)
 #pragma unroll
-    for (int i = 0; i < 2; i++) av[kk][i] = lld<gq_bf16x8>(smem, aoff[kk][i]);
+      for (int i = 0; i < TT; i++) av[kk][i] = lld<gq_bf16x8>(smem, aoff[kk][i]);
+  }
   PW<DT>::dequant(raw, s0, b);
   for (int s = 0; s < ns; s++) {
     if (s + 1 < ns) wait_groups<NPS, kRing - 3>(ns - 2 - s);
     __syncthreads();
     if (s + kRing - 1 < ns) issue(s + kRing - 1);
-    /* LDS reads for step s + 1 first, so their latency hides behind the
-     * MFMAs of step s */
-    gq_bf16x8 an[4][2];
-    const bool more = s + 1 < ns;
-    if (more) {
-      const GQ_LDS uint8_t *xn = smem + ((s + 1) % kRing) * SB;
-      PW<DT>::read(raw, wslot(s + 1), lane, s0 + s + 1);
+    const GQ_LDS uint8_t *xc = smem + (s % kRing) * SB;
+    if (TT == 4) {
 #pragma unroll
       for (int kk = 0; kk < 4; kk++)
 #pragma unroll
-        for (int i = 0; i < 2; i++) an[kk][i] = lld<gq_bf16x8>(xn, aoff[kk][i]);
+        for (int i = 0; i < TT; i++) av[kk][i] = lld<gq_bf16x8>(xc, aoff[kk][i]);
+    }
+    /* LDS reads for step s + 1 first, so their latency hides behind the
+     * MFMAs of step s */
+    gq_bf16x8 an[4][TT == 2 ? 2 : 1];
+    const bool more = s + 1 < ns;
+    if (more) {
+      PW<DT>::read(raw, wslot(s + 1), lane, s0 + s + 1);
+      if (TT == 2) {
+        const GQ_LDS uint8_t *xn = smem + ((s + 1) % kRing) * SB;
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+          for (int i = 0; i < 2; i++) an[kk][i] = lld<gq_bf16x8>(xn, aoff[kk][i]);
+      }
     }
 #pragma unroll
     for (int kk = 0; kk < 4; kk++)
 #pragma unroll
-      for (int i = 0; i < 2; i++) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[kk][i], b[kk], acc[i], 0, 0, 0);
+      for (int i = 0; i < TT; i++) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[kk][i], b[kk], acc[i], 0, 0, 0);
     if (more) {
       PW<DT>::dequant(raw, s0 + s + 1, b);
+      if (TT == 2) {
 #pragma unroll
-      for (int kk = 0; kk < 4; kk++)
+        for (int kk = 0; kk < 4; kk++)
 #pragma unroll
-        for (int i = 0; i < 2; i++) av[kk][i] = an[kk][i];
+          for (int i = 0; i < 2; i++) av[kk][i] = an[kk][i];
+      }
     }
   }
 }
@@ -341,14 +368,14 @@ __device__ __forceinline__ int tile_token(int i, int e, int lane) {
 }
 
 /* Grid: x = row tiles over the segments (kBN rows each; MV_SWIGLU: 64 gate
- * rows with the same 64 up rows), y = token tiles; 256 KS threads. */
-template <int MODE, int KS>
+ * rows with the same 64 up rows), y = token tiles of 32 TT; 256 KS threads. */
+template <int MODE, int KS, int TT>
 __global__ __launch_bounds__(kPThreads * KS) void pgemm_kernel(PgArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t pg_smem[];
   GQ_LDS uint8_t *smem = (GQ_LDS uint8_t *)pg_smem;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kh = wave >> 2, rw = wave & 3;
-  const int t0 = blockIdx.y * kBM;
+  const int t0 = blockIdx.y * 32 * TT;
   int sg = 0, tb = blockIdx.x;
   if (MODE != MV_SWIGLU)
     while (sg + 1 < a.nseg && tb >= a.seg[sg].rows / kBN) tb -= a.seg[sg].rows / kBN, sg++;
@@ -359,33 +386,38 @@ __global__ __launch_bounds__(kPThreads * KS) void pgemm_kernel(PgArgs a) {
   const int dt = a.seg[sg].dtype;
   const uint32_t rowbytes = (uint32_t)(a.K / 256) * (dt == GQ_Q4_K ? 144u : 210u);
   const uint8_t *w = S.w + (size_t)r0 * rowbytes;
-  gq_f32x16 acc[2];
-  if (dt == GQ_Q4_K)
-    tile_loop<GQ_Q4_K, KS>(a, w, rowbytes, t0, smem, acc);
-  else
-    tile_loop<GQ_Q6_K, KS>(a, w, rowbytes, t0, smem, acc);
+  gq_f32x16 acc[TT];
+  if constexpr (fits<GQ_Q6_K, KS, TT>()) {
+    if (dt == GQ_Q4_K)
+      tile_loop<GQ_Q4_K, KS, TT>(a, w, rowbytes, t0, smem, acc);
+    else
+      tile_loop<GQ_Q6_K, KS, TT>(a, w, rowbytes, t0, smem, acc);
+  } else { /* the launcher sends Q6_K to shapes that fit */
+    tile_loop<GQ_Q4_K, KS, TT>(a, w, rowbytes, t0, smem, acc);
+  }
+  constexpr int XS = 4 * TT * 16 * 64 * 4; /* bytes of one K-half's tiles */
   GQ_LDS float *xk = (GQ_LDS float *)smem;
   if (KS == 2) { /* add the upper K half (waves 4..7) into waves 0..3, in a fixed order */
     __syncthreads(); /* every wave is done reading the ring */
     if (kh == 1) {
 #pragma unroll
-      for (int i = 0; i < 2; i++)
+      for (int i = 0; i < TT; i++)
 #pragma unroll
-        for (int e = 0; e < 16; e++) xk[((rw * 2 + i) * 16 + e) * 64 + lane] = acc[i][e];
+        for (int e = 0; e < 16; e++) xk[((rw * TT + i) * 16 + e) * 64 + lane] = acc[i][e];
     }
     __syncthreads();
     if (kh == 0) {
 #pragma unroll
-      for (int i = 0; i < 2; i++)
+      for (int i = 0; i < TT; i++)
 #pragma unroll
-        for (int e = 0; e < 16; e++) acc[i][e] += xk[((rw * 2 + i) * 16 + e) * 64 + lane];
+        for (int e = 0; e < 16; e++) acc[i][e] += xk[((rw * TT + i) * 16 + e) * 64 + lane];
     }
   }
   const int n = r0 + (lane & 31);
   if (MODE != MV_SWIGLU) {
     if (kh == 0) {
 #pragma unroll
-      for (int i = 0; i < 2; i++)
+      for (int i = 0; i < TT; i++)
 #pragma unroll
         for (int e = 0; e < 16; e++) {
           const int t = t0 + tile_token(i, e, lane);
@@ -403,21 +435,21 @@ __global__ __launch_bounds__(kPThreads * KS) void pgemm_kernel(PgArgs a) {
    * 1) through LDS; act = (g * sigmoid(g)) * u as silu_inplace then
    * elemwise_mul (kernels_cpu.c:312-389), rounded to bf16 */
   __syncthreads(); /* the ring (and the K-half exchange) are free */
-  GQ_LDS float *xch = (GQ_LDS float *)(smem + (KS == 2 ? 4 * 2 * 16 * 64 * 4 : 0));
+  GQ_LDS float *xch = (GQ_LDS float *)(smem + (KS == 2 ? XS : 0));
   if (kh == 0 && rw >= 2) {
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < TT; i++)
 #pragma unroll
-      for (int e = 0; e < 16; e++) xch[(((rw - 2) * 2 + i) * 16 + e) * 64 + lane] = acc[i][e];
+      for (int e = 0; e < 16; e++) xch[(((rw - 2) * TT + i) * 16 + e) * 64 + lane] = acc[i][e];
   }
   __syncthreads();
   if (kh == 0 && rw < 2) {
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < TT; i++)
 #pragma unroll
       for (int e = 0; e < 16; e++) {
         const int t = t0 + tile_token(i, e, lane);
-        const float g = acc[i][e], u = xch[((rw * 2 + i) * 16 + e) * 64 + lane];
+        const float g = acc[i][e], u = xch[((rw * TT + i) * 16 + e) * 64 + lane];
         const float sig = 1.0f / (1.0f + expf(0.0f - g));
         const __bf16 v = (__bf16)((g * sig) * u);
         if (t < a.T) gst<unsigned short>(a.act + (size_t)t * S.rows + n, __builtin_bit_cast(unsigned short, v));
@@ -430,48 +462,62 @@ __global__ void to_bf16_kernel(const float *x, __bf16 *y, size_t n) {
   if (i < n) y[i] = (__bf16)x[i];
 }
 
-/* K-splits per workgroup: 2 when the grid has at most one workgroup per
- * CU (a second wave per SIMD then comes from the split), 1 when it has
- * more (two workgroups per CU already give two waves per SIMD);
- * GQ_PG_KS=1 or 2 overrides, for timing */
-int pg_ks(int wgs) {
-  static const int forced = [] {
-    const char *e = getenv("GQ_PG_KS");
-    return e ? atoi(e) : 0;
-  }();
+/* Launch shape: token tiles of 128 (TT = 4: each dequantized weight feeds
+ * four MFMAs) for Q4_K-only launches whose grid still gives every CU a
+ * workgroup (gate/up at 512 tokens), else of 64; then 2 K-splits when the
+ * grid has at most one workgroup per CU (a second wave per SIMD comes from
+ * the split), 1 when it has more.  GQ_PG_TT and GQ_PG_KS override (for
+ * timing). */
+int env_int(const char *name) {
+  const char *e = getenv(name);
+  return e ? atoi(e) : 0;
+}
+
+int n_cus() {
   static const int cus = [] {
     int dev = 0, n = 0;
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev))
       return 256;
     return n > 0 ? n : 256;
   }();
-  if (forced == 1 || forced == 2) return forced;
-  return wgs <= cus ? 2 : 1;
+  return cus;
 }
 
-template <int MODE, int KS>
-int launch_ks(const PgArgs &a, int row_tiles, size_t lds, hipStream_t s) {
+template <int MODE, int KS, int TT>
+int launch_shape(const PgArgs &a, int row_tiles, size_t lds, hipStream_t s) {
   static bool attr_done = false;
   if (!attr_done) {
-    (void)hipFuncSetAttribute((const void *)pgemm_kernel<MODE, KS>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    (void)hipFuncSetAttribute((const void *)pgemm_kernel<MODE, KS, TT>, hipFuncAttributeMaxDynamicSharedMemorySize,
                               160 * 1024);
     attr_done = true;
   }
-  hipLaunchKernelGGL((pgemm_kernel<MODE, KS>), dim3(row_tiles, (a.T + kBM - 1) / kBM), dim3(kPThreads * KS), lds, s,
-                     a);
+  hipLaunchKernelGGL((pgemm_kernel<MODE, KS, TT>), dim3(row_tiles, (a.T + 32 * TT - 1) / (32 * TT)),
+                     dim3(kPThreads * KS), lds, s, a);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
 template <int MODE>
 int launch_mode(const PgArgs &a, int row_tiles, hipStream_t s) {
+  static const int force_tt = env_int("GQ_PG_TT"), force_ks = env_int("GQ_PG_KS");
   bool q4 = false, q6 = false;
   for (int i = 0; i < a.nseg; i++) q4 |= a.seg[i].dtype == GQ_Q4_K, q6 |= a.seg[i].dtype == GQ_Q6_K;
-  if (pg_ks(row_tiles * ((a.T + kBM - 1) / kBM)) == 2 && (a.K / kBK) % 2 == 0) {
-    const size_t lds = std::max(q6 ? ring_bytes<GQ_Q6_K, 2>() : 0, q4 ? ring_bytes<GQ_Q4_K, 2>() : 0);
-    return launch_ks<MODE, 2>(a, row_tiles, lds, s);
+  const int tt = q6                                ? 2
+                 : force_tt == 2 || force_tt == 4 ? force_tt
+                 : row_tiles * ((a.T + 127) / 128) >= n_cus() ? 4
+                                                              : 2;
+  const int wgs = row_tiles * ((a.T + 32 * tt - 1) / (32 * tt));
+  int ks = force_ks == 1 || force_ks == 2 ? force_ks : wgs <= n_cus() ? 2 : 1;
+  if ((a.K / kBK) % 2) ks = 1;
+  if (tt == 4) {
+    const size_t lds = ks == 2 ? ring_bytes<GQ_Q4_K, 2, 4>() : ring_bytes<GQ_Q4_K, 1, 4>();
+    return ks == 2 ? launch_shape<MODE, 2, 4>(a, row_tiles, lds, s) : launch_shape<MODE, 1, 4>(a, row_tiles, lds, s);
   }
-  const size_t lds = std::max(q6 ? ring_bytes<GQ_Q6_K, 1>() : 0, q4 ? ring_bytes<GQ_Q4_K, 1>() : 0);
-  return launch_ks<MODE, 1>(a, row_tiles, lds, s);
+  if (ks == 2) {
+    const size_t lds = std::max(q6 ? ring_bytes<GQ_Q6_K, 2, 2>() : 0, q4 ? ring_bytes<GQ_Q4_K, 2, 2>() : 0);
+    return launch_shape<MODE, 2, 2>(a, row_tiles, lds, s);
+  }
+  const size_t lds = std::max(q6 ? ring_bytes<GQ_Q6_K, 1, 2>() : 0, q4 ? ring_bytes<GQ_Q4_K, 1, 2>() : 0);
+  return launch_shape<MODE, 1, 2>(a, row_tiles, lds, s);
 }
 
 } // namespace
@@ -491,11 +537,13 @@ int gq_launch_pgemm(int mode, const PgArgs &a, hipStream_t s) {
       tiles += g.rows / kBN;
     }
   }
-  /* the K-half exchange (32 KB) and the SwiGLU exchange (16 KB) reuse the
-   * ring, which is larger */
-  static_assert(ring_bytes<GQ_Q4_K, 1>() >= 2 * 2 * 16 * 64 * 4 && ring_bytes<GQ_Q6_K, 1>() >= 2 * 2 * 16 * 64 * 4,
+  /* the K-half exchange (4 TT tiles) and the SwiGLU exchange (2 TT tiles)
+   * reuse the ring, which is larger */
+  static_assert(ring_bytes<GQ_Q4_K, 1, 2>() >= 2 * 2 * 16 * 64 * 4 && ring_bytes<GQ_Q6_K, 1, 2>() >= 2 * 2 * 16 * 64 * 4 &&
+                    ring_bytes<GQ_Q4_K, 1, 4>() >= 2 * 4 * 16 * 64 * 4,
                 "exchange fits the ring");
-  static_assert(ring_bytes<GQ_Q4_K, 2>() >= 6 * 2 * 16 * 64 * 4 && ring_bytes<GQ_Q6_K, 2>() >= 6 * 2 * 16 * 64 * 4,
+  static_assert(ring_bytes<GQ_Q4_K, 2, 2>() >= 6 * 2 * 16 * 64 * 4 && ring_bytes<GQ_Q6_K, 2, 2>() >= 6 * 2 * 16 * 64 * 4 &&
+                    ring_bytes<GQ_Q4_K, 2, 4>() >= 6 * 4 * 16 * 64 * 4,
                 "exchanges fit the ring");
   if (mode == MV_SWIGLU) {
     if (a.nseg != 2 || !a.act) return -1;

@@ -244,6 +244,24 @@ def test_prefill_model_vs_oracle(ctx, orc, pre, T, ms):
     print(f"prefill T={T} pre={pre}: logits rel {rel_l2(lg, lc):.2e}, device {ms_dev:.3f} ms")
 
 
+def test_prefill_token_by_token_fallback(ctx, orc):
+    """A model whose Q6_K projections have cols % 512 != 0 (hidden 768) is
+    not taken by the GEMM: the prefill runs the decode step per token, so
+    it matches the decode path (and the oracle) to the decode tolerance."""
+    import guanaco_amd.hip as H
+    from oracle import HostModel
+    spec = S.ModelSpec("tiny-fallback", n_layers=2, hidden=768, ff=1536, n_heads=12, n_kv_heads=3, vocab=1000,
+                       layer_dtypes=S._q6k_on_even)
+    hm = HostModel(orc, spec, 64)
+    dm = H.DeviceModel(ctx, spec, 64)
+    toks = np.random.default_rng(3).integers(0, spec.vocab, 20).astype(np.int32)
+    nxt, lg, _, _ = dm.prefill(toks, 0)
+    kv = hm.new_kv()
+    for t in range(len(toks)):
+        t_cpu, lc, _ = hm.forward(kv, int(toks[t]), t)
+    assert rel_l2(lg, lc) < 1e-3 and nxt == t_cpu
+
+
 def test_prefill_model_rejects_bad_input(ctx):
     import guanaco_amd.hip as H
     dm = H.DeviceModel(ctx, S.TINY_TEST, 64)
