@@ -307,15 +307,19 @@ typedef __bf16 gq_bf2a __attribute__((ext_vector_type(2)));
  *                 4 j + i), B = V rows; output tile d holds dims ND c + d,
  *                 so a lane reads ND consecutive floats of each V row and
  *                 holds ND consecutive output dims of rows 4 j + i.
- * Same mathematics as the reference (engine.c:476-501: scores * 1/sqrt(hd),
- * -inf past the query position, softmax, P V) in fp32 throughout; only the
- * summation order differs. */
+ * Two waves per workgroup take alternate key blocks and combine their
+ * (max, sum, O) through LDS at the end, so the longest causal rows finish in
+ * half the time.  Same mathematics as the reference (engine.c:476-501:
+ * scores * 1/sqrt(hd), -inf past the query position, softmax, P V) in fp32
+ * throughout; only the summation order differs. */
 template <int HD, int G>
-__global__ __launch_bounds__(64) void flash_prefill_kernel(AttnArgs a) {
+__global__ __launch_bounds__(128) void flash_prefill_kernel(AttnArgs a) {
   constexpr int TPT = 16 / G; /* tokens per tile */
   constexpr int NS = HD / 4;  /* QK^T MFMA steps */
   constexpr int ND = HD / 16; /* output tiles over the head dimension */
-  const int lane = threadIdx.x, c = lane & 15, j = lane >> 4;
+  __shared__ float xm[64], xl[64], xo[ND * 4][64];
+  const int lane = threadIdx.x & 63, c = lane & 15, j = lane >> 4;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   /* heavy (late) tiles first */
   const int tile = gridDim.x - 1 - blockIdx.x, g = blockIdx.y;
   const int t0 = tile * TPT;
@@ -379,12 +383,15 @@ __global__ __launch_bounds__(64) void flash_prefill_kernel(AttnArgs a) {
     float mb = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
     mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
     mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
-    const float mn = fmaxf(m, mb); /* finite: key 0 is visible to every row */
-    const float alpha = __expf(m - mn);
+    /* a wave's rows may not see any key of its first blocks (the second
+     * wave starts at block 1): keep m = -inf and weigh those blocks 0 */
+    const float mn = fmaxf(m, mb);
+    const float ms = mn == -INFINITY ? 0.f : mn;
+    const float alpha = __expf(m - ms);
     float p[4], lb = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      p[i] = __expf(sv[i] - mn);
+      p[i] = __expf(sv[i] - ms);
       lb += p[i];
     }
     lb += __shfl_xor(lb, 16, 64);
@@ -403,15 +410,38 @@ __global__ __launch_bounds__(64) void flash_prefill_kernel(AttnArgs a) {
 #pragma unroll
       for (int d = 0; d < ND; d++) o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[i], vq[i][d], o[d], 0, 0, 0);
   };
-  /* two register buffers, block b + 1 loading while block b computes */
+  /* wave wv takes blocks wv, wv + 2, ...; two register buffers, the next
+   * block of the wave loading while the current one computes */
   float k2[NS], v2[4][ND];
-  load(0, kv, vv);
-  for (int b = 0; b < nblk; b += 2) {
-    if (b + 1 < nblk) load(16 * (b + 1), k2, v2);
+  if (wv < nblk) load(16 * wv, kv, vv);
+  for (int b = wv; b < nblk; b += 4) {
+    if (b + 2 < nblk) load(16 * (b + 2), k2, v2);
     step(16 * b, kv, vv);
-    if (b + 1 >= nblk) break;
-    if (b + 2 < nblk) load(16 * (b + 2), kv, vv);
-    step(16 * (b + 1), k2, v2);
+    if (b + 2 >= nblk) break;
+    if (b + 4 < nblk) load(16 * (b + 4), kv, vv);
+    step(16 * (b + 2), k2, v2);
+  }
+  /* combine: wave 1 hands (m, l, O) to wave 0 (wave 0 holds block 0, so its
+   * m is finite; wave 1's is -inf when it had no block and then weighs 0) */
+  if (wv == 1) {
+    xm[lane] = m, xl[lane] = l;
+#pragma unroll
+    for (int d = 0; d < ND; d++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) xo[4 * d + i][lane] = o[d][i];
+  }
+  __syncthreads();
+  if (wv == 1) return;
+  {
+    const float m1 = xm[lane], mt = fmaxf(m, m1);
+    const float s0 = __expf(m - mt), s1 = __expf(m1 - mt);
+    l = l * s0 + xl[lane] * s1;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float a0 = __shfl(s0, 4 * j + i, 64), a1 = __shfl(s1, 4 * j + i, 64);
+#pragma unroll
+      for (int d = 0; d < ND; d++) o[d][i] = o[d][i] * a0 + xo[4 * d + i][lane] * a1;
+    }
   }
   /* out[row] = O[row] / l[row]; row 4 j + i -> token t0 + row / G, head
    * g G + row % G */
@@ -440,7 +470,7 @@ __global__ __launch_bounds__(64) void flash_prefill_kernel(AttnArgs a) {
 
 template <int HD, int G>
 int launch_flash(const AttnArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL((flash_prefill_kernel<HD, G>), dim3((a.ntok + 16 / G - 1) / (16 / G), a.n_kv), dim3(64), 0, s,
+  hipLaunchKernelGGL((flash_prefill_kernel<HD, G>), dim3((a.ntok + 16 / G - 1) / (16 / G), a.n_kv), dim3(128), 0, s,
                      a);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
