@@ -419,6 +419,22 @@ extern "C" int gq_hip_kv_sync(gq_ctx *c, int layer, int pos, int T, const float 
   return 0;
 }
 
+extern "C" int gq_hip_kv_fetch(gq_ctx *c, int layer, int pos, int T, float *h_k, float *h_v, int head_stride,
+                               int max_seq) {
+  if (!c || !c->kslab || !h_k || !h_v || T <= 0) return fail(c, -1, "kv_fetch: bad argument");
+  if (layer < 0 || layer >= c->kv_layers || max_seq != c->kv_max_seq)
+    return fail(c, -1, "kv_fetch: layer/max_seq mismatch");
+  if (pos < 0 || pos + T > c->kv_max_seq) return fail(c, -5, "kv_fetch: rows outside the cache");
+  const size_t hd = c->kv_hd, w = sizeof(float) * hd * T;
+  const size_t spitch = sizeof(float) * hd * c->kv_max_seq, dpitch = sizeof(float) * head_stride;
+  HIPCHK(c, hipMemcpy2DAsync(h_k + pos * hd, dpitch, gq_hip_kv_k(c, layer) + pos * hd, spitch, w, c->kv_heads,
+                             hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipMemcpy2DAsync(h_v + pos * hd, dpitch, gq_hip_kv_v(c, layer) + pos * hd, spitch, w, c->kv_heads,
+                             hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return 0;
+}
+
 extern "C" int gq_hip_kv_prefill_synth(gq_ctx *c, uint64_t seed_k, uint64_t seed_v, int n_pos) {
   if (!c || !c->kslab) return fail(c, -1, "kv_prefill_synth: no cache");
   if (n_pos < 0 || n_pos > c->kv_max_seq) return fail(c, -5, "kv_prefill_synth: n_pos");

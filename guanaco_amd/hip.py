@@ -54,6 +54,7 @@ def _load():
         "gq_hip_kv_write_layer": (C.c_int, [_vp, C.c_int, _fp, _fp]),
         "gq_hip_kv_sync": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _fp, _fp, C.c_int, C.c_int]),
         "gq_hip_kv_prefill_synth": (C.c_int, [_vp, C.c_uint64, C.c_uint64, C.c_int]),
+        "gq_hip_kv_fetch": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _fp, _fp, C.c_int, C.c_int]),
         "gq_hip_lctx_save": (C.c_int, [_vp, C.c_char_p, C.c_int, C.POINTER(C.c_int32), C.c_int]),
         "gq_hip_lctx_load": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_int),
                                        C.POINTER(C.POINTER(C.c_int32)), C.POINTER(C.c_int)]),

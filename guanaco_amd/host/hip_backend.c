@@ -20,6 +20,7 @@
 #include "hip_backend.h"
 
 #include <stdlib.h>
+#include <string.h>
 
 #include "../../include/gq_hip.h"
 
@@ -118,4 +119,99 @@ int hip_backend_upload(Backend *b, Tensor *t) {
 int hip_backend_finish(Backend *b) {
   gq_ctx *ctx = hip_backend_context(b);
   return ctx ? gq_hip_sync(ctx) : -1;
+}
+
+/* The reference's KV accessors (kv_cache.c:189-205), as engine.c:307-309
+ * declares them. */
+extern float *kv_cache_raw_k(KVCache *kv, int layer);
+extern float *kv_cache_raw_v(KVCache *kv, int layer);
+extern int kv_cache_head_stride(KVCache *kv);
+
+static int gq_dtype(DataType d) {
+  switch (d) {
+  case DTYPE_F32: return GQ_F32;
+  case DTYPE_Q8_0: return GQ_Q8_0;
+  case DTYPE_Q4_K: return GQ_Q4_K;
+  case DTYPE_Q6_K: return GQ_Q6_K;
+  default: return -1;
+  }
+}
+
+/* A device copy of a tensor: its own d_data when the loader uploaded it,
+ * else a fresh upload owned by the device context. */
+static const void *device_copy(gq_ctx *ctx, const Tensor *t) {
+  if (!t || !t->data) return NULL;
+  if (t->device_residency == 1 && t->d_data) return t->d_data;
+  size_t bytes = t->byte_size;
+  if (!bytes && t->dtype == DTYPE_F32) {
+    bytes = sizeof(float);
+    for (int i = 0; i < t->ndim; i++) bytes *= (size_t)t->shape[i];
+  }
+  return bytes ? gq_hip_upload_weight(ctx, t->data, bytes) : NULL;
+}
+
+static int weight_of(gq_ctx *ctx, const Tensor *t, gq_weight *w) {
+  if (!t || t->ndim != 2 || gq_dtype(t->dtype) < 0) return -1;
+  w->data = device_copy(ctx, t);
+  w->dtype = gq_dtype(t->dtype);
+  w->rows = t->shape[0];
+  w->cols = t->shape[1];
+  return w->data ? 0 : -1;
+}
+
+int hip_backend_bind_model(Backend *b, ModelWeights *mw, KVCache *kv) {
+  gq_ctx *ctx = hip_backend_context(b);
+  if (!ctx || !mw || !mw->layers || !kv) return -1;
+  const ModelConfig *c = &mw->config;
+  if (gq_hip_kv_init(ctx, c->n_layers, c->n_kv_heads, c->head_dim, c->max_seq_len, 500000.0f)) return -1;
+  gq_layer *layers = (gq_layer *)calloc((size_t)c->n_layers, sizeof(gq_layer));
+  if (!layers) return -1;
+  int rc = 0;
+  for (int l = 0; l < c->n_layers && !rc; l++) {
+    const LayerWeights *L = &mw->layers[l];
+    gq_layer *g = &layers[l];
+    rc = weight_of(ctx, L->wq, &g->wq) || weight_of(ctx, L->wk, &g->wk) || weight_of(ctx, L->wv, &g->wv) ||
+         weight_of(ctx, L->wo, &g->wo) || weight_of(ctx, L->w_gate, &g->w_gate) ||
+         weight_of(ctx, L->w_up, &g->w_up) || weight_of(ctx, L->w_down, &g->w_down);
+    if (!rc) {
+      g->rms_att = (const float *)device_copy(ctx, L->rms_att);
+      g->rms_ffn = (const float *)device_copy(ctx, L->rms_ffn);
+      rc = g->rms_att && g->rms_ffn ? 0 : -1;
+    }
+  }
+  gq_model m;
+  memset(&m, 0, sizeof m);
+  if (!rc) {
+    m.n_layers = c->n_layers, m.hidden = c->hidden_dim, m.ff = c->ff_dim;
+    m.n_heads = c->n_heads, m.n_kv_heads = c->n_kv_heads, m.head_dim = c->head_dim, m.vocab = c->vocab_size;
+    m.rope_theta = 500000.0f; /* kernels_cpu.c:408 */
+    m.rms_eps = 1e-6f;        /* engine.c:359, 524, 582 */
+    m.layers = layers;
+    m.rms_final = (const float *)device_copy(ctx, mw->rms_final);
+    rc = weight_of(ctx, mw->embedding, &m.embed) || weight_of(ctx, mw->lm_head, &m.lm_head) || !m.rms_final;
+  }
+  if (!rc) rc = gq_hip_model_bind(ctx, &m);
+  free(layers); /* gq_hip_model_bind copies the layer array */
+  if (rc) return -1;
+  /* the host cache may already hold a prefix (a restored session) */
+  const int hs = kv_cache_head_stride(kv);
+  for (int l = 0; l < c->n_layers; l++)
+    if (gq_hip_kv_sync(ctx, l, 0, c->max_seq_len, kv_cache_raw_k(kv, l), kv_cache_raw_v(kv, l), hs,
+                       c->max_seq_len))
+      return -1;
+  return 0;
+}
+
+int hip_backend_prefill(const Backend *backend, ModelWeights *model, KVCache *kv, Scratch *scr,
+                        const int *token_ids, int n_tokens, int pos) {
+  (void)scr;
+  gq_ctx *ctx = hip_backend_context(backend);
+  if (!ctx || !model || !kv || !token_ids || n_tokens <= 0) return -1;
+  if (gq_hip_prefill(ctx, (const int32_t *)token_ids, n_tokens, pos, NULL, NULL, NULL) < 0) return -1;
+  const int hs = kv_cache_head_stride(kv);
+  for (int l = 0; l < model->config.n_layers; l++)
+    if (gq_hip_kv_fetch(ctx, l, pos, n_tokens, kv_cache_raw_k(kv, l), kv_cache_raw_v(kv, l), hs,
+                        model->config.max_seq_len))
+      return -1;
+  return 0;
 }

@@ -22,4 +22,22 @@ int hip_backend_upload(Backend *b, Tensor *t);
 /* Wait for queued device work (cuda_finish_layer). */
 int hip_backend_finish(Backend *b);
 
+/* Bind the whole model to the device after the loader's uploads
+ * (loader.c:701-728): every layer's seven projections must be
+ * device-resident or are uploaded here, the F32 norm weights, the embedding
+ * and the LM head get device copies, the device KV cache is sized from
+ * ModelConfig (θ 500000, kernels_cpu.c:408) and takes the host cache's
+ * contents (a restored session's prefix).  After this, gq_hip_forward_token,
+ * gq_hip_decode_loop and gq_hip_prefill run on hip_backend_context(b).
+ * Returns 0, or -1 (the model stays on its CPU path). */
+int hip_backend_bind_model(Backend *b, ModelWeights *mw, KVCache *kv);
+
+/* The gpu_prefill slot (gpu_prefill.h:13-20, same signature): the prompt
+ * through every layer on the device (gq_hip_prefill), then the new K/V rows
+ * copied into the host cache so the engine's CPU decode (or kv_cache_save)
+ * sees them.  Needs hip_backend_bind_model first.  Returns 0, or non-zero
+ * for the CPU forward() fallback. */
+int hip_backend_prefill(const Backend *backend, ModelWeights *model, KVCache *kv, Scratch *scr,
+                        const int *token_ids, int n_tokens, int pos);
+
 #endif

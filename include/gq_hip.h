@@ -106,6 +106,12 @@ int gq_hip_kv_write_layer(gq_ctx *ctx, int layer, const float *k, const float *v
  * cuda_sync_kv_cache (cuda_layer_kernels.cu:585-603). */
 int gq_hip_kv_sync(gq_ctx *ctx, int layer, int pos, int T, const float *h_k, const float *h_v,
                    int head_stride, int max_seq);
+/* The reverse of gq_hip_kv_sync: rows pos .. pos+T-1 of every KV head of
+ * `layer` from the device cache into the host slabs (head_stride floats
+ * between heads, kv_cache_head_stride), so a CPU layer or a host-side
+ * kv_cache_save after a device prefill sees them.  Synchronous. */
+int gq_hip_kv_fetch(gq_ctx *ctx, int layer, int pos, int T, float *h_k, float *h_v, int head_stride,
+                    int max_seq);
 /* Seeded N(0,1) history at positions 0..n_pos-1 (gq_synth.h gq_kv_index). */
 int gq_hip_kv_prefill_synth(gq_ctx *ctx, uint64_t seed_k, uint64_t seed_v, int n_pos);
 

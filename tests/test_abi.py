@@ -35,3 +35,18 @@ def test_no_device_means_null_context():
     assert not H.lib.gq_hip_create(0)
     with pytest.raises(H.HipError):
         H.Context(0)
+
+
+def test_host_backend_exports(ref):
+    """libgq_host.so (the HIP backend behind the reference's KernelVTable)
+    exports the reference's factory (backend.h:41-52) and every hook
+    guanaco_amd/host/include/hip_backend.h declares.  Its CPU backend is
+    resolved from the reference's objects, so libref.so is loaded first."""
+    src = open(os.path.join(ROOT, "guanaco_amd", "host", "include", "hip_backend.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    names = sorted(set(re.findall(r"\b(hip_backend_\w+)\s*\(", src)))
+    assert {"hip_backend_upload", "hip_backend_bind_model", "hip_backend_prefill"} <= set(names)
+    lib = ctypes.CDLL(os.path.join(ROOT, "guanaco_amd", "libgq_host.so"))
+    missing = [n for n in names + ["backend_create", "backend_kernels", "backend_destroy"]
+               if not hasattr(lib, n)]
+    assert not missing, missing

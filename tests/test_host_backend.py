@@ -114,3 +114,48 @@ def test_reference_engine_through_hip_vtable(host, ref, orc):
     cpu.close()
     gpu.close()
     host.backend_destroy(b)
+
+
+@pytest.mark.gpu
+def test_bind_model_and_gpu_prefill_slot(host, ref, orc):
+    """The whole model bound from the reference's own ModelWeights
+    (hip_backend_bind_model) and the gpu_prefill slot (hip_backend_prefill,
+    gpu_prefill.h:13-20): the prompt runs on the device, its K/V rows land
+    in the reference's host cache, and the reference's CPU forward() decodes
+    the next token from that cache.  Against the all-CPU reference (its
+    T-token forward() for the prompt, engine.c:559-595): the bf16 prefill
+    tolerance (3e-2 relative L2) and the same greedy token; the device
+    decode through the bound model likewise."""
+    import guanaco_amd.hip as H
+    from oracle import RModelWeights
+    spec, ms, n = S.TINY_TEST, 64, 20
+    b = host.backend_create(C.byref(RBackendConfig(BACKEND_HIP, 4, 0, spec.n_layers)))
+    assert b, "HIP backend unavailable on a GPU box"
+    host.hip_backend_bind_model.argtypes = [C.c_void_p, C.POINTER(RModelWeights), C.c_void_p]
+    host.hip_backend_prefill.argtypes = [C.c_void_p, C.POINTER(RModelWeights), C.c_void_p, C.c_void_p,
+                                         C.POINTER(C.c_int), C.c_int, C.c_int]
+    hm = HostModel(orc, spec, ms)
+    cpu, gpu = RefModel(ref, hm), RefModel(ref, hm)
+    for l in range(spec.n_layers):
+        for f in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down"):
+            assert host.hip_backend_upload(b, getattr(gpu.mw.layers[l], f)) == 0
+    assert host.hip_backend_bind_model(b, C.byref(gpu.mw), gpu.kv) == 0
+    toks = np.random.default_rng(7).integers(0, spec.vocab, n).astype(np.int32)
+    prompt = (C.c_int * (n - 1))(*[int(t) for t in toks[:-1]])
+    ref.lib.forward(C.byref(cpu.mw), cpu.kv, cpu.scratch, prompt, n - 1, 0, ref.vtable)
+    t_cpu, lc = cpu.forward(int(toks[-1]), n - 1)
+    assert host.hip_backend_prefill(b, C.byref(gpu.mw), gpu.kv, gpu.scratch, prompt, n - 1, 0) == 0
+    for l in range(spec.n_layers):
+        for w in ("k", "v"):
+            hk = gpu.slab(w, l).reshape(spec.n_kv_heads, ms, spec.head_dim)[:, :n - 1]
+            ck = cpu.slab(w, l).reshape(spec.n_kv_heads, ms, spec.head_dim)[:, :n - 1]
+            assert rel_l2(hk, ck) < 3e-2, (l, w)
+    t_g, lg = gpu.forward(int(toks[-1]), n - 1)  # the reference's CPU decode on the filled cache
+    assert rel_l2(lg, lc) < 3e-2 and t_g == t_cpu
+    ctx = host.hip_backend_context(b)
+    ld = np.empty(spec.vocab, np.float32)
+    t_d = H.lib.gq_hip_forward_token(ctx, int(toks[-1]), n - 1, ld.ctypes.data_as(C.POINTER(C.c_float)), None)
+    assert rel_l2(ld, lc) < 3e-2 and t_d == t_cpu
+    cpu.close()
+    gpu.close()
+    host.backend_destroy(b)
