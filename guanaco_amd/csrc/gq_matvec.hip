@@ -35,6 +35,20 @@
 namespace {
 
 constexpr int kThreads = 256;
+
+/* x staged in LDS by the split-K kernel has its 16-byte units permuted
+ * inside each 256-byte row: unit u sits at (u & ~15) | ((u ^ (u >> 4)) & 15),
+ * an involution.  The traits' lanes read the same unit of different rows at
+ * once (a 4-lane Q4_K wave reads 64 units 256 bytes apart), which the
+ * permutation spreads over all the banks. */
+__device__ __forceinline__ uint32_t xswz(uint32_t byteoff) {
+  const uint32_t u = byteoff >> 4;
+  return ((u & ~15u) | ((u ^ (u >> 4)) & 15u)) << 4;
+}
+template <bool SW>
+__device__ __forceinline__ float4 lldx(const GQ_LDS uint8_t *p, uint32_t off) {
+  return lld<float4>(p, SW ? xswz(off) : off);
+}
 constexpr int kWaves = kThreads / GQ_WAVE;
 
 template <int DT>
@@ -58,13 +72,14 @@ struct Tr<GQ_Q4_K> {
   /* x slice of block b from x staged in LDS (byte base xs), times the
    * RMSNorm weight staged at nw when given; *ss (when given) accumulates the
    * raw x^2 of the slice */
+  template <bool SW = false>
   __device__ static void load_x(X &x, const GQ_LDS uint8_t *xs, const GQ_LDS uint8_t *nw, int b, int p,
                                 float *ss = nullptr) {
     const uint32_t a = 4u * (256 * b + 64 * p), c = a + 128;
     float sl = 0.f, sh = 0.f;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
-      float4 u = lld<float4>(xs, a + 16 * k), v = lld<float4>(xs, c + 16 * k);
+      float4 u = lldx<SW>(xs, a + 16 * k), v = lldx<SW>(xs, c + 16 * k);
       if (ss) {
         float q = *ss;
         q = __builtin_fmaf(u.x, u.x, q), q = __builtin_fmaf(u.y, u.y, q), q = __builtin_fmaf(u.z, u.z, q);
@@ -73,7 +88,7 @@ struct Tr<GQ_Q4_K> {
         *ss = q;
       }
       if (nw) {
-        const float4 wu = lld<float4>(nw, a + 16 * k), wv = lld<float4>(nw, c + 16 * k);
+        const float4 wu = lldx<SW>(nw, a + 16 * k), wv = lldx<SW>(nw, c + 16 * k);
         u = make_float4(wu.x * u.x, wu.y * u.y, wu.z * u.z, wu.w * u.w);
         v = make_float4(wv.x * v.x, wv.y * v.y, wv.z * v.z, wv.w * v.w);
       }
@@ -166,13 +181,28 @@ struct TrQ4K8 {
     x.slo = sl;
     x.shi = sh;
   }
+  template <bool SW = false>
   __device__ static void load_x(X &x, const GQ_LDS uint8_t *xs, const GQ_LDS uint8_t *nw, int b, int p,
                                 float *ss = nullptr) {
-    (void)nw, (void)ss;
     const uint32_t a = 4u * (256 * b + 64 * (p >> 1) + 16 * (p & 1));
     float4 u[4], v[4];
 #pragma unroll
-    for (int k = 0; k < 4; k++) u[k] = lld<float4>(xs, a + 16 * k), v[k] = lld<float4>(xs, a + 128 + 16 * k);
+    for (int k = 0; k < 4; k++) {
+      u[k] = lldx<SW>(xs, a + 16 * k), v[k] = lldx<SW>(xs, a + 128 + 16 * k);
+      if (ss) {
+        float q = *ss;
+        q = __builtin_fmaf(u[k].x, u[k].x, q), q = __builtin_fmaf(u[k].y, u[k].y, q);
+        q = __builtin_fmaf(u[k].z, u[k].z, q), q = __builtin_fmaf(u[k].w, u[k].w, q);
+        q = __builtin_fmaf(v[k].x, v[k].x, q), q = __builtin_fmaf(v[k].y, v[k].y, q);
+        q = __builtin_fmaf(v[k].z, v[k].z, q), q = __builtin_fmaf(v[k].w, v[k].w, q);
+        *ss = q;
+      }
+      if (nw) {
+        const float4 wu = lldx<SW>(nw, a + 16 * k), wv = lldx<SW>(nw, a + 128 + 16 * k);
+        u[k] = make_float4(wu.x * u[k].x, wu.y * u[k].y, wu.z * u[k].z, wu.w * u[k].w);
+        v[k] = make_float4(wv.x * v[k].x, wv.y * v[k].y, wv.z * v[k].z, wv.w * v[k].w);
+      }
+    }
     fill(x, u, v);
   }
   /* x slice straight from global memory, times the RMSNorm weight when given;
@@ -271,12 +301,13 @@ struct Tr<GQ_Q6_K> {
     float v[4][8];
     float s[4];
   };
+  template <bool SW = false>
   __device__ static void load_x(X &x, const GQ_LDS uint8_t *xs, const GQ_LDS uint8_t *nw, int b, int p,
                                 float *ss = nullptr) {
     const uint32_t base = 4u * (256 * b + 128 * (p >> 2) + 8 * (p & 3));
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-      float4 u = lld<float4>(xs, base + 128 * r), v = lld<float4>(xs, base + 128 * r + 16);
+      float4 u = lldx<SW>(xs, base + 128 * r), v = lldx<SW>(xs, base + 128 * r + 16);
       if (ss) {
         float q = *ss;
         q = __builtin_fmaf(u.x, u.x, q), q = __builtin_fmaf(u.y, u.y, q), q = __builtin_fmaf(u.z, u.z, q);
@@ -285,7 +316,7 @@ struct Tr<GQ_Q6_K> {
         *ss = q;
       }
       if (nw) {
-        const float4 wu = lld<float4>(nw, base + 128 * r), wv = lld<float4>(nw, base + 128 * r + 16);
+        const float4 wu = lldx<SW>(nw, base + 128 * r), wv = lldx<SW>(nw, base + 128 * r + 16);
         u = make_float4(wu.x * u.x, wu.y * u.y, wu.z * u.z, wu.w * u.w);
         v = make_float4(wv.x * v.x, wv.y * v.y, wv.z * v.z, wv.w * v.w);
       }
@@ -372,13 +403,14 @@ struct Tr<GQ_Q8_0> {
   struct X {
     float v[32];
   };
+  template <bool SW = false>
   __device__ static void load_x(X &x, const GQ_LDS uint8_t *xs, const GQ_LDS uint8_t *nw, int b, int p,
                                 float *ss = nullptr) {
     (void)p;
     const uint32_t base = 128u * b;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
-      float4 u = lld<float4>(xs, base + 16 * k);
+      float4 u = lldx<SW>(xs, base + 16 * k);
       if (ss) {
         float q = *ss;
         q = __builtin_fmaf(u.x, u.x, q), q = __builtin_fmaf(u.y, u.y, q);
@@ -386,7 +418,7 @@ struct Tr<GQ_Q8_0> {
         *ss = q;
       }
       if (nw) {
-        const float4 w = lld<float4>(nw, base + 16 * k);
+        const float4 w = lldx<SW>(nw, base + 16 * k);
         u = make_float4(w.x * u.x, w.y * u.y, w.z * u.z, w.w * u.w);
       }
       x.v[4 * k] = u.x, x.v[4 * k + 1] = u.y, x.v[4 * k + 2] = u.z, x.v[4 * k + 3] = u.w;
@@ -447,6 +479,19 @@ struct TrSplit {
 template <>
 struct TrSplit<GQ_Q4_K> {
   using type = TrQ4K8;
+};
+
+/* The split-K LDS kernel's traits: with x staged in LDS (XL) a Q4_K lane
+ * takes a 64-weight chunk of each block (4 lanes per block: half the
+ * per-weight cost of decoding scales and reducing, but x slices twice as
+ * long, which only pays when they come from LDS); otherwise as TrSplit. */
+template <int DT, bool XL>
+struct TrL {
+  using type = typename TrSplit<DT>::type;
+};
+template <>
+struct TrL<GQ_Q4_K, true> {
+  using type = Tr<GQ_Q4_K>;
 };
 
 /* Stage x (optionally RMS-normalised: w * (x * 1/sqrt(mean(x^2) + eps)),
@@ -681,6 +726,7 @@ struct MvPlan {
   int rowbytes;
   int stride;       /* LDS bytes per stage buffer */
   int total;        /* output rows */
+  int xl;           /* LDS offset of x staged by DMA (slot 2 onwards), XL kernels */
 };
 
 /* Wave `wave`'s 1 KB copy instructions for nbytes (a multiple of 16) split
@@ -688,6 +734,19 @@ struct MvPlan {
 __device__ __forceinline__ int copy_count(int nbytes, int wave, int nwv = kWaves) {
   const int ng = (nbytes / 16 + 63) / 64;
   return wave < ng ? (ng - wave + nwv - 1) / nwv : 0;
+}
+
+/* [src, src + nbytes) into LDS at dst in the xswz order (nbytes a multiple
+ * of 256): the lane that writes position q reads source unit xswz(q). */
+__device__ __forceinline__ void copy_range_sw(const uint8_t *src, int nbytes, GQ_LDS uint8_t *dst, int wave,
+                                              int lane) {
+  const int nchunk = nbytes / 16, ng = (nchunk + 63) / 64;
+  const uint32_t base = (uint32_t)(uintptr_t)dst;
+  for (int g = wave; g < ng; g += kWaves) {
+    const int c = g * 64 + lane;
+    const uint32_t d = __builtin_amdgcn_readfirstlane(base + (uint32_t)g * 1024u);
+    if (c < nchunk) dma16(src + xswz(16u * (uint32_t)c), d);
+  }
 }
 
 /* Rows [src, src + nbytes) into LDS at dst by 16-byte DMA (dma16), 1 KB per
@@ -770,9 +829,9 @@ __device__ __forceinline__ void store_row(const MvArgs &a, int s, int lr, float 
     gst<float>(sg.y + ((size_t)h * a.rope.max_seq + pos) * hd + d, v);
 }
 
-template <int DT, int MODE, int TPW, int RW>
+template <int DT, int MODE, int TPW, int RW, bool XL>
 __global__ __launch_bounds__(kThreads) void mvl_kernel(MvArgs a, MvPlan pl) {
-  using T = typename TrSplit<DT>::type;
+  using T = typename TrL<DT, XL>::type;
   constexpr int NS = kNS;
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   GQ_LDS uint8_t *lds = (GQ_LDS uint8_t *)smem;
@@ -790,25 +849,61 @@ __global__ __launch_bounds__(kThreads) void mvl_kernel(MvArgs a, MvPlan pl) {
   const bool active = team < pl.nteam;
   const int mygroups = (int)blockIdx.x < pl.ngroups ? (pl.ngroups - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
 
-  /* everything the loop needs from global memory besides the weights is
-   * loaded and consumed first: x slices (and the RMSNorm sum of squares from
-   * team 0), the position and the RoPE table row */
   typename T::X xs[TPW];
   float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < TPW; i++) {
-    const int b = (wj + i * pl.ts) * BPT + bt;
-    float s2 = 0.f;
-    T::load_xg(xs[i], a.x, a.norm_w, min(b, nb - 1), part, s2);
-    if (b < nb && (wj + i * pl.ts) < pl.ntile) ss += s2;
-  }
   int pos = 0;
-  if (MODE == MV_STORE && a.rope.cs) {
-    pos = a.rope.pos_dev ? gld<int>(a.rope.pos_dev) : a.rope.pos;
-    const int half = a.rope.head_dim >> 1;
-    if (pos >= 0 && pos < a.rope.max_seq)
-      for (int i = threadIdx.x; i < half && i < 256; i += kThreads)
-        scs[i] = gld<float2>(a.rope.cs + (size_t)pos * half + i);
+  int nxt; /* this wave's DMA instructions of stage k+1 */
+  if constexpr (XL) {
+    /* x, the norm weight and the RoPE row go to LDS by DMA (x at slot 2,
+     * which stage 2 overwrites only after the barrier below), followed by
+     * the first two stages: x's latency overlaps theirs */
+    const int xb = a.cols * 4;
+    copy_range_sw((const uint8_t *)a.x, xb, lds + pl.xl, wave, lane);
+    if (a.norm_w) copy_range_sw((const uint8_t *)a.norm_w, xb, lds + pl.xl + xb, wave, lane);
+    if (MODE == MV_STORE && a.rope.cs) {
+      pos = a.rope.pos_dev ? gq_sld<int>(a.rope.pos_dev) : a.rope.pos;
+      const int hd = a.rope.head_dim; /* floats in one table row (hd/2 pairs) */
+      if (wave == 0 && pos >= 0 && pos < a.rope.max_seq) {
+        const float *crow = (const float *)(a.rope.cs + (size_t)pos * (hd >> 1));
+        const uint32_t base = (uint32_t)(uintptr_t)(GQ_LDS float2 *)scs;
+        for (int o = 0; o < hd; o += 64)
+          if (lane < hd - o) dma4(crow + o + lane, __builtin_amdgcn_readfirstlane(base + 4u * o));
+      }
+    }
+    const int c0 = issue_stage<MODE>(a, pl, blockIdx.x, lds, lres, wave, lane); /* mygroups >= 1 */
+    nxt = mygroups > 1 ? issue_stage<MODE>(a, pl, blockIdx.x + gridDim.x, lds + pl.stride, lres + 32, wave, lane)
+                       : 0;
+    /* VMEM loads complete in issue order: with only the two stages' copies
+     * outstanding, this wave's part of x has landed; the barrier extends
+     * that to every wave's */
+    wait_vmcnt(c0 + nxt);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < TPW; i++) {
+      const int b = (wj + i * pl.ts) * BPT + bt;
+      float s2 = 0.f;
+      T::template load_x<true>(xs[i], lds + pl.xl, a.norm_w ? lds + pl.xl + xb : nullptr, min(b, nb - 1), part,
+                               &s2);
+      if (b < nb && (wj + i * pl.ts) < pl.ntile) ss += s2;
+    }
+  } else {
+    /* everything the loop needs from global memory besides the weights is
+     * loaded and consumed first: x slices (and the RMSNorm sum of squares
+     * from team 0), the position and the RoPE table row */
+#pragma unroll
+    for (int i = 0; i < TPW; i++) {
+      const int b = (wj + i * pl.ts) * BPT + bt;
+      float s2 = 0.f;
+      T::load_xg(xs[i], a.x, a.norm_w, min(b, nb - 1), part, s2);
+      if (b < nb && (wj + i * pl.ts) < pl.ntile) ss += s2;
+    }
+    if (MODE == MV_STORE && a.rope.cs) {
+      pos = a.rope.pos_dev ? gld<int>(a.rope.pos_dev) : a.rope.pos;
+      const int half = a.rope.head_dim >> 1;
+      if (pos >= 0 && pos < a.rope.max_seq)
+        for (int i = threadIdx.x; i < half && i < 256; i += kThreads)
+          scs[i] = gld<float2>(a.rope.cs + (size_t)pos * half + i);
+    }
   }
   float rscale = 1.f;
   if (a.norm_w) { /* 1/sqrt(mean(x^2) + eps) (kernels_cpu.c:242-253) */
@@ -819,18 +914,21 @@ __global__ __launch_bounds__(kThreads) void mvl_kernel(MvArgs a, MvPlan pl) {
     tot = tot / (float)a.cols;
     tot = tot + a.eps;
     rscale = 1.0f / sqrtf(tot);
+  } else if (XL) {
+    __syncthreads(); /* every wave has read x before stage 2 overwrites it */
   }
-  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); /* those loads are done */
+  if constexpr (!XL) {
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); /* those loads are done */
+    (void)issue_stage<MODE>(a, pl, blockIdx.x, lds, lres, wave, lane); /* mygroups >= 1 */
+    nxt = mygroups > 1 ? issue_stage<MODE>(a, pl, blockIdx.x + gridDim.x, lds + pl.stride, lres + 32, wave, lane)
+                       : 0;
+  }
 
   static_assert(NS == 3 && NS + 1 <= kRing, "the loop below keeps two stages in flight");
   /* Stage k's copies are issued at iteration k-2, before that iteration's
    * wait, into the slot stage k-3 used (computed at iteration k-3, before
    * the barrier closing it); at iteration k they are waited for, computed
    * and at iteration k+1 its rows are finished (reduced, stored). */
-  (void)issue_stage<MODE>(a, pl, blockIdx.x, lds, lres, wave, lane); /* mygroups >= 1 */
-  int nxt = mygroups > 1 ? issue_stage<MODE>(a, pl, blockIdx.x + gridDim.x, lds + pl.stride, lres + 32, wave, lane)
-                         : 0; /* this wave's copies of stage k+1 */
-
   const int hrows = MODE == MV_SWIGLU ? pl.rs / 2 : pl.rs;
   const int rpw = pl.rs / pl.nteam; /* rows per team and stage, a multiple of RW */
   int slot = 0;                     /* k % NS */
@@ -1296,21 +1394,22 @@ int launch_r(const MvArgs &a, int total, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
-/* Plan and launch the LDS-streamed kernel; returns 1 when the shape does not
- * fit it (rows not a multiple of 16 bytes, more than 8 column tiles, or
- * segments that a stage would straddle) so the caller uses mv_kernel. */
-template <int DT, int MODE>
-int launch_lds(const MvArgs &a, int total, hipStream_t s) {
-  using T = typename TrSplit<DT>::type;
+/* Plan the LDS-streamed kernel for traits T: stage rows, teams, LDS bytes
+ * and workgroups per CU; false when the shape does not fit it (rows not a
+ * multiple of 16 bytes, more than 8 column tiles, or segments that a stage
+ * would straddle).  With xl, x (and the norm weight) are staged from slot 2
+ * onwards, growing the LDS past the three slots when they need more. */
+template <typename T, int MODE>
+bool plan_lds(const MvArgs &a, int total, bool xl, MvPlan &pl, size_t &lds, int &per_cu, int &tpw, int &rw) {
   const int nb = a.cols / T::QK;
   const int rowbytes = nb * T::BB;
-  if (rowbytes % 16) return 1;
-  if (a.rope.cs && a.rope.head_dim > 512) return 1; /* the kernel's RoPE row holds 256 pairs */
+  if (rowbytes % 16) return false;
+  if (a.rope.cs && a.rope.head_dim > 512) return false; /* the kernel's RoPE row holds 256 pairs */
   constexpr int BPT = GQ_WAVE / T::LPB;
   const int ntile = (nb + BPT - 1) / BPT;
-  const int tpw = ntile <= kWaves ? 1 : 2;
+  tpw = ntile <= kWaves ? 1 : 2;
   const int ts = (ntile + tpw - 1) / tpw;
-  if (ts > kWaves) return 1;
+  if (ts > kWaves) return false;
   const int nteam = kWaves / ts;
   int rs = min(32, g_stage_cap / rowbytes);
   rs -= rs % (2 * nteam);
@@ -1322,32 +1421,61 @@ int launch_lds(const MvArgs &a, int total, hipStream_t s) {
       else
         i++;
     }
-  if (rs < 2 * nteam || rs < 2) return 1;
-  MvPlan pl;
+  if (rs < 2 * nteam || rs < 2) return false;
   pl.rs = rs, pl.ts = ts, pl.nteam = nteam, pl.ntile = ntile, pl.rowbytes = rowbytes, pl.total = total;
   pl.stride = (rs * rowbytes + 64 + 1023) / 1024 * 1024;
   const int per = MODE == MV_SWIGLU ? rs / 2 : rs;
   pl.ngroups = (total + per - 1) / per;
-  const size_t lds = (size_t)kNS * pl.stride;
-  if (lds > kMaxDynLds) return 1;
-  int per_cu = max(1, (int)(160 * 1024 / (lds + 8192)));
+  lds = (size_t)kNS * pl.stride;
+  pl.xl = -1;
+  if (xl) {
+    pl.xl = 2 * pl.stride;
+    lds = std::max(lds, (size_t)pl.xl + (size_t)a.cols * 4 * (a.norm_w ? 2 : 1));
+  }
+  if (lds > kMaxDynLds) return false;
+  per_cu = max(1, (int)(160 * 1024 / (lds + 8192)));
   if (g_lds_wg_per_cu > 0) per_cu = min(per_cu, g_lds_wg_per_cu);
-  const int grid = min(pl.ngroups, per_cu * g_n_cu);
   /* rows per team per stage is even (rs is a multiple of 2 nteam) */
-  const int rw = (rs / nteam) % 4 == 0 ? 4 : 2;
+  rw = (rs / nteam) % 4 == 0 ? 4 : 2;
+  return true;
+}
+
+template <int DT, int MODE, bool XL>
+int launch_lds_as(const MvArgs &a, const MvPlan &pl, size_t lds, int per_cu, int tpw, int rw, hipStream_t s) {
   static bool attr_set = false;
   if (!attr_set) {
-    const void *fs[] = {(const void *)mvl_kernel<DT, MODE, 1, 2>, (const void *)mvl_kernel<DT, MODE, 2, 2>,
-                        (const void *)mvl_kernel<DT, MODE, 1, 4>, (const void *)mvl_kernel<DT, MODE, 2, 4>};
+    const void *fs[] = {(const void *)mvl_kernel<DT, MODE, 1, 2, XL>, (const void *)mvl_kernel<DT, MODE, 2, 2, XL>,
+                        (const void *)mvl_kernel<DT, MODE, 1, 4, XL>, (const void *)mvl_kernel<DT, MODE, 2, 4, XL>};
     for (const void *f : fs) (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds);
     attr_set = true;
   }
-  const dim3 g(grid), b(kThreads);
-  if (rw == 2 && tpw == 1) hipLaunchKernelGGL((mvl_kernel<DT, MODE, 1, 2>), g, b, lds, s, a, pl);
-  if (rw == 2 && tpw == 2) hipLaunchKernelGGL((mvl_kernel<DT, MODE, 2, 2>), g, b, lds, s, a, pl);
-  if (rw == 4 && tpw == 1) hipLaunchKernelGGL((mvl_kernel<DT, MODE, 1, 4>), g, b, lds, s, a, pl);
-  if (rw == 4 && tpw == 2) hipLaunchKernelGGL((mvl_kernel<DT, MODE, 2, 4>), g, b, lds, s, a, pl);
+  const dim3 g(min(pl.ngroups, per_cu * g_n_cu)), b(kThreads);
+  if (rw == 2 && tpw == 1) hipLaunchKernelGGL((mvl_kernel<DT, MODE, 1, 2, XL>), g, b, lds, s, a, pl);
+  if (rw == 2 && tpw == 2) hipLaunchKernelGGL((mvl_kernel<DT, MODE, 2, 2, XL>), g, b, lds, s, a, pl);
+  if (rw == 4 && tpw == 1) hipLaunchKernelGGL((mvl_kernel<DT, MODE, 1, 4, XL>), g, b, lds, s, a, pl);
+  if (rw == 4 && tpw == 2) hipLaunchKernelGGL((mvl_kernel<DT, MODE, 2, 4, XL>), g, b, lds, s, a, pl);
   return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+int g_mv_xl = -1; /* x staged in LDS by the split-K kernel: -1 auto, 0 never, 1 whenever it fits */
+
+/* Plan and launch the LDS-streamed kernel; returns 1 when the shape does not
+ * fit it, so the caller uses mv_kernel.  x goes through LDS (the XL kernel)
+ * when that costs no workgroup per CU (auto: gate/up, q/k/v, o at the 8B
+ * shape measured 8-12% faster; the LM head, which would drop from three
+ * workgroups per CU to two, 13% slower), else each wave loads its x slices
+ * from global memory. */
+template <int DT, int MODE>
+int launch_lds(const MvArgs &a, int total, hipStream_t s) {
+  MvPlan pl, px;
+  size_t lds, lx;
+  int per_cu, tpw, rw, pcx, tpx, rwx;
+  const bool base = plan_lds<typename TrL<DT, false>::type, MODE>(a, total, false, pl, lds, per_cu, tpw, rw);
+  if (g_mv_xl != 0 && plan_lds<typename TrL<DT, true>::type, MODE>(a, total, true, px, lx, pcx, tpx, rwx) &&
+      (g_mv_xl == 1 || !base || pcx >= per_cu))
+    return launch_lds_as<DT, MODE, true>(a, px, lx, pcx, tpx, rwx, s);
+  if (!base) return 1;
+  return launch_lds_as<DT, MODE, false>(a, pl, lds, per_cu, tpw, rw, s);
 }
 
 int g_mw_rw = 4;   /* rows per group of the wave-private kernel */
@@ -1532,6 +1660,8 @@ void gq_matvec_set_cus(int n_cu) {
    * allows) */
   if (const char *e = getenv("GQ_MV_STAGE_BYTES")) g_stage_cap = std::min(std::max(atoi(e), 4096), 40960);
   if (const char *e = getenv("GQ_MV_LDS_WG")) g_lds_wg_per_cu = std::max(atoi(e), 0);
+  /* GQ_MV_XL: x through LDS in the split-K kernel (-1 auto, 0 never, 1 when it fits) */
+  if (const char *e = getenv("GQ_MV_XL")) g_mv_xl = std::min(std::max(atoi(e), -1), 1);
 }
 
 extern "C" int gq_hip_set_matvec_path(int path) {
