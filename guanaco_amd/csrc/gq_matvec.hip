@@ -712,7 +712,7 @@ __global__ __launch_bounds__(kThreads) void mv_kernel(MvArgs a) {
  * their LDS reads issued before the arithmetic), reduces each row over its
  * 16-lane DPP rows only, and the 4 row partials per wave meet in LDS, where
  * the epilogue adds them. */
-constexpr int kNS = 3;    /* stage buffers: deeper rings measured no faster */
+constexpr int kNS = 3;    /* stage buffers: 4-6 measured slower (one workgroup per CU) */
 constexpr int kRing = 8;  /* residual-row ring slots (>= kNS + 1) */
 constexpr int kRedW = kWaves * 4; /* row partials per row: 4 per wave */
 int g_stage_cap = 24576;  /* bytes of weights per stage buffer */
@@ -739,10 +739,10 @@ __device__ __forceinline__ int copy_count(int nbytes, int wave, int nwv = kWaves
 /* [src, src + nbytes) into LDS at dst in the xswz order (nbytes a multiple
  * of 256): the lane that writes position q reads source unit xswz(q). */
 __device__ __forceinline__ void copy_range_sw(const uint8_t *src, int nbytes, GQ_LDS uint8_t *dst, int wave,
-                                              int lane) {
+                                              int lane, int nwv = kWaves) {
   const int nchunk = nbytes / 16, ng = (nchunk + 63) / 64;
   const uint32_t base = (uint32_t)(uintptr_t)dst;
-  for (int g = wave; g < ng; g += kWaves) {
+  for (int g = wave; g < ng; g += nwv) {
     const int c = g * 64 + lane;
     const uint32_t d = __builtin_amdgcn_readfirstlane(base + (uint32_t)g * 1024u);
     if (c < nchunk) dma16(src + xswz(16u * (uint32_t)c), d);
@@ -829,10 +829,10 @@ __device__ __forceinline__ void store_row(const MvArgs &a, int s, int lr, float 
     gst<float>(sg.y + ((size_t)h * a.rope.max_seq + pos) * hd + d, v);
 }
 
-template <int DT, int MODE, int TPW, int RW, bool XL>
+template <int DT, int MODE, int TPW, int RW, bool XL, int NS>
 __global__ __launch_bounds__(kThreads) void mvl_kernel(MvArgs a, MvPlan pl) {
   using T = typename TrL<DT, XL>::type;
-  constexpr int NS = kNS;
+  static_assert(NS >= 3 && NS + 1 <= kRing, "ring of NS stage slots, NS - 1 stages in flight");
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   GQ_LDS uint8_t *lds = (GQ_LDS uint8_t *)smem;
   __shared__ __attribute__((aligned(16))) float red[2][32][kRedW];
@@ -852,11 +852,13 @@ __global__ __launch_bounds__(kThreads) void mvl_kernel(MvArgs a, MvPlan pl) {
   typename T::X xs[TPW];
   float ss = 0.f;
   int pos = 0;
-  int nxt; /* this wave's DMA instructions of stage k+1 */
+  /* this wave's DMA instructions of stages k .. k + NS - 2 at the top of
+   * iteration k */
+  int cnt[NS - 1];
   if constexpr (XL) {
-    /* x, the norm weight and the RoPE row go to LDS by DMA (x at slot 2,
-     * which stage 2 overwrites only after the barrier below), followed by
-     * the first two stages: x's latency overlaps theirs */
+    /* x, the norm weight and the RoPE row go to LDS by DMA (x at slot NS-1,
+     * which stage NS-1 overwrites only after the barrier below), followed by
+     * the first NS-1 stages: x's latency overlaps theirs */
     const int xb = a.cols * 4;
     copy_range_sw((const uint8_t *)a.x, xb, lds + pl.xl, wave, lane);
     if (a.norm_w) copy_range_sw((const uint8_t *)a.norm_w, xb, lds + pl.xl + xb, wave, lane);
@@ -870,13 +872,18 @@ __global__ __launch_bounds__(kThreads) void mvl_kernel(MvArgs a, MvPlan pl) {
           if (lane < hd - o) dma4(crow + o + lane, __builtin_amdgcn_readfirstlane(base + 4u * o));
       }
     }
-    const int c0 = issue_stage<MODE>(a, pl, blockIdx.x, lds, lres, wave, lane); /* mygroups >= 1 */
-    nxt = mygroups > 1 ? issue_stage<MODE>(a, pl, blockIdx.x + gridDim.x, lds + pl.stride, lres + 32, wave, lane)
-                       : 0;
-    /* VMEM loads complete in issue order: with only the two stages' copies
+    int sum = 0;
+#pragma unroll
+    for (int j = 0; j < NS - 1; j++) {
+      cnt[j] = j < mygroups ? issue_stage<MODE>(a, pl, blockIdx.x + j * gridDim.x, lds + j * pl.stride,
+                                                lres + j * 32, wave, lane)
+                            : 0; /* mygroups >= 1 */
+      sum += cnt[j];
+    }
+    /* VMEM loads complete in issue order: with only the stages' copies
      * outstanding, this wave's part of x has landed; the barrier extends
      * that to every wave's */
-    wait_vmcnt(c0 + nxt);
+    wait_vmcnt(sum);
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < TPW; i++) {
@@ -919,30 +926,37 @@ __global__ __launch_bounds__(kThreads) void mvl_kernel(MvArgs a, MvPlan pl) {
   }
   if constexpr (!XL) {
     __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); /* those loads are done */
-    (void)issue_stage<MODE>(a, pl, blockIdx.x, lds, lres, wave, lane); /* mygroups >= 1 */
-    nxt = mygroups > 1 ? issue_stage<MODE>(a, pl, blockIdx.x + gridDim.x, lds + pl.stride, lres + 32, wave, lane)
-                       : 0;
+#pragma unroll
+    for (int j = 0; j < NS - 1; j++)
+      cnt[j] = j < mygroups ? issue_stage<MODE>(a, pl, blockIdx.x + j * gridDim.x, lds + j * pl.stride,
+                                                lres + j * 32, wave, lane)
+                            : 0; /* mygroups >= 1 */
   }
 
-  static_assert(NS == 3 && NS + 1 <= kRing, "the loop below keeps two stages in flight");
-  /* Stage k's copies are issued at iteration k-2, before that iteration's
-   * wait, into the slot stage k-3 used (computed at iteration k-3, before
-   * the barrier closing it); at iteration k they are waited for, computed
-   * and at iteration k+1 its rows are finished (reduced, stored). */
+  /* Stage k's copies are issued at iteration k-(NS-1), before that
+   * iteration's wait, into the slot stage k-NS used (computed at iteration
+   * k-NS, before the barrier closing it); at iteration k they are waited
+   * for, computed and at iteration k+1 its rows are finished (reduced,
+   * stored). */
   const int hrows = MODE == MV_SWIGLU ? pl.rs / 2 : pl.rs;
   const int rpw = pl.rs / pl.nteam; /* rows per team and stage, a multiple of RW */
   int slot = 0;                     /* k % NS */
   for (int k = 0; k <= mygroups; k++) {
     if (k < mygroups) {
-      const int kn = k + 2, sn = slot == 0 ? 2 : slot - 1; /* kn % NS */
+      const int kn = k + NS - 1, sn = slot == 0 ? NS - 1 : slot - 1; /* kn % NS */
       const int nn = kn < mygroups ? issue_stage<MODE>(a, pl, blockIdx.x + kn * gridDim.x, lds + sn * pl.stride,
                                                        lres + (kn % kRing) * 32, wave, lane)
                                    : 0;
-      /* VMEM loads complete in issue order: with at most stages k+1 and k+2
-       * outstanding, this wave's copies of stage k have landed; the barrier
-       * extends that to every wave's */
-      wait_vmcnt(nxt + nn);
-      nxt = nn;
+      /* VMEM loads complete in issue order: with at most stages k+1 ..
+       * k+NS-1 outstanding, this wave's copies of stage k have landed; the
+       * barrier extends that to every wave's */
+      int pend = nn;
+#pragma unroll
+      for (int j = 1; j < NS - 1; j++) pend += cnt[j];
+      wait_vmcnt(pend);
+#pragma unroll
+      for (int j = 0; j < NS - 2; j++) cnt[j] = cnt[j + 1];
+      cnt[NS - 2] = nn;
     }
     __syncthreads();
     if (k > 0) { /* finish the rows of stage k-1: row t on lane t/4 of wave t%4 */
@@ -1092,8 +1106,8 @@ __global__ __launch_bounds__(kMaxWaves * GQ_WAVE) void mvw_kernel(MvArgs a, MwPl
   /* prologue: x, the norm weight and the RoPE row into LDS (the whole
    * workgroup), then this wave's first ns-1 groups, all with DMA */
   const int xb = a.cols * 4;
-  copy_range((const uint8_t *)a.x, xb, lds + pl.x_off, wave, lane, nwv);
-  if (a.norm_w) copy_range((const uint8_t *)a.norm_w, xb, lds + pl.nw_off, wave, lane, nwv);
+  copy_range_sw((const uint8_t *)a.x, xb, lds + pl.x_off, wave, lane, nwv);
+  if (a.norm_w) copy_range_sw((const uint8_t *)a.norm_w, xb, lds + pl.nw_off, wave, lane, nwv);
   int pos = 0;
   if (MODE == MV_STORE && a.rope.cs) {
     pos = a.rope.pos_dev ? gq_sld<int>(a.rope.pos_dev) : a.rope.pos;
@@ -1139,7 +1153,8 @@ __global__ __launch_bounds__(kMaxWaves * GQ_WAVE) void mvw_kernel(MvArgs a, MwPl
   typename T::X xs[TPW];
 #pragma unroll
   for (int i = 0; i < TPW; i++)
-    T::load_x(xs[i], lds + pl.x_off, a.norm_w ? lds + pl.nw_off : nullptr, min(i * BPT + bt, nb - 1), part);
+    T::template load_x<true>(xs[i], lds + pl.x_off, a.norm_w ? lds + pl.nw_off : nullptr, min(i * BPT + bt, nb - 1),
+                             part);
   __syncthreads(); /* the last slot row is free from here on */
   for (int k = npre; k < ns - 1 && k < mygroups; k++) {
     issue_group<MODE, RW>(a, pl, gw + k * W, ring + k * row, rr + 4 * k, lane);
@@ -1400,7 +1415,8 @@ int launch_r(const MvArgs &a, int total, hipStream_t s) {
  * would straddle).  With xl, x (and the norm weight) are staged from slot 2
  * onwards, growing the LDS past the three slots when they need more. */
 template <typename T, int MODE>
-bool plan_lds(const MvArgs &a, int total, bool xl, MvPlan &pl, size_t &lds, int &per_cu, int &tpw, int &rw) {
+bool plan_lds(const MvArgs &a, int total, bool xl, int ns, MvPlan &pl, size_t &lds, int &per_cu, int &tpw,
+              int &rw) {
   const int nb = a.cols / T::QK;
   const int rowbytes = nb * T::BB;
   if (rowbytes % 16) return false;
@@ -1411,25 +1427,27 @@ bool plan_lds(const MvArgs &a, int total, bool xl, MvPlan &pl, size_t &lds, int 
   const int ts = (ntile + tpw - 1) / tpw;
   if (ts > kWaves) return false;
   const int nteam = kWaves / ts;
+  /* rs: two rows per team at least, so a wave's step covers a RoPE pair */
+  const int unit = 2 * nteam;
   int rs = min(32, g_stage_cap / rowbytes);
-  rs -= rs % (2 * nteam);
+  rs -= rs % unit;
   /* with several segments a stage must not straddle two: rs divides them all */
   if (MODE != MV_SWIGLU && a.nseg > 1)
-    for (int i = 0; i < a.nseg && rs >= 2 * nteam;) {
+    for (int i = 0; i < a.nseg && rs >= unit;) {
       if (a.seg[i].rows % rs)
-        rs -= 2 * nteam, i = 0;
+        rs -= unit, i = 0;
       else
         i++;
     }
-  if (rs < 2 * nteam || rs < 2) return false;
+  if (rs < unit || rs < 2) return false;
   pl.rs = rs, pl.ts = ts, pl.nteam = nteam, pl.ntile = ntile, pl.rowbytes = rowbytes, pl.total = total;
   pl.stride = (rs * rowbytes + 64 + 1023) / 1024 * 1024;
   const int per = MODE == MV_SWIGLU ? rs / 2 : rs;
   pl.ngroups = (total + per - 1) / per;
-  lds = (size_t)kNS * pl.stride;
+  lds = (size_t)ns * pl.stride;
   pl.xl = -1;
   if (xl) {
-    pl.xl = 2 * pl.stride;
+    pl.xl = (ns - 1) * pl.stride;
     lds = std::max(lds, (size_t)pl.xl + (size_t)a.cols * 4 * (a.norm_w ? 2 : 1));
   }
   if (lds > kMaxDynLds) return false;
@@ -1440,20 +1458,21 @@ bool plan_lds(const MvArgs &a, int total, bool xl, MvPlan &pl, size_t &lds, int 
   return true;
 }
 
-template <int DT, int MODE, bool XL>
+template <int DT, int MODE, bool XL, int NS>
 int launch_lds_as(const MvArgs &a, const MvPlan &pl, size_t lds, int per_cu, int tpw, int rw, hipStream_t s) {
   static bool attr_set = false;
   if (!attr_set) {
-    const void *fs[] = {(const void *)mvl_kernel<DT, MODE, 1, 2, XL>, (const void *)mvl_kernel<DT, MODE, 2, 2, XL>,
-                        (const void *)mvl_kernel<DT, MODE, 1, 4, XL>, (const void *)mvl_kernel<DT, MODE, 2, 4, XL>};
+    const void *fs[] = {
+        (const void *)mvl_kernel<DT, MODE, 1, 2, XL, NS>, (const void *)mvl_kernel<DT, MODE, 2, 2, XL, NS>,
+        (const void *)mvl_kernel<DT, MODE, 1, 4, XL, NS>, (const void *)mvl_kernel<DT, MODE, 2, 4, XL, NS>};
     for (const void *f : fs) (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds);
     attr_set = true;
   }
   const dim3 g(min(pl.ngroups, per_cu * g_n_cu)), b(kThreads);
-  if (rw == 2 && tpw == 1) hipLaunchKernelGGL((mvl_kernel<DT, MODE, 1, 2, XL>), g, b, lds, s, a, pl);
-  if (rw == 2 && tpw == 2) hipLaunchKernelGGL((mvl_kernel<DT, MODE, 2, 2, XL>), g, b, lds, s, a, pl);
-  if (rw == 4 && tpw == 1) hipLaunchKernelGGL((mvl_kernel<DT, MODE, 1, 4, XL>), g, b, lds, s, a, pl);
-  if (rw == 4 && tpw == 2) hipLaunchKernelGGL((mvl_kernel<DT, MODE, 2, 4, XL>), g, b, lds, s, a, pl);
+  if (rw == 2 && tpw == 1) hipLaunchKernelGGL((mvl_kernel<DT, MODE, 1, 2, XL, NS>), g, b, lds, s, a, pl);
+  if (rw == 2 && tpw == 2) hipLaunchKernelGGL((mvl_kernel<DT, MODE, 2, 2, XL, NS>), g, b, lds, s, a, pl);
+  if (rw == 4 && tpw == 1) hipLaunchKernelGGL((mvl_kernel<DT, MODE, 1, 4, XL, NS>), g, b, lds, s, a, pl);
+  if (rw == 4 && tpw == 2) hipLaunchKernelGGL((mvl_kernel<DT, MODE, 2, 4, XL, NS>), g, b, lds, s, a, pl);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
@@ -1470,12 +1489,12 @@ int launch_lds(const MvArgs &a, int total, hipStream_t s) {
   MvPlan pl, px;
   size_t lds, lx;
   int per_cu, tpw, rw, pcx, tpx, rwx;
-  const bool base = plan_lds<typename TrL<DT, false>::type, MODE>(a, total, false, pl, lds, per_cu, tpw, rw);
-  if (g_mv_xl != 0 && plan_lds<typename TrL<DT, true>::type, MODE>(a, total, true, px, lx, pcx, tpx, rwx) &&
+  const bool base = plan_lds<typename TrL<DT, false>::type, MODE>(a, total, false, kNS, pl, lds, per_cu, tpw, rw);
+  if (g_mv_xl != 0 && plan_lds<typename TrL<DT, true>::type, MODE>(a, total, true, kNS, px, lx, pcx, tpx, rwx) &&
       (g_mv_xl == 1 || !base || pcx >= per_cu))
-    return launch_lds_as<DT, MODE, true>(a, px, lx, pcx, tpx, rwx, s);
+    return launch_lds_as<DT, MODE, true, kNS>(a, px, lx, pcx, tpx, rwx, s);
   if (!base) return 1;
-  return launch_lds_as<DT, MODE, false>(a, pl, lds, per_cu, tpw, rw, s);
+  return launch_lds_as<DT, MODE, false, kNS>(a, pl, lds, per_cu, tpw, rw, s);
 }
 
 int g_mw_rw = 4;   /* rows per group of the wave-private kernel */
