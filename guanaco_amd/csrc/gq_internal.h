@@ -57,6 +57,9 @@ struct MvArgs {
 };
 
 int gq_launch_matvec(int dtype, int mode, const MvArgs &a, hipStream_t s);
+/* Two MV_STORE matvecs of different dtypes (Q4_K, then Q6_K) over the same
+ * x in one launch; 1 when the pair is not supported (launch them apart). */
+int gq_launch_matvec_pair(int dt0, const MvArgs &a0, int dt1, const MvArgs &a1, hipStream_t s);
 /* workgroups the matvec launcher puts on the device at most (persistent grid) */
 void gq_matvec_set_cus(int n_cu);
 

@@ -829,16 +829,27 @@ __device__ __forceinline__ void store_row(const MvArgs &a, int s, int lr, float 
     gst<float>(sg.y + ((size_t)h * a.rope.max_seq + pos) * hd + d, v);
 }
 
+/* The split-K kernel's statically sized LDS: row partials, the RMSNorm
+ * partial sums, the residual ring and the RoPE row. */
+struct MvShared {
+  __attribute__((aligned(16))) float red[2][32][kRedW];
+  float red_ss[kWaves];
+  __attribute__((aligned(16))) float rres[kRing][32];
+  float2 scs[256];
+};
+
+/* One launch's work as workgroup `bid` of `nblk` (the whole grid, or one
+ * side of a paired launch) */
 template <int DT, int MODE, int TPW, int RW, bool XL, int NS>
-__global__ __launch_bounds__(kThreads) void mvl_kernel(MvArgs a, MvPlan pl) {
+__device__ __forceinline__ void mvl_body(const MvArgs &a, const MvPlan &pl, int bid, int nblk, MvShared &sh) {
   using T = typename TrL<DT, XL>::type;
   static_assert(NS >= 3 && NS + 1 <= kRing, "ring of NS stage slots, NS - 1 stages in flight");
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   GQ_LDS uint8_t *lds = (GQ_LDS uint8_t *)smem;
-  __shared__ __attribute__((aligned(16))) float red[2][32][kRedW];
-  __shared__ float red_ss[kWaves];
-  __shared__ __attribute__((aligned(16))) float rres[kRing][32];
-  __shared__ float2 scs[256];
+  auto &red = sh.red;
+  auto &red_ss = sh.red_ss;
+  auto &rres = sh.rres;
+  float2 *scs = sh.scs;
   GQ_LDS float *lres = (GQ_LDS float *)&rres[0][0];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); /* scalar: the DMA counts are too */
@@ -847,7 +858,7 @@ __global__ __launch_bounds__(kThreads) void mvl_kernel(MvArgs a, MvPlan pl) {
   const int part = lane % T::LPB, bt = lane / T::LPB;
   const int team = wave / pl.ts, wj = wave - team * pl.ts;
   const bool active = team < pl.nteam;
-  const int mygroups = (int)blockIdx.x < pl.ngroups ? (pl.ngroups - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+  const int mygroups = bid < pl.ngroups ? (pl.ngroups - 1 - bid) / nblk + 1 : 0;
 
   typename T::X xs[TPW];
   float ss = 0.f;
@@ -875,7 +886,7 @@ __global__ __launch_bounds__(kThreads) void mvl_kernel(MvArgs a, MvPlan pl) {
     int sum = 0;
 #pragma unroll
     for (int j = 0; j < NS - 1; j++) {
-      cnt[j] = j < mygroups ? issue_stage<MODE>(a, pl, blockIdx.x + j * gridDim.x, lds + j * pl.stride,
+      cnt[j] = j < mygroups ? issue_stage<MODE>(a, pl, bid + j * nblk, lds + j * pl.stride,
                                                 lres + j * 32, wave, lane)
                             : 0; /* mygroups >= 1 */
       sum += cnt[j];
@@ -928,7 +939,7 @@ __global__ __launch_bounds__(kThreads) void mvl_kernel(MvArgs a, MvPlan pl) {
     __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); /* those loads are done */
 #pragma unroll
     for (int j = 0; j < NS - 1; j++)
-      cnt[j] = j < mygroups ? issue_stage<MODE>(a, pl, blockIdx.x + j * gridDim.x, lds + j * pl.stride,
+      cnt[j] = j < mygroups ? issue_stage<MODE>(a, pl, bid + j * nblk, lds + j * pl.stride,
                                                 lres + j * 32, wave, lane)
                             : 0; /* mygroups >= 1 */
   }
@@ -944,7 +955,7 @@ __global__ __launch_bounds__(kThreads) void mvl_kernel(MvArgs a, MvPlan pl) {
   for (int k = 0; k <= mygroups; k++) {
     if (k < mygroups) {
       const int kn = k + NS - 1, sn = slot == 0 ? NS - 1 : slot - 1; /* kn % NS */
-      const int nn = kn < mygroups ? issue_stage<MODE>(a, pl, blockIdx.x + kn * gridDim.x, lds + sn * pl.stride,
+      const int nn = kn < mygroups ? issue_stage<MODE>(a, pl, bid + kn * nblk, lds + sn * pl.stride,
                                                        lres + (kn % kRing) * 32, wave, lane)
                                    : 0;
       /* VMEM loads complete in issue order: with at most stages k+1 ..
@@ -960,7 +971,7 @@ __global__ __launch_bounds__(kThreads) void mvl_kernel(MvArgs a, MvPlan pl) {
     }
     __syncthreads();
     if (k > 0) { /* finish the rows of stage k-1: row t on lane t/4 of wave t%4 */
-      const int r0 = (blockIdx.x + (k - 1) * gridDim.x) * hrows;
+      const int r0 = (bid + (k - 1) * nblk) * hrows;
       int s = 0, lr0 = r0;
       if (MODE != MV_SWIGLU) locate(a, r0, s, lr0);
       s = __builtin_amdgcn_readfirstlane(s);
@@ -1008,6 +1019,25 @@ __global__ __launch_bounds__(kThreads) void mvl_kernel(MvArgs a, MvPlan pl) {
     __syncthreads();
     slot = slot == NS - 1 ? 0 : slot + 1;
   }
+}
+
+template <int DT, int MODE, int TPW, int RW, bool XL, int NS>
+__global__ __launch_bounds__(kThreads) void mvl_kernel(MvArgs a, MvPlan pl) {
+  __shared__ MvShared sh;
+  mvl_body<DT, MODE, TPW, RW, XL, NS>(a, pl, (int)blockIdx.x, (int)gridDim.x, sh);
+}
+
+/* Two MV_STORE launches of different dtypes in one: workgroups [0, g0) run
+ * the first (a0, p0), the rest the second.  For the q/k/v projections of
+ * layers whose v is Q6_K and q, k are Q4_K. */
+template <int DT0, int TPW0, int RW0, bool XL0, int DT1, int TPW1, int RW1, bool XL1>
+__global__ __launch_bounds__(kThreads) void mvl_pair_kernel(MvArgs a0, MvPlan p0, MvArgs a1, MvPlan p1, int g0) {
+  __shared__ MvShared sh;
+  const int b = (int)blockIdx.x;
+  if (b < g0)
+    mvl_body<DT0, MV_STORE, TPW0, RW0, XL0, kNS>(a0, p0, b, g0, sh);
+  else
+    mvl_body<DT1, MV_STORE, TPW1, RW1, XL1, kNS>(a1, p1, b - g0, (int)gridDim.x - g0, sh);
 }
 
 /* ------------------------------------------------------------------------
@@ -1497,6 +1527,21 @@ int launch_lds(const MvArgs &a, int total, hipStream_t s) {
   return launch_lds_as<DT, MODE, false, kNS>(a, pl, lds, per_cu, tpw, rw, s);
 }
 
+/* q/k (Q4_K) and v (Q6_K) in one launch; returns 1 when the shapes do not
+ * fit the paired kernel (the caller launches them one by one) */
+template <int RW0, int RW1>
+int launch_pair_as(const MvArgs &a0, const MvPlan &p0, const MvArgs &a1, const MvPlan &p1, int g0, int g1, size_t lds,
+                   hipStream_t s) {
+  static bool attr_set = false;
+  auto f = mvl_pair_kernel<GQ_Q4_K, 1, RW0, true, GQ_Q6_K, 1, RW1, true>;
+  if (!attr_set) {
+    (void)hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLds);
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(f, dim3(g0 + g1), dim3(kThreads), lds, s, a0, p0, a1, p1, g0);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
 int g_mw_rw = 4;   /* rows per group of the wave-private kernel */
 int g_mw_waves = 0; /* waves per workgroup of the wave-private kernel (0: chosen per shape) */
 int g_mw_pre = -1;  /* groups issued before x is waited for (-1: all ns-1) */
@@ -1687,6 +1732,52 @@ extern "C" int gq_hip_set_matvec_path(int path) {
   const int prev = g_use_lds;
   if (path >= 0 && path <= 4) g_use_lds = path;
   return prev;
+}
+
+int gq_launch_matvec_pair(int dt0, const MvArgs &a0, int dt1, const MvArgs &a1, hipStream_t s) {
+  if (g_use_lds != 4 || g_mv_xl == 0 || dt0 != GQ_Q4_K || dt1 != GQ_Q6_K) return 1;
+  const MvArgs *as[2] = {&a0, &a1};
+  int totals[2];
+  for (int k = 0; k < 2; k++) {
+    const MvArgs &a = *as[k];
+    if (a.nseg < 1 || a.nseg > 3 || a.cols <= 0 || a.cols > 16384 || a.cols % 256) return 1;
+    int total = 0;
+    bool fused = false;
+    for (int i = 0; i < a.nseg; i++) {
+      if (a.seg[i].kind != SEG_PLAIN) {
+        fused = true;
+        if (!a.rope.cs || a.rope.head_dim <= 0 || (a.rope.head_dim & 1) || a.seg[i].rows % a.rope.head_dim)
+          return 1;
+      }
+      total += a.seg[i].rows;
+    }
+    if (fused)
+      for (int i = 0; i < a.nseg; i++)
+        if (a.seg[i].rows % 4) return 1;
+    if (total <= 0) return 1;
+    totals[k] = total;
+  }
+  MvPlan p0, p1;
+  size_t l0, l1;
+  int c0, c1, t0, t1, r0, r1;
+  if (!plan_lds<typename TrL<GQ_Q4_K, true>::type, MV_STORE>(a0, totals[0], true, kNS, p0, l0, c0, t0, r0) ||
+      !plan_lds<typename TrL<GQ_Q6_K, true>::type, MV_STORE>(a1, totals[1], true, kNS, p1, l1, c1, t1, r1))
+    return 1;
+  if (t0 != 1 || t1 != 1) return 1;
+  const size_t lds = std::max(l0, l1);
+  int per_cu = max(1, (int)(160 * 1024 / (lds + 8192)));
+  if (g_lds_wg_per_cu > 0) per_cu = min(per_cu, g_lds_wg_per_cu);
+  /* one resident wave of workgroups, split in proportion to the bytes */
+  const int slots = per_cu * g_n_cu;
+  const double b0 = (double)totals[0] * p0.rowbytes, b1 = (double)totals[1] * p1.rowbytes;
+  int g1 = (int)(slots * b1 / (b0 + b1) + 0.5);
+  g1 = min(max(g1, 1), p1.ngroups);
+  const int g0 = min(max(slots - g1, 1), p0.ngroups);
+  if (r0 == 2 && r1 == 2) return launch_pair_as<2, 2>(a0, p0, a1, p1, g0, g1, lds, s);
+  if (r0 == 2 && r1 == 4) return launch_pair_as<2, 4>(a0, p0, a1, p1, g0, g1, lds, s);
+  if (r0 == 4 && r1 == 2) return launch_pair_as<4, 2>(a0, p0, a1, p1, g0, g1, lds, s);
+  if (r0 == 4 && r1 == 4) return launch_pair_as<4, 4>(a0, p0, a1, p1, g0, g1, lds, s);
+  return 1;
 }
 
 int gq_launch_matvec(int dtype, int mode, const MvArgs &a, hipStream_t s) {

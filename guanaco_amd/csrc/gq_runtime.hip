@@ -667,22 +667,36 @@ static int op_qkv(gq_ctx *c, int l, int pos, const int *pos_dev, float *hidden) 
   float *Y[3] = {c->ws.qkv, gq_hip_kv_k(c, l), gq_hip_kv_v(c, l)};
   const int kind[3] = {SEG_ROPE, SEG_ROPE_KV, SEG_KV};
   bool done[3] = {false, false, false};
+  MvArgs g[3];
+  int gdt[3], ng = 0;
+  double bytes = 4.0 * m.hidden;
   for (int i = 0; i < 3; i++) {
     if (done[i]) continue;
-    MvArgs a{};
+    MvArgs &a = g[ng];
+    a = MvArgs{};
+    gdt[ng++] = W[i]->dtype;
     a.cols = m.hidden, a.x = hidden, a.norm_w = L.rms_att, a.eps = m.rms_eps;
     a.rope = MvRope{c->rope, pos_dev, pos, m.head_dim, c->kv_max_seq};
-    double bytes = 4.0 * m.hidden;
     for (int j = i; j < 3; j++)
       if (!done[j] && W[j]->dtype == W[i]->dtype) {
         a.seg[a.nseg++] = MvSeg{(const uint8_t *)W[j]->data, Y[j], nullptr, W[j]->rows, kind[j]};
         bytes += mv_bytes(*W[j], 0) - 4.0 * m.hidden;
         done[j] = true;
       }
-    const int rc = gq_launch_matvec(W[i]->dtype, MV_STORE, a, c->stream);
-    if (rc) return rc;
-    mark(c, PC_QKV, bytes);
   }
+  /* Q4_K q, k and Q6_K v (the Q4_K_M mix): one paired launch */
+  if (ng == 2) {
+    const int rc = gq_launch_matvec_pair(gdt[0], g[0], gdt[1], g[1], c->stream);
+    if (rc <= 0) {
+      if (rc == 0) mark(c, PC_QKV, bytes);
+      return rc;
+    }
+  }
+  for (int k = 0; k < ng; k++) {
+    const int rc = gq_launch_matvec(gdt[k], MV_STORE, g[k], c->stream);
+    if (rc) return rc;
+  }
+  mark(c, PC_QKV, bytes);
   return 0;
 }
 
