@@ -209,18 +209,24 @@ struct TrQ4K8 {
    * ss accumulates the raw x^2 of the slice */
   __device__ static void load_xg(X &x, const float *xg, const float *nw, int b, int p, float &ss) {
     const int base = 256 * b + 64 * (p >> 1) + 16 * (p & 1);
-    float4 u[4], v[4];
+    /* every load first (the norm weight, or x again in its place), so the
+     * slice costs one memory round trip */
+    const float *np = nw ? nw : xg;
+    float4 u[4], v[4], wu[4], wv[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       u[k] = gld<float4>(xg + base + 4 * k), v[k] = gld<float4>(xg + base + 32 + 4 * k);
+      wu[k] = gld<float4>(np + base + 4 * k), wv[k] = gld<float4>(np + base + 32 + 4 * k);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
       ss = __builtin_fmaf(u[k].x, u[k].x, ss), ss = __builtin_fmaf(u[k].y, u[k].y, ss);
       ss = __builtin_fmaf(u[k].z, u[k].z, ss), ss = __builtin_fmaf(u[k].w, u[k].w, ss);
       ss = __builtin_fmaf(v[k].x, v[k].x, ss), ss = __builtin_fmaf(v[k].y, v[k].y, ss);
       ss = __builtin_fmaf(v[k].z, v[k].z, ss), ss = __builtin_fmaf(v[k].w, v[k].w, ss);
       if (nw) {
-        const float4 wu = gld<float4>(nw + base + 4 * k), wv = gld<float4>(nw + base + 32 + 4 * k);
-        u[k] = make_float4(wu.x * u[k].x, wu.y * u[k].y, wu.z * u[k].z, wu.w * u[k].w);
-        v[k] = make_float4(wv.x * v[k].x, wv.y * v[k].y, wv.z * v[k].z, wv.w * v[k].w);
+        u[k] = make_float4(wu[k].x * u[k].x, wu[k].y * u[k].y, wu[k].z * u[k].z, wu[k].w * u[k].w);
+        v[k] = make_float4(wv[k].x * v[k].x, wv[k].y * v[k].y, wv[k].z * v[k].z, wv[k].w * v[k].w);
       }
     }
     fill(x, u, v);
@@ -327,17 +333,24 @@ struct Tr<GQ_Q6_K> {
   }
   __device__ static void load_xg(X &x, const float *xg, const float *nw, int b, int p, float &ss) {
     const int base = 256 * b + 128 * (p >> 2) + 8 * (p & 3);
+    /* every load first (one memory round trip), as in TrQ4K8::load_xg */
+    const float *np = nw ? nw : xg;
+    float4 uu[4], vv[4], wu[4], wv[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-      float4 u = gld<float4>(xg + base + 32 * r), v = gld<float4>(xg + base + 32 * r + 4);
+      uu[r] = gld<float4>(xg + base + 32 * r), vv[r] = gld<float4>(xg + base + 32 * r + 4);
+      wu[r] = gld<float4>(np + base + 32 * r), wv[r] = gld<float4>(np + base + 32 * r + 4);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      float4 u = uu[r], v = vv[r];
       ss = __builtin_fmaf(u.x, u.x, ss), ss = __builtin_fmaf(u.y, u.y, ss);
       ss = __builtin_fmaf(u.z, u.z, ss), ss = __builtin_fmaf(u.w, u.w, ss);
       ss = __builtin_fmaf(v.x, v.x, ss), ss = __builtin_fmaf(v.y, v.y, ss);
       ss = __builtin_fmaf(v.z, v.z, ss), ss = __builtin_fmaf(v.w, v.w, ss);
       if (nw) {
-        const float4 wu = gld<float4>(nw + base + 32 * r), wv = gld<float4>(nw + base + 32 * r + 4);
-        u = make_float4(wu.x * u.x, wu.y * u.y, wu.z * u.z, wu.w * u.w);
-        v = make_float4(wv.x * v.x, wv.y * v.y, wv.z * v.z, wv.w * v.w);
+        u = make_float4(wu[r].x * u.x, wu[r].y * u.y, wu[r].z * u.z, wu[r].w * u.w);
+        v = make_float4(wv[r].x * v.x, wv[r].y * v.y, wv[r].z * v.z, wv[r].w * v.w);
       }
       x.v[r][0] = u.x, x.v[r][1] = u.y, x.v[r][2] = u.z, x.v[r][3] = u.w;
       x.v[r][4] = v.x, x.v[r][5] = v.y, x.v[r][6] = v.z, x.v[r][7] = v.w;
@@ -426,13 +439,18 @@ struct Tr<GQ_Q8_0> {
   }
   __device__ static void load_xg(X &x, const float *xg, const float *nw, int b, int p, float &ss) {
     (void)p;
+    /* every load first (one memory round trip), as in TrQ4K8::load_xg */
+    const float *np = nw ? nw : xg;
+    float4 uu[8], ww[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) uu[k] = gld<float4>(xg + 32 * b + 4 * k), ww[k] = gld<float4>(np + 32 * b + 4 * k);
 #pragma unroll
     for (int k = 0; k < 8; k++) {
-      float4 u = gld<float4>(xg + 32 * b + 4 * k);
+      float4 u = uu[k];
       ss = __builtin_fmaf(u.x, u.x, ss), ss = __builtin_fmaf(u.y, u.y, ss);
       ss = __builtin_fmaf(u.z, u.z, ss), ss = __builtin_fmaf(u.w, u.w, ss);
       if (nw) {
-        const float4 w = gld<float4>(nw + 32 * b + 4 * k);
+        const float4 w = ww[k];
         u = make_float4(w.x * u.x, w.y * u.y, w.z * u.z, w.w * u.w);
       }
       x.v[4 * k] = u.x, x.v[4 * k + 1] = u.y, x.v[4 * k + 2] = u.z, x.v[4 * k + 3] = u.w;
@@ -907,7 +925,9 @@ __device__ __forceinline__ void mvl_body(const MvArgs &a, const MvPlan &pl, int 
   } else {
     /* everything the loop needs from global memory besides the weights is
      * loaded and consumed first: x slices (and the RMSNorm sum of squares
-     * from team 0), the position and the RoPE table row */
+     * from team 0), the position and the RoPE table row.  (Issuing stage 0
+     * before them measured slower: stage 1 then goes out a round trip
+     * later.) */
 #pragma unroll
     for (int i = 0; i < TPW; i++) {
       const int b = (wj + i * pl.ts) * BPT + bt;
