@@ -72,19 +72,20 @@ __global__ __launch_bounds__(kThreads) void rope_append_kernel(RopeArgs a) {
   }
 }
 
-/* Positions per split-K chunk (one workgroup): 64 gives 1024 workgroups at
- * the 8B shape and ctx 8192, four per CU, whose load and compute phases
- * overlap each other (measured 1.3% faster per decode step than 128, the
- * same as 32). */
-constexpr int kChunk = 64;
+/* Positions per split-K chunk (one workgroup), chosen by the cache
+ * capacity.  64 gives 1024 workgroups at the 8B shape and ctx 8192, four per
+ * CU, whose load and compute phases overlap each other (measured 1.3% faster
+ * per decode step than 128, the same as 32).  Past 12288 positions the merge,
+ * which reads every chunk's partials, grows enough that 128 wins (16384:
+ * 32.7 vs 34.7 us per layer; 32768: 57.0 vs 61.9). */
+int chunk_for(int max_seq) { return max_seq > 12288 ? 128 : 64; }
 
-/* Workgroup (g, c) handles positions [64c, 64c + 64) of KV head g for the
- * G query heads sharing it.  Every K and V load of the chunk is issued before
- * any arithmetic (32 + 32 VGPRs per thread at head_dim 128), so a workgroup
- * costs one memory round trip plus its FMAs. */
-template <int HD, int G>
+/* Workgroup (g, c) handles positions [Sc, Sc + S) of KV head g for the G
+ * query heads sharing it.  Every K and V load of the chunk is issued before
+ * any arithmetic (S/2 + S/2 VGPRs per thread at head_dim 128), so a
+ * workgroup costs one memory round trip plus its FMAs. */
+template <int HD, int G, int S>
 __global__ __launch_bounds__(kThreads) void attn_partial_kernel(AttnArgs a) {
-  constexpr int S = kChunk;
   constexpr int LPP = HD / 8;          /* lanes per position, phase 1 */
   constexpr int PPI = kThreads / LPP;  /* positions per pass, phase 1 */
   constexpr int KIT = S / PPI;
@@ -209,7 +210,7 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
   const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int pos = a.pos_dev ? gld<int>(a.pos_dev) : a.pos;
   const int L = min(pos + 1, a.max_seq);
-  const int nc = (L + kChunk - 1) / kChunk;
+  const int nc = (L + a.s_max - 1) / a.s_max;
   const float *ml = a.part_ml + (size_t)h * a.nch * 2;
   float *sl = sw + a.nch;
   float m = -INFINITY;
@@ -251,7 +252,10 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
 
 template <int HD, int G>
 int launch_partial(const AttnArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL((attn_partial_kernel<HD, G>), dim3(a.n_kv, a.nch), dim3(kThreads), 0, s, a);
+  if (a.s_max == 128)
+    hipLaunchKernelGGL((attn_partial_kernel<HD, G, 128>), dim3(a.n_kv, a.nch), dim3(kThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL((attn_partial_kernel<HD, G, 64>), dim3(a.n_kv, a.nch), dim3(kThreads), 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
@@ -259,17 +263,19 @@ int launch_partial(const AttnArgs &a, hipStream_t s) {
 
 int gq_attn_nch(int n_kv, int max_seq) {
   (void)n_kv;
-  return (max_seq + kChunk - 1) / kChunk;
+  const int s = chunk_for(max_seq);
+  return (max_seq + s - 1) / s;
 }
 
 int gq_attn_smax(int max_seq, int nch) {
-  (void)max_seq;
   (void)nch;
-  return kChunk;
+  return chunk_for(max_seq);
 }
 
 int gq_launch_attention(const AttnArgs &a, hipStream_t s, hipEvent_t mid) {
-  if (a.n_kv <= 0 || a.n_heads % a.n_kv || a.nch != gq_attn_nch(a.n_kv, a.max_seq)) return -1;
+  if (a.n_kv <= 0 || a.n_heads % a.n_kv || a.nch != gq_attn_nch(a.n_kv, a.max_seq) ||
+      a.s_max != chunk_for(a.max_seq))
+    return -1;
   if (a.hd % 32 || (size_t)a.nch * 2 * sizeof(float) > 32768) return -1;
   const int G = a.n_heads / a.n_kv;
   int rc = -1;

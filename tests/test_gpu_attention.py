@@ -1,7 +1,8 @@
 """Split-K GQA decode attention against the oracle's restatement of the
 reference (engine.c:433-509) on seeded N(0,1) K/V and N(0,1) queries (the
-config-4 setting), at the 8B shape up to 8192 positions, the TinyLlama shape
-and edge lengths.  Tolerance: relative L2 <= 1e-5."""
+config-4 setting), at the 8B shape up to 16384 positions (64- and
+128-position chunks), the TinyLlama shape and edge lengths.  Tolerance:
+relative L2 <= 1e-5."""
 import numpy as np
 import pytest
 
@@ -20,6 +21,9 @@ pytestmark = pytest.mark.gpu
     (32, 4, 64, 640, 640),      # cache exactly full
     (8, 8, 64, 77, 96),         # no grouping (G = 1)
     (64, 8, 128, 1000, 1024),   # G = 8 at head_dim 128
+    (32, 8, 128, 12289, 12400),  # 128-position chunks (caches past 12288)
+    (32, 8, 128, 16384, 16384),  # config 4 at ctx 16384, cache exactly full
+    (32, 4, 64, 13000, 13000),   # 128-position chunks at head_dim 64
 ])
 def test_attention_vs_oracle(ctx, orc, nh, nkv, hd, L, ms):
     ctx.kv_init(1, nkv, hd, ms, 500000.0)
