@@ -159,3 +159,60 @@ def test_bind_model_and_gpu_prefill_slot(host, ref, orc):
     cpu.close()
     gpu.close()
     host.backend_destroy(b)
+
+
+@pytest.mark.gpu
+def test_n_gpu_layers_split(host, ref, orc):
+    """The --n-gpu-layers split (loader.c:672-729, engine.c:314-350): layer 0
+    runs on the device through the per-layer hook (gq_hip_transformer_layer:
+    host hidden state in and out, its new K/V row written back into the
+    reference's host cache), layer 1 through the reference's own CPU
+    transformer_layer on that same KVCache.  Against both layers on the CPU:
+    each layer's hidden state within the decode tolerance (1e-3 relative L2)
+    and the host cache's new rows alike."""
+    import guanaco_amd.hip as H
+    from oracle import F32, RModelWeights, rtensor
+    spec, ms, pre = S.TINY_TEST, 64, 24
+    b = host.backend_create(C.byref(RBackendConfig(BACKEND_HIP, 4, 0, spec.n_layers)))
+    assert b, "HIP backend unavailable on a GPU box"
+    host.hip_backend_bind_model.argtypes = [C.c_void_p, C.POINTER(RModelWeights), C.c_void_p]
+    ref.lib.kv_cache_head_stride.argtypes = [C.c_void_p]
+    hm = HostModel(orc, spec, ms)
+    cpu, mix = RefModel(ref, hm), RefModel(ref, hm)
+    kv = hm.new_kv()
+    kv.prefill(orc, spec, pre)
+    cpu.load_kv(kv)
+    mix.load_kv(kv)
+    for l in range(spec.n_layers):
+        for f in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down"):
+            assert host.hip_backend_upload(b, getattr(mix.mw.layers[l], f)) == 0
+    assert host.hip_backend_bind_model(b, C.byref(mix.mw), mix.kv) == 0  # device cache = host prefix
+    ctx = host.hip_backend_context(b)
+    h0 = orc.synth_normal(5, spec.hidden)
+
+    def cpu_layer(m, h, l):
+        ref.lib.scratch_reset(m.scratch)
+        t = rtensor(h, F32, (1, spec.hidden))
+        ref.lib.transformer_layer(C.byref(t), C.byref(m.mw.layers[l]), m.kv, l, pre, m.scratch,
+                                  C.byref(m.mw.config), ref.vtable)
+
+    hc = [h0.copy()]
+    for l in range(spec.n_layers):
+        h = hc[-1].copy()
+        cpu_layer(cpu, h, l)
+        hc.append(h)
+    hs = h0.copy()
+    rc = H.lib.gq_hip_transformer_layer(ctx, 0, pre, hs.ctypes.data_as(C.POINTER(C.c_float)),
+                                        C.cast(ref.lib.kv_cache_raw_k(mix.kv, 0), C.POINTER(C.c_float)),
+                                        C.cast(ref.lib.kv_cache_raw_v(mix.kv, 0), C.POINTER(C.c_float)),
+                                        ref.lib.kv_cache_head_stride(mix.kv))
+    assert rc == 0 and rel_l2(hs, hc[1]) < 1e-3
+    for w in ("k", "v"):  # the device layer's new row, in the reference's host cache
+        row = lambda m: m.slab(w, 0).reshape(spec.n_kv_heads, ms, spec.head_dim)[:, pre]  # noqa: E731
+        assert np.abs(row(mix)).sum() > 0 and rel_l2(row(mix), row(cpu)) < 1e-3
+    for l in range(1, spec.n_layers):
+        cpu_layer(mix, hs, l)
+        assert rel_l2(hs, hc[l + 1]) < 1e-3, l
+    cpu.close()
+    mix.close()
+    host.backend_destroy(b)
