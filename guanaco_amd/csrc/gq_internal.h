@@ -116,6 +116,23 @@ int gq_launch_embed(int dtype, const void *table, int hidden, const int *token_d
 int gq_launch_argmax(const float *x, int n, float *scratch, int nblk, int *out_index,
                      int *tokens, int *step_dev, int *pos_dev, hipStream_t s);
 int gq_argmax_blocks(int n);
+
+/* On-device sampling (gq_sample.hip).  top-k handles k <= kMaxTopK. */
+constexpr int kMaxTopK = 1024;
+struct SampleWs {
+  float *keys = nullptr;           /* sorted logits (top-p) or probabilities (temperature) */
+  int *ids_in = nullptr, *ids = nullptr;
+  void *cub = nullptr;             /* radix-sort temporary storage */
+  size_t cub_bytes = 0;
+  int cap = 0;                     /* vocabulary the buffers hold */
+};
+/* radix-sort temporary bytes for a vocabulary */
+size_t gq_sample_ws_bytes(int vocab);
+/* The reference's sampler choice (generate.c:302-311) for rnd = its rand()
+ * draw: 0 launched (token -> *out on the device), 1 greedy (use the argmax),
+ * -1 bad argument or workspace, -2 top_k above kMaxTopK, -4 launch error. */
+int gq_launch_sample(const float *logits, int vocab, float temperature, int top_k, float top_p, int rnd,
+                     const SampleWs &ws, int *out, hipStream_t s);
 int gq_launch_silu_mul(float *gate, const float *up, int n, hipStream_t s);
 int gq_launch_copy(void *dst, const void *src, size_t bytes, int n_cu, hipStream_t s);
 

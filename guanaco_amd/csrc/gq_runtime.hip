@@ -72,6 +72,8 @@ struct gq_ctx {
   std::vector<gq_layer> layers;
   Workspace ws;
   PrefillWs pf;
+  SampleWs sw;
+  int *d_sample = nullptr; /* sampled token (device) */
   /* graph */
   hipGraph_t graph = nullptr;
   hipGraphExec_t gexec = nullptr;
@@ -1284,6 +1286,65 @@ extern "C" int gq_hip_argmax_dev(gq_ctx *c, const float *x, int n, int *out_inde
   (void)hipStreamSynchronize(c->stream);
   gq_hip_free(c, scratch);
   return rc ? fail(c, rc, "argmax") : 0;
+}
+
+/* ---- on-device sampling (tokenizer.c:175-333, generate.c:302-311) ---- */
+static int sample_ensure(gq_ctx *c, int vocab, bool big) {
+  SampleWs &w = c->sw;
+  if (!c->d_sample && !(c->d_sample = (int *)dev_alloc(c, sizeof(int)))) return -4;
+  if (!big || w.cap >= vocab) return 0;
+  const size_t cub = gq_sample_ws_bytes(vocab);
+  float *keys = (float *)dev_alloc(c, sizeof(float) * vocab);
+  int *ids_in = (int *)dev_alloc(c, sizeof(int) * vocab), *ids = (int *)dev_alloc(c, sizeof(int) * vocab);
+  void *tmp = dev_alloc(c, cub);
+  if (!keys || !ids_in || !ids || !tmp) return -4;
+  if (w.keys) gq_hip_free(c, w.keys), gq_hip_free(c, w.ids_in), gq_hip_free(c, w.ids), gq_hip_free(c, w.cub);
+  w.keys = keys, w.ids_in = ids_in, w.ids = ids, w.cub = tmp, w.cub_bytes = cub, w.cap = vocab;
+  return 0;
+}
+
+/* The next token from device logits as the reference's generate loop picks
+ * it; greedy falls back to the argmax.  Returns the token or < 0. */
+static int sample_on_device(gq_ctx *c, const float *logits, int vocab, float temperature, int top_k, float top_p,
+                            int rnd) {
+  /* top-p and plain temperature sampling use the vocabulary-sized buffers */
+  const bool big = temperature > 0.0f && !(top_k > 0 && top_k < vocab) && top_p > 0.0f;
+  int rc = sample_ensure(c, vocab, big);
+  if (rc) return rc;
+  rc = gq_launch_sample(logits, vocab, temperature, top_k, top_p, rnd, c->sw, c->d_sample, c->stream);
+  if (rc == 1) { /* greedy */
+    const int nblk = gq_argmax_blocks(vocab);
+    float *scratch = c->ws.amax && c->ws.amax_blocks >= nblk ? c->ws.amax
+                                                             : (float *)dev_alloc(c, sizeof(float) * 2 * nblk);
+    if (!scratch) return -4;
+    rc = gq_launch_argmax(logits, vocab, scratch, nblk, c->d_sample, nullptr, nullptr, nullptr, c->stream);
+    if (scratch != c->ws.amax) {
+      (void)hipStreamSynchronize(c->stream);
+      gq_hip_free(c, scratch);
+    }
+  }
+  if (rc == -2) return fail(c, -2, "top_k %d above the device limit %d", top_k, kMaxTopK);
+  if (rc) return fail(c, rc, "sampling launch failed");
+  int tok = -1;
+  HIPCHK(c, hipMemcpyAsync(&tok, c->d_sample, sizeof(int), hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return tok;
+}
+
+extern "C" int gq_hip_sample_dev(gq_ctx *c, const float *logits, int vocab, float temperature, int top_k,
+                                 float top_p, int rnd) {
+  if (!c || !logits || vocab <= 0) return -1;
+  return sample_on_device(c, logits, vocab, temperature, top_k, top_p, rnd);
+}
+
+extern "C" int gq_hip_forward_sample(gq_ctx *c, int token, int pos, float temperature, int top_k, float top_p,
+                                     int rnd) {
+  if (!c) return -1;
+  int rc = check_pos(c, pos, 1);
+  if (rc) return rc;
+  if (token < 0 || token >= c->m.vocab) return fail(c, -1, "token %d out of range", token);
+  if ((rc = run_step(c, token, pos, false, nullptr))) return fail(c, rc, "step launch failed");
+  return sample_on_device(c, c->ws.logits, c->m.vocab, temperature, top_k, top_p, rnd);
 }
 
 /* fp32 x -> the bf16 copy the GEMM reads */

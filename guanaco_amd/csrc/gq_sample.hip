@@ -1,0 +1,435 @@
+/*
+ * gq_sample.hip — sampling the next token on the device from logits already
+ * there (the LM head's output), so a sampled decode step needs no logits
+ * round trip (tokenizer.c:175-333 on the host copies 501 KiB per token at
+ * the 8B shape).
+ *
+ * The reference draws one rand() per sampled token and scales it as
+ * (float)rand() / (float)RAND_MAX (temperature, top-k) or in double
+ * (top-p).  The caller passes that raw draw (`rnd`), so with the same libc
+ * stream the device sees the same random numbers.
+ *
+ *   top-k (tokenizer.c:219-280): the reference keeps k slots, filled with
+ *     logits 0..k-1, and for every later logit above the slots' minimum
+ *     replaces that minimum (the lowest slot among equal minima).  The
+ *     slots' order decides which token a given draw picks, so the kernel
+ *     replays exactly that insertion sequence: logits 0..kPre-1 one chunk at
+ *     a time, then every later logit above the minimum after kPre (the
+ *     running minimum only rises, so nothing below it can be inserted
+ *     later), in index order.  The softmax over the slots and the draw then
+ *     run on one thread in the reference's order.
+ *   top-p (tokenizer.c:282-333): stable descending sort (hipCUB radix sort;
+ *     the reference's qsort is glibc's merge sort, stable for equal logits),
+ *     then the cumulative probabilities in double.
+ *   temperature (tokenizer.c:187-217): the exponentials in parallel, the
+ *     reference's sequential float sum and scan on one thread (see
+ *     temp_kernel).
+ */
+#include <hipcub/hipcub.hpp>
+
+#include "gq_device.h"
+#include "gq_internal.h"
+
+namespace {
+
+constexpr int kST = 1024;           /* threads of the one-workgroup kernels */
+constexpr int kSW = kST / GQ_WAVE;  /* their waves */
+constexpr int kPre = 4 * kST;       /* logits replayed chunk by chunk before the filter */
+constexpr int kCandCap = 8192;      /* filtered candidates held in LDS */
+constexpr float kRandMax = 2147483647.0f; /* RAND_MAX of glibc, as the reference casts it */
+
+/* A float's bits mapped to an unsigned integer of the same order. */
+__device__ __forceinline__ uint32_t ord_bits(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+/* 64-bit DPP move of the row operation CTRL (rows not in RM keep their own
+ * value) */
+template <int CTRL, int RM>
+__device__ __forceinline__ uint64_t dpp64(uint64_t k) {
+  const int lo = (int)(uint32_t)k, hi = (int)(uint32_t)(k >> 32);
+  const uint32_t nlo = (uint32_t)__builtin_amdgcn_update_dpp(lo, lo, CTRL, RM, 0xf, false);
+  const uint32_t nhi = (uint32_t)__builtin_amdgcn_update_dpp(hi, hi, CTRL, RM, 0xf, false);
+  return ((uint64_t)nhi << 32) | nlo;
+}
+
+/* The wave's smallest 64-bit key, in every lane: quad swaps, half-row and
+ * row mirrors, then the row broadcasts 15 and 31 into lane 63. */
+__device__ __forceinline__ uint64_t wave_min_key(uint64_t k) {
+  uint64_t t;
+  t = dpp64<0xb1, 0xf>(k), k = t < k ? t : k; /* quad_perm [1,0,3,2] */
+  t = dpp64<0x4e, 0xf>(k), k = t < k ? t : k; /* quad_perm [2,3,0,1] */
+  t = dpp64<0x141, 0xf>(k), k = t < k ? t : k; /* row_half_mirror */
+  t = dpp64<0x140, 0xf>(k), k = t < k ? t : k; /* row_mirror */
+  t = dpp64<0x142, 0xa>(k), k = t < k ? t : k; /* row_bcast:15 */
+  t = dpp64<0x143, 0xc>(k), k = t < k ? t : k; /* row_bcast:31 */
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, 63);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(k >> 32), 63);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+/* (value, slot) of the slots' minimum with the reference's tie rule (the
+ * first slot holding the smallest value), over slots [0, k), by one wave:
+ * the minimum of (value order, slot) keys */
+__device__ void wave_min(const float *tv, int k, int lane, float &mv, int &mj) {
+  uint64_t key = ~0ull;
+  for (int s = lane; s < k; s += GQ_WAVE) {
+    const float t = tv[s];
+    const uint64_t c = ((uint64_t)ord_bits(t == 0.f ? 0.f : t) << 32) | (uint32_t)s; /* -0 equals +0 */
+    key = c < key ? c : key;
+  }
+  key = wave_min_key(key);
+  mj = (int)(uint32_t)key;
+  mv = tv[mj];
+}
+
+/* Compact the flagged (index, value) pairs of one 1024-logit chunk into
+ * out[base ..] in index order; returns the count (all threads). */
+__device__ int compact(bool flag, int i, float v, int *oi, float *ov, int base, int cap, int *wcount) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t bal = __ballot(flag);
+  const int pre = __popcll(bal & ((1ull << lane) - 1ull));
+  if (lane == 0) wcount[wave] = __popcll(bal);
+  __syncthreads();
+  int off = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < kSW; w++) {
+    off += w < wave ? wcount[w] : 0;
+    tot += wcount[w];
+  }
+  if (flag && base + off + pre < cap) oi[base + off + pre] = i, ov[base + off + pre] = v;
+  __syncthreads();
+  return tot;
+}
+
+/* Replay of the reference's top-k slot updates over candidates [0, n) in
+ * index order, by wave 0; returns with the slots' minimum in (mv, mj).
+ * Candidates are read 64 at a time and only those above the current
+ * minimum looked at, in order. */
+__device__ void insert_all(float *tv, int *ti, int k, const int *ci, const float *cv, int n, int lane, float &mv,
+                           int &mj) {
+  for (int q0 = 0; q0 < n; q0 += GQ_WAVE) {
+    const int q = q0 + lane;
+    const float v = q < n ? cv[q] : -INFINITY;
+    const int id = q < n ? ci[q] : 0;
+    uint64_t live = __ballot(q < n && v > mv);
+    while (live) {
+      const int l = __builtin_ctzll(live); /* the next candidate in index order */
+      const float vl = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+      const int il = __builtin_amdgcn_readlane(id, l);
+      if (lane == 0) tv[mj] = vl, ti[mj] = il;
+      __builtin_amdgcn_s_waitcnt(0xc07f); /* lgkmcnt(0): the slot write lands before the rescan */
+      __builtin_amdgcn_wave_barrier();
+      wave_min(tv, k, lane, mv, mj);
+      live = __ballot(q < n && lane > l && v > mv);
+    }
+  }
+}
+
+__global__ __launch_bounds__(kST) void topk_kernel(const float *x, int V, int k, float T, int rnd, int *out) {
+  __shared__ float tv[kMaxTopK], pr[kMaxTopK];
+  __shared__ int ti[kMaxTopK];
+  __shared__ int ci[kCandCap];
+  __shared__ float cv[kCandCap];
+  __shared__ int wcount[kSW];
+  __shared__ float s_mv;
+  __shared__ int s_mj;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int j = tid; j < k; j += kST) ti[j] = j, tv[j] = x[j];
+  __syncthreads();
+  if (wave == 0) {
+    float mv;
+    int mj;
+    wave_min(tv, k, lane, mv, mj);
+    if (lane == 0) s_mv = mv, s_mj = mj;
+  }
+  __syncthreads();
+  /* logits k .. pre-1: chunk by chunk, each chunk's logits above the current
+   * minimum inserted in index order */
+  const int pre = min(V, max(kPre, k));
+  for (int base = k; base < pre; base += kST) {
+    const int i = base + tid;
+    const float v = i < pre ? x[i] : 0.f;
+    const int n = compact(i < pre && v > s_mv, i, v, ci, cv, 0, kCandCap, wcount);
+    if (wave == 0) {
+      float mv = s_mv;
+      int mj = s_mj;
+      insert_all(tv, ti, k, ci, cv, n, lane, mv, mj);
+      if (lane == 0) s_mv = mv, s_mj = mj;
+    }
+    __syncthreads();
+  }
+  /* the rest: everything above the minimum after `pre` logits, gathered in
+   * index order, then inserted in that order; should the list outgrow LDS
+   * (logits rising along the vocabulary), the remainder goes chunk by chunk */
+  const float thr = s_mv;
+  int ncand = 0, stop = V;
+  for (int base0 = pre; base0 < V && stop == V; base0 += 8 * kST) {
+    float vv[8]; /* eight chunks' loads in flight at once */
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int i = base0 + u * kST + tid;
+      vv[u] = i < V ? x[i] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int base = base0 + u * kST, i = base + tid;
+      if (stop == V && base < V) {
+        const int n = compact(i < V && vv[u] > thr, i, vv[u], ci, cv, ncand, kCandCap, wcount);
+        if (ncand + n > kCandCap)
+          stop = base; /* chunk `base` onwards not gathered */
+        else
+          ncand += n;
+      }
+    }
+  }
+  if (wave == 0) {
+    float mv = s_mv;
+    int mj = s_mj;
+    insert_all(tv, ti, k, ci, cv, ncand, lane, mv, mj);
+    if (lane == 0) s_mv = mv, s_mj = mj;
+  }
+  __syncthreads();
+  for (int base = stop; base < V; base += kST) {
+    const int i = base + tid;
+    const float v = i < V ? x[i] : 0.f;
+    const int n = compact(i < V && v > s_mv, i, v, ci, cv, 0, kCandCap, wcount);
+    if (wave == 0) {
+      float mv = s_mv;
+      int mj = s_mj;
+      insert_all(tv, ti, k, ci, cv, n, lane, mv, mj);
+      if (lane == 0) s_mv = mv, s_mj = mj;
+    }
+    __syncthreads();
+  }
+  /* temperature softmax over the slots and the draw, in the reference's
+   * order (tokenizer.c:254-276) */
+  if (tid == 0) {
+    float mx = tv[0];
+    for (int j = 1; j < k; j++)
+      if (tv[j] > mx) mx = tv[j];
+    float sum = 0.f;
+    for (int j = 0; j < k; j++) {
+      const float p = expf((tv[j] - mx) / T);
+      pr[j] = p;
+      sum += p;
+    }
+    const float r = ((float)rnd / kRandMax) * sum;
+    float acc = 0.f;
+    int pick = k - 1;
+    for (int j = 0; j < k; j++) {
+      acc += pr[j];
+      if (r <= acc) {
+        pick = j;
+        break;
+      }
+    }
+    *out = ti[pick];
+  }
+}
+
+/* Block-wide exclusive scan of one double per thread; returns the prefix,
+ * *total gets the sum (all threads). */
+__device__ double block_scan(double v, double *total, double *sw) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  double inc = v;
+#pragma unroll
+  for (int o = 1; o < GQ_WAVE; o <<= 1) {
+    const double t = __shfl_up(inc, o);
+    if (lane >= o) inc += t;
+  }
+  if (lane == GQ_WAVE - 1) sw[wave] = inc;
+  __syncthreads();
+  double off = 0.0, tot = 0.0;
+#pragma unroll
+  for (int w = 0; w < kSW; w++) {
+    off += w < wave ? sw[w] : 0.0;
+    tot += sw[w];
+  }
+  __syncthreads();
+  *total = tot;
+  return off + inc - v;
+}
+
+__device__ float block_max(float v, float *sw) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v = gq_wave_max(v);
+  if (lane == 0) sw[wave] = v;
+  __syncthreads();
+  float m = sw[0];
+#pragma unroll
+  for (int w = 1; w < kSW; w++) m = fmaxf(m, sw[w]);
+  __syncthreads();
+  return m;
+}
+
+/* The first index i in [0, n) whose inclusive running sum of w(i) reaches r
+ * (n - 1 when none does); w(i) summed in double, each thread over one
+ * contiguous segment. */
+template <typename W>
+__device__ int first_reaching(W w, int n, double r, double *sw, int *s_pick) {
+  const int tid = threadIdx.x, seg = (n + kST - 1) / kST, lo = min(tid * seg, n), hi = min(lo + seg, n);
+  double part = 0.0;
+  for (int i = lo; i < hi; i++) part += w(i);
+  double tot;
+  const double before = block_scan(part, &tot, sw);
+  if (tid == 0) *s_pick = n - 1;
+  __syncthreads();
+  if (before < r && r <= before + part) {
+    /* the running sum reaches r inside this segment (its last element when
+     * the sequential sum rounds just below before + part) */
+    double acc = before;
+    int found = hi - 1;
+    for (int i = lo; i < hi; i++) {
+      acc += w(i);
+      if (r <= acc) {
+        found = i;
+        break;
+      }
+    }
+    atomicMin(s_pick, found);
+  } else if (r <= before && tid == 0) {
+    atomicMin(s_pick, 0);
+  }
+  __syncthreads();
+  return *s_pick;
+}
+
+/* softmax(x / T) over the vocabulary and one draw (tokenizer.c:187-217).
+ * The reference sums the probabilities sequentially in float, and over a
+ * large vocabulary that sum's rounding moves the cumulative boundaries by
+ * far more than a last bit (a double sum picks a different token for about
+ * one draw in four at 128256 entries), so the two sequential loops run as
+ * written, on one thread: the workgroup computes the exponentials in
+ * parallel and stages them through LDS in chunks of kChunkP. */
+constexpr int kChunkP = 32768;
+
+constexpr int kCkMax = 4096; /* 64-entry blocks: vocabularies up to 262144 */
+
+__global__ __launch_bounds__(kST) void temp_kernel(const float *x, int V, float T, int rnd, float *prob, int *out) {
+  __shared__ float sf[kSW];
+  __shared__ float chunk[kChunkP];
+  __shared__ float ck[kCkMax + 1]; /* running sum before each 64-entry block, then the total */
+  __shared__ float s_r;
+  __shared__ int s_blk, s_pick;
+  const int tid = threadIdx.x;
+  float m = -INFINITY;
+  for (int i = tid; i < V; i += kST) m = fmaxf(m, x[i]);
+  const float mx = block_max(m, sf);
+  for (int i = tid; i < V; i += kST) prob[i] = expf((x[i] - mx) / T);
+  /* the reference's running float sum, one thread, its value recorded at
+   * the start of every 64-entry block */
+  float sum = 0.f;
+  for (int base = 0; base < V; base += kChunkP) {
+    const int n = min(kChunkP, V - base);
+    __syncthreads();
+    for (int i = tid; i < n; i += kST) chunk[i] = prob[base + i];
+    __syncthreads();
+    if (tid == 0)
+      for (int b = 0; b < n; b += 64) {
+        ck[(base + b) >> 6] = sum;
+        const int e = min(64, n - b);
+        if (e == 64) {
+#pragma unroll
+          for (int j = 0; j < 64; j++) sum += chunk[b + j];
+        } else {
+          for (int j = 0; j < e; j++) sum += chunk[b + j];
+        }
+      }
+  }
+  const int nblk = (V + 63) >> 6;
+  if (tid == 0) ck[nblk] = sum, s_r = ((float)rnd / kRandMax) * sum, s_blk = nblk, s_pick = V - 1;
+  __syncthreads();
+  /* the first block whose closing sum reaches r (sums never decrease) ... */
+  const float r = s_r;
+  for (int q = tid; q < nblk; q += kST)
+    if (r <= ck[q + 1]) {
+      atomicMin(&s_blk, q);
+      break;
+    }
+  __syncthreads();
+  /* ... then its 64 additions again, from its opening sum */
+  if (tid == 0 && s_blk < nblk) {
+    float acc = ck[s_blk];
+    const int lo = s_blk << 6, hi = min(lo + 64, V);
+    for (int i = lo; i < hi; i++) {
+      acc += prob[i];
+      if (r <= acc) {
+        s_pick = i;
+        break;
+      }
+    }
+  }
+  __syncthreads();
+  if (tid == 0) *out = s_pick;
+}
+
+/* top-p over the logits sorted in descending order (keys) with their token
+ * ids (ids), tokenizer.c:296-333 */
+__global__ __launch_bounds__(kST) void topp_kernel(const float *keys, const int *ids, int V, float p, float T, int rnd,
+                                                    int *out) {
+  __shared__ double sw[kSW];
+  __shared__ int s_pick;
+  const float mx = keys[0];
+  auto w = [&](int i) { return (double)expf((keys[i] - mx) / T); };
+  double tot = 0.0;
+  {
+    const int seg = (V + kST - 1) / kST, lo = min((int)threadIdx.x * seg, V), hi = min(lo + seg, V);
+    double part = 0.0;
+    for (int i = lo; i < hi; i++) part += w(i);
+    (void)block_scan(part, &tot, sw);
+  }
+  /* cutoff: how many leading tokens until the cumulative share reaches p */
+  const double tot_c = tot;
+  auto share = [&](int i) { return w(i) / tot_c; };
+  const int cutoff = first_reaching(share, V, (double)p, sw, &s_pick) + 1;
+  /* the draw over the first `cutoff` tokens */
+  double cut = 0.0;
+  {
+    const int seg = (cutoff + kST - 1) / kST, lo = min((int)threadIdx.x * seg, cutoff), hi = min(lo + seg, cutoff);
+    double part = 0.0;
+    for (int i = lo; i < hi; i++) part += w(i);
+    (void)block_scan(part, &cut, sw);
+  }
+  const double r = ((double)rnd / 2147483647.0) * cut;
+  const int pick = first_reaching(w, cutoff, r, sw, &s_pick);
+  if (threadIdx.x == 0) *out = ids[pick];
+}
+
+__global__ void iota_kernel(int *v, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) v[i] = i;
+}
+
+} // namespace
+
+size_t gq_sample_ws_bytes(int vocab) {
+  size_t cub = 0;
+  (void)hipcub::DeviceRadixSort::SortPairsDescending(nullptr, cub, (const float *)nullptr, (float *)nullptr,
+                                                     (const int *)nullptr, (int *)nullptr, vocab, 0, 32);
+  return cub;
+}
+
+int gq_launch_sample(const float *logits, int vocab, float temperature, int top_k, float top_p, int rnd,
+                     const SampleWs &ws, int *out, hipStream_t s) {
+  if (vocab <= 0 || !logits || !out) return -1;
+  if (temperature <= 0.0f) return 1; /* greedy: the argmax path */
+  if (top_k > 0 && top_k < vocab) {
+    if (top_k > kMaxTopK) return -2;
+    hipLaunchKernelGGL(topk_kernel, dim3(1), dim3(kST), 0, s, logits, vocab, top_k, temperature, rnd, out);
+  } else if (top_p < 1.0f) {
+    if (top_p <= 0.0f) return 1; /* greedy (tokenizer.c:287) */
+    if (!ws.keys || !ws.ids_in || !ws.ids || !ws.cub || ws.cap < vocab) return -1;
+    hipLaunchKernelGGL(iota_kernel, dim3((vocab + 255) / 256), dim3(256), 0, s, ws.ids_in, vocab);
+    size_t bytes = ws.cub_bytes;
+    if (hipcub::DeviceRadixSort::SortPairsDescending(ws.cub, bytes, logits, ws.keys, ws.ids_in, ws.ids, vocab, 0,
+                                                     32, s) != hipSuccess)
+      return -4;
+    hipLaunchKernelGGL(topp_kernel, dim3(1), dim3(kST), 0, s, ws.keys, ws.ids, vocab, top_p, temperature, rnd, out);
+  } else {
+    if (!ws.keys || ws.cap < vocab || vocab > 64 * kCkMax) return -1;
+    hipLaunchKernelGGL(temp_kernel, dim3(1), dim3(kST), 0, s, logits, vocab, temperature, rnd, ws.keys, out);
+  }
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}

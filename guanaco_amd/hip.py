@@ -66,6 +66,8 @@ def _load():
         "gq_hip_decode_layer_dev": (C.c_int, [_vp, C.c_int, C.c_int, _vp]),
         "gq_hip_transformer_layer": (C.c_int, [_vp, C.c_int, C.c_int, _fp, _fp, _fp, C.c_int]),
         "gq_hip_forward_token": (C.c_int, [_vp, C.c_int, C.c_int, _fp, _fp]),
+        "gq_hip_sample_dev": (C.c_int, [_vp, _vp, C.c_int, C.c_float, C.c_int, C.c_float, C.c_int]),
+        "gq_hip_forward_sample": (C.c_int, [_vp, C.c_int, C.c_int, C.c_float, C.c_int, C.c_float, C.c_int]),
         "gq_hip_decode_loop": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int,
                                          C.POINTER(C.c_int32), C.POINTER(C.c_float)]),
         "gq_hip_profile_step": (C.c_int, [_vp, C.c_int, C.c_int, C.POINTER(C.c_double),

@@ -25,6 +25,11 @@
         causal attention of the 512 tokens, and forward() of a 512-token
         prompt through the whole 32-layer model.
 
+    python3 -m guanaco_amd.prof sample --vocab 128256 --iters 50
+        on-device sampling (gq_hip_sample_dev) of N(0, 3^2) logits already
+        in HBM: greedy, top-k 40, top-p 0.9 and plain temperature, each the
+        wall time per call including the 4-byte token copy back.
+
 The decode workload itself is ``python3 bench.py --eager`` (one kernel launch
 per op, so per-dispatch counters map onto ops).
 """
@@ -240,6 +245,25 @@ def run_gemm(dtype, rows, cols, T, iters):
     ctx.close()
 
 
+def run_sample(vocab, iters):
+    ctx = H.Context(0)
+    x = (np.random.default_rng(5).standard_normal(vocab) * 3.0).astype(np.float32)
+    xd = ctx.upload(x)
+    for what, T, k, p in (("greedy", 0.0, 0, 1.0), ("top-k 40, T 0.8", 0.8, 40, 1.0),
+                          ("top-p 0.9, T 0.8", 0.8, 0, 0.9), ("temperature 0.8", 0.8, 0, 1.0)):
+        rnd = 12345
+        for _ in range(3):
+            ctx.check(min(0, H.lib.gq_hip_sample_dev(ctx.h, xd.ptr, vocab, T, k, p, rnd)), "sample")
+        t0 = time.perf_counter()
+        for i in range(iters):
+            tok = H.lib.gq_hip_sample_dev(ctx.h, xd.ptr, vocab, T, k, p, rnd + i)
+            ctx.check(min(0, tok), "sample")
+        dt = (time.perf_counter() - t0) / iters
+        emit(what=f"on-device sampling, {what}", vocab=vocab, us_per_call=round(dt * 1e6, 1),
+             logits_bytes_not_copied=4 * vocab)
+    ctx.close()
+
+
 def run_configs():
     ctx = H.Context(0)
     config1(ctx)
@@ -260,6 +284,9 @@ def main():
     c.add_argument("--mib", type=int, default=256)
     c.add_argument("--iters", type=int, default=20)
     sub.add_parser("configs")
+    smp = sub.add_parser("sample")
+    smp.add_argument("--vocab", type=int, default=128256)
+    smp.add_argument("--iters", type=int, default=50)
     sub.add_parser("config5")
     g = sub.add_parser("gemm")
     g.add_argument("--dtype", type=int, default=S.Q4_K)
@@ -272,6 +299,8 @@ def main():
         run_copy(a.mib, a.iters)
     elif a.cmd == "configs":
         run_configs()
+    elif a.cmd == "sample":
+        run_sample(a.vocab, a.iters)
     elif a.cmd == "config5":
         config5(H.Context(0))
     elif a.cmd == "gemm":

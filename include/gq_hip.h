@@ -247,6 +247,24 @@ int gq_hip_qkv_rope_dev(gq_ctx *ctx, int layer, int pos, const float *hidden, fl
 int gq_hip_embed_dev(gq_ctx *ctx, int dtype, const void *table, int hidden, int token,
                      float *out);
 int gq_hip_argmax_dev(gq_ctx *ctx, const float *x, int n, int *out_index_dev);
+
+/* Sampling on the device, replacing the reference's sampler choice
+ * (generate.c:302-311) and sample_greedy / sample_top_k / sample_top_p /
+ * sample_temperature (tokenizer.c:175-333) without copying the logits to the
+ * host: temperature <= 0 -> greedy; 0 < top_k < vocab -> top-k (top_k at most
+ * 1024); top_p < 1 -> top-p (top_p <= 0 greedy); else temperature.  rnd is
+ * the value of the caller's rand() for this token (the reference draws one
+ * per sampled token; unused for greedy).  logits: vocab floats in device
+ * memory.  Returns the token, or -1 bad argument, -2 top_k above 1024, -4 HIP
+ * error.  Every mode follows the reference's arithmetic order (plain
+ * temperature sampling sums on one device thread, ~0.3 ms at 128256
+ * entries); exponentials come from the device's expf. */
+int gq_hip_sample_dev(gq_ctx *ctx, const float *logits, int vocab, float temperature, int top_k, float top_p,
+                      int rnd);
+/* forward() of one token (gq_hip_forward_token) followed by on-device
+ * sampling of the next one as above: generate.c:294-311 without the logits
+ * round trip.  Returns the sampled token or < 0 (as gq_hip_forward_token). */
+int gq_hip_forward_sample(gq_ctx *ctx, int token, int pos, float temperature, int top_k, float top_p, int rnd);
 int gq_hip_silu_mul_dev(gq_ctx *ctx, float *gate, const float *up, int n);
 /* ------------------------------------------------------- prefill chunk
  * y[t][n] = sum_k x[t][k] w[n][k] for t < T tokens at once on the bf16
