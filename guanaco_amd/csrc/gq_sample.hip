@@ -13,11 +13,13 @@
  *     logits 0..k-1, and for every later logit above the slots' minimum
  *     replaces that minimum (the lowest slot among equal minima).  The
  *     slots' order decides which token a given draw picks, so the kernel
- *     replays exactly that insertion sequence: logits 0..kPre-1 one chunk at
- *     a time, then every later logit above the minimum after kPre (the
- *     running minimum only rises, so nothing below it can be inserted
- *     later), in index order.  The softmax over the slots and the draw then
- *     run on one thread in the reference's order.
+ *     replays exactly that insertion sequence: logits 0..kPre-1 by one
+ *     wave, 64 at a time, then every later logit above the minimum after
+ *     kPre (the running minimum only rises, so nothing below it can be
+ *     inserted later), gathered by all waves and inserted in index order.
+ *     For k <= 64 the slots live in registers, one per lane, and a
+ *     replacement's new minimum is one DPP reduction.  The softmax over the
+ *     slots and the draw then run on one thread in the reference's order.
  *   top-p (tokenizer.c:282-333): stable descending sort (hipCUB radix sort;
  *     the reference's qsort is glibc's merge sort, stable for equal logits),
  *     then the cumulative probabilities in double.
@@ -84,125 +86,168 @@ __device__ void wave_min(const float *tv, int k, int lane, float &mv, int &mj) {
   mv = tv[mj];
 }
 
-/* Compact the flagged (index, value) pairs of one 1024-logit chunk into
- * out[base ..] in index order; returns the count (all threads). */
-__device__ int compact(bool flag, int i, float v, int *oi, float *ov, int base, int cap, int *wcount) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint64_t bal = __ballot(flag);
-  const int pre = __popcll(bal & ((1ull << lane) - 1ull));
-  if (lane == 0) wcount[wave] = __popcll(bal);
-  __syncthreads();
-  int off = 0, tot = 0;
-#pragma unroll
-  for (int w = 0; w < kSW; w++) {
-    off += w < wave ? wcount[w] : 0;
-    tot += wcount[w];
-  }
-  if (flag && base + off + pre < cap) oi[base + off + pre] = i, ov[base + off + pre] = v;
-  __syncthreads();
-  return tot;
+/* inverse of ord_bits */
+__device__ __forceinline__ float from_ord(uint32_t o) {
+  return __builtin_bit_cast(float, (o & 0x80000000u) ? (o ^ 0x80000000u) : ~o);
 }
 
-/* Replay of the reference's top-k slot updates over candidates [0, n) in
- * index order, by wave 0; returns with the slots' minimum in (mv, mj).
- * Candidates are read 64 at a time and only those above the current
- * minimum looked at, in order. */
-__device__ void insert_all(float *tv, int *ti, int k, const int *ci, const float *cv, int n, int lane, float &mv,
-                           int &mj) {
-  for (int q0 = 0; q0 < n; q0 += GQ_WAVE) {
-    const int q = q0 + lane;
-    const float v = q < n ? cv[q] : -INFINITY;
-    const int id = q < n ? ci[q] : 0;
-    uint64_t live = __ballot(q < n && v > mv);
-    while (live) {
-      const int l = __builtin_ctzll(live); /* the next candidate in index order */
-      const float vl = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
-      const int il = __builtin_amdgcn_readlane(id, l);
-      if (lane == 0) tv[mj] = vl, ti[mj] = il;
-      __builtin_amdgcn_s_waitcnt(0xc07f); /* lgkmcnt(0): the slot write lands before the rescan */
-      __builtin_amdgcn_wave_barrier();
-      wave_min(tv, k, lane, mv, mj);
-      live = __ballot(q < n && lane > l && v > mv);
-    }
+/* The k slots of the reference's top-k, held by wave 0.  k <= 64: one slot
+ * per lane in registers; larger k: in LDS. */
+struct RegSlots {
+  float v;
+  int i, k, lane;
+  __device__ void init(const float *x, int k_, int lane_) {
+    k = k_, lane = lane_;
+    v = lane < k ? x[lane] : 0.f;
+    i = lane;
+  }
+  /* the minimum with the reference's tie rule (first slot of the smallest) */
+  __device__ void minimum(float &mv, int &mj) const {
+    const uint64_t key = lane < k ? ((uint64_t)ord_bits(v == 0.f ? 0.f : v) << 32) | (uint32_t)lane : ~0ull;
+    const uint64_t m = wave_min_key(key);
+    mj = (int)(uint32_t)m;
+    mv = from_ord((uint32_t)(m >> 32));
+  }
+  __device__ void replace(int mj, float nv, int ni) {
+    if (lane == mj) v = nv, i = ni;
+  }
+  __device__ void store(float *tv, int *ti) const {
+    if (lane < k) tv[lane] = v, ti[lane] = i;
+  }
+};
+
+struct LdsSlots {
+  float *tv;
+  int *ti;
+  int k, lane;
+  __device__ void init(const float *x, int k_, int lane_) {
+    k = k_, lane = lane_;
+    for (int j = lane; j < k; j += GQ_WAVE) tv[j] = x[j], ti[j] = j;
+    __builtin_amdgcn_s_waitcnt(0xc07f); /* lgkmcnt(0) */
+    __builtin_amdgcn_wave_barrier();
+  }
+  __device__ void minimum(float &mv, int &mj) const { wave_min(tv, k, lane, mv, mj); }
+  __device__ void replace(int mj, float nv, int ni) {
+    if (lane == 0) tv[mj] = nv, ti[mj] = ni;
+    __builtin_amdgcn_s_waitcnt(0xc07f); /* the slot write lands before the rescan */
+    __builtin_amdgcn_wave_barrier();
+  }
+  __device__ void store(float *, int *) const {}
+};
+
+/* Wave 0 replays the reference's slot updates for a group of up to 64
+ * candidates held one per lane in index order (valid lanes flagged). */
+template <class S>
+__device__ __forceinline__ void insert_lanes(S &sl, bool valid, float v, int id, float &mv, int &mj) {
+  const int lane = sl.lane;
+  uint64_t live = __ballot(valid && v > mv);
+  while (live) {
+    const int l = __builtin_ctzll(live); /* the next candidate in index order */
+    const float vl = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+    const int il = __builtin_amdgcn_readlane(id, l);
+    sl.replace(mj, vl, il);
+    sl.minimum(mv, mj);
+    live = __ballot(valid && lane > l && v > mv);
   }
 }
 
-__global__ __launch_bounds__(kST) void topk_kernel(const float *x, int V, int k, float T, int rnd, int *out) {
-  __shared__ float tv[kMaxTopK], pr[kMaxTopK];
-  __shared__ int ti[kMaxTopK];
-  __shared__ int ci[kCandCap];
-  __shared__ float cv[kCandCap];
-  __shared__ int wcount[kSW];
-  __shared__ float s_mv;
-  __shared__ int s_mj;
+/* Wave 0 over logits [lo, hi) in index order, 64 at a time (the next 64
+ * already loading) */
+template <class S>
+__device__ void scan_range(S &sl, const float *x, int lo, int hi, float &mv, int &mj) {
+  const int lane = sl.lane;
+  float nx = lo + lane < hi ? x[lo + lane] : 0.f;
+  for (int b = lo; b < hi; b += GQ_WAVE) {
+    const float v = nx;
+    nx = b + GQ_WAVE + lane < hi ? x[b + GQ_WAVE + lane] : 0.f;
+    insert_lanes(sl, b + lane < hi, v, b + lane, mv, mj);
+  }
+}
+
+struct TopkShared {
+  float tv[kMaxTopK], pr[kMaxTopK];
+  int ti[kMaxTopK];
+  int ci[kCandCap];
+  float cv[kCandCap];
+  int wn[kSW], wovf[kSW];
+  float s_mv;
+  int s_mj;
+};
+
+template <class S>
+__device__ void topk_body(S &sl, const float *x, int V, int k, float T, int rnd, int *out, TopkShared &sh) {
+  float *tv = sh.tv, *pr = sh.pr, *cv = sh.cv;
+  int *ti = sh.ti, *ci = sh.ci, *wn = sh.wn, *wovf = sh.wovf;
+  float &s_mv = sh.s_mv;
+  int &s_mj = sh.s_mj;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int j = tid; j < k; j += kST) ti[j] = j, tv[j] = x[j];
-  __syncthreads();
+  /* logits 0 .. pre-1 by wave 0 alone: the slots' first k, then in order */
+  const int pre = min(V, max(kPre, k));
   if (wave == 0) {
     float mv;
     int mj;
-    wave_min(tv, k, lane, mv, mj);
+    sl.init(x, k, lane);
+    sl.minimum(mv, mj);
+    scan_range(sl, x, k, pre, mv, mj);
     if (lane == 0) s_mv = mv, s_mj = mj;
   }
   __syncthreads();
-  /* logits k .. pre-1: chunk by chunk, each chunk's logits above the current
-   * minimum inserted in index order */
-  const int pre = min(V, max(kPre, k));
-  for (int base = k; base < pre; base += kST) {
-    const int i = base + tid;
-    const float v = i < pre ? x[i] : 0.f;
-    const int n = compact(i < pre && v > s_mv, i, v, ci, cv, 0, kCandCap, wcount);
-    if (wave == 0) {
-      float mv = s_mv;
-      int mj = s_mj;
-      insert_all(tv, ti, k, ci, cv, n, lane, mv, mj);
-      if (lane == 0) s_mv = mv, s_mj = mj;
-    }
-    __syncthreads();
-  }
-  /* the rest: everything above the minimum after `pre` logits, gathered in
-   * index order, then inserted in that order; should the list outgrow LDS
-   * (logits rising along the vocabulary), the remainder goes chunk by chunk */
+  /* the rest: each wave gathers, in index order, the logits of its own
+   * contiguous slice above the minimum after `pre` logits (the minimum only
+   * rises, so no other logit can enter a slot later); a wave whose list
+   * fills up records where it stopped */
   const float thr = s_mv;
-  int ncand = 0, stop = V;
-  for (int base0 = pre; base0 < V && stop == V; base0 += 8 * kST) {
-    float vv[8]; /* eight chunks' loads in flight at once */
+  constexpr int kCapW = kCandCap / kSW;
+  const int per = (V - pre + kSW - 1) / kSW, lo = min(V, pre + wave * per), hi = min(V, lo + per);
+  int n = 0, ovf = hi;
+  for (int b0 = lo; b0 < hi && ovf == hi; b0 += 8 * GQ_WAVE) {
+    float vv[8]; /* eight groups' loads in flight at once */
 #pragma unroll
     for (int u = 0; u < 8; u++) {
-      const int i = base0 + u * kST + tid;
-      vv[u] = i < V ? x[i] : 0.f;
+      const int i = b0 + u * GQ_WAVE + lane;
+      vv[u] = i < hi ? x[i] : 0.f;
     }
 #pragma unroll
     for (int u = 0; u < 8; u++) {
-      const int base = base0 + u * kST, i = base + tid;
-      if (stop == V && base < V) {
-        const int n = compact(i < V && vv[u] > thr, i, vv[u], ci, cv, ncand, kCandCap, wcount);
-        if (ncand + n > kCandCap)
-          stop = base; /* chunk `base` onwards not gathered */
-        else
-          ncand += n;
+      const int b = b0 + u * GQ_WAVE, i = b + lane;
+      const bool c = i < hi && vv[u] > thr;
+      const uint64_t bal = __ballot(c);
+      const int cnt = __popcll(bal);
+      if (ovf == hi && b < hi) {
+        if (n + cnt > kCapW) {
+          ovf = b;
+        } else {
+          const int at = n + __popcll(bal & ((1ull << lane) - 1ull));
+          if (c) ci[wave * kCapW + at] = i, cv[wave * kCapW + at] = vv[u];
+          n += cnt;
+        }
       }
     }
   }
+  if (lane == 0) wn[wave] = n, wovf[wave] = ovf;
+  __syncthreads();
+  /* wave 0: the gathered lists in order up to the first slice that filled
+   * up, then logit by logit from there */
   if (wave == 0) {
     float mv = s_mv;
     int mj = s_mj;
-    insert_all(tv, ti, k, ci, cv, ncand, lane, mv, mj);
-    if (lane == 0) s_mv = mv, s_mj = mj;
+    int resume = V;
+    for (int w = 0; w < kSW; w++) {
+      for (int q0 = 0; q0 < wn[w]; q0 += GQ_WAVE) {
+        const int q = q0 + lane;
+        const bool ok = q < wn[w];
+        insert_lanes(sl, ok, ok ? cv[w * kCapW + q] : 0.f, ok ? ci[w * kCapW + q] : 0, mv, mj);
+      }
+      const int whi = min(V, min(V, pre + w * per) + per);
+      if (wovf[w] < whi) {
+        resume = wovf[w];
+        break;
+      }
+    }
+    if (resume < V) scan_range(sl, x, resume, V, mv, mj);
+    sl.store(tv, ti);
   }
   __syncthreads();
-  for (int base = stop; base < V; base += kST) {
-    const int i = base + tid;
-    const float v = i < V ? x[i] : 0.f;
-    const int n = compact(i < V && v > s_mv, i, v, ci, cv, 0, kCandCap, wcount);
-    if (wave == 0) {
-      float mv = s_mv;
-      int mj = s_mj;
-      insert_all(tv, ti, k, ci, cv, n, lane, mv, mj);
-      if (lane == 0) s_mv = mv, s_mj = mj;
-    }
-    __syncthreads();
-  }
   /* temperature softmax over the slots and the draw, in the reference's
    * order (tokenizer.c:254-276) */
   if (tid == 0) {
@@ -226,6 +271,18 @@ __global__ __launch_bounds__(kST) void topk_kernel(const float *x, int V, int k,
       }
     }
     *out = ti[pick];
+  }
+}
+
+__global__ __launch_bounds__(kST) void topk_kernel(const float *x, int V, int k, float T, int rnd, int *out) {
+  __shared__ TopkShared sh;
+  if (k <= GQ_WAVE) {
+    RegSlots sl;
+    topk_body(sl, x, V, k, T, rnd, out, sh);
+  } else {
+    LdsSlots sl;
+    sl.tv = sh.tv, sl.ti = sh.ti;
+    topk_body(sl, x, V, k, T, rnd, out, sh);
   }
 }
 
