@@ -54,6 +54,10 @@ struct MvArgs {
   const float *norm_w;
   float eps;
   MvRope rope;
+  /* the same weights tile-interleaved for the matrix-core kernel
+   * (gq_launch_mm_tile), segments in order (MV_SWIGLU: gate and up in one
+   * tensor); NULL: that kernel is not used */
+  const uint8_t *mm;
 };
 
 int gq_launch_matvec(int dtype, int mode, const MvArgs &a, hipStream_t s);
@@ -62,6 +66,21 @@ int gq_launch_matvec(int dtype, int mode, const MvArgs &a, hipStream_t s);
 int gq_launch_matvec_pair(int dt0, const MvArgs &a0, int dt1, const MvArgs &a1, hipStream_t s);
 /* workgroups the matvec launcher puts on the device at most (persistent grid) */
 void gq_matvec_set_cus(int n_cu);
+
+/* Tile-interleaved copy of a Q4_K or Q6_K weight for the matrix-core matvec.
+ * For each 16-row tile T and block b, the 16 rows' block bytes are stored
+ * together (16 * block bytes), as 16-byte units ordered (chunk, row): byte o
+ * of row n's block at (o / 16) * 256 + 16 n + o % 16, and Q6_K's last two
+ * bytes (d) at 13 * 256 + 2 n.  Tile T covers rows 16T .. 16T+15 of w0 (rows
+ * past `rows` zero), or with w1 (MV_SWIGLU) rows 8T .. 8T+7 of w0 then the
+ * same rows of w1.  Bytes: gq_mm_tile_bytes. */
+size_t gq_mm_tile_bytes(int dtype, int rows, int cols, bool swiglu);
+int gq_launch_mm_tile(void *dst, int dtype, const void *w0, const void *w1, int rows, int cols, hipStream_t s);
+/* whether the matvec launcher uses the matrix-core kernel (where MvArgs.mm
+ * is set); forced: selected explicitly (gq_hip_set_matvec_path(5)), which
+ * makes the op-level entry points tile their weights per call */
+bool gq_matvec_mm_enabled();
+bool gq_matvec_mm_forced();
 
 /* ---- attention -------------------------------------------------------- */
 struct AttnArgs {

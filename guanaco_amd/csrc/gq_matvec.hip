@@ -1439,12 +1439,542 @@ __global__ __launch_bounds__(8 * GQ_WAVE) void mvr_kernel(MvArgs a, MwPlan pl) {
 }
 
 
+/* ------------------------------------------------------------------------
+ * Matrix-core matvec (v_mfma_i32_16x16x64_i8).
+ *
+ * The dot products run on the int8 matrix cores, exactly, and the VALU only
+ * unpacks quants and applies the per-sub-block scales (a third of the
+ * instructions per weight of the fp32 kernels above).
+ *
+ *  - x (times the RMSNorm weight) becomes a 22-bit fixed point per 256-value
+ *    block: x_int = rint(x * 2^e_b), e_b chosen from the block's max |x| so
+ *    |x_int| < 2^22, split into three signed base-256 digits (byte planes,
+ *    staged in LDS once per workgroup).  The error is at most 2^-23 of the
+ *    block's max |x|, below the fp32 rounding of the reference's own sums.
+ *  - An MFMA computes C[combo][row] = sum_k A[combo][k] B[k][row] over
+ *    16 weight rows (B: their quants as int8, lane (row n, k-group g)) and 16
+ *    "combos" (A: lane (combo c, k-group g) holds digit plane c%4 of x when
+ *    c/4 == g and c%4 < 3, else zeros).  Output lane (n, g) then holds, for
+ *    row n, the three plane sums of exactly the sub-block its own k-group
+ *    covers: the lane that unpacked the quants also finishes them, with the
+ *    scales it decoded, and no data crosses lanes until the row reduction.
+ *  - Plane sums are exact int32 (|sum| <= 32*15*128); the fp32 part is
+ *    (d*sc) * (s0 + 256 s1 + 65536 s2) * 2^-e_b - dmin*m*sum(x) per sub-block.
+ *  - Weights stream from a tile-interleaved copy (gq_launch_mm_tile, made
+ *    once when a model is bound): a stage is 16 rows x a chunk of the row's
+ *    blocks, one contiguous range, so every DMA instruction reads 1 KB of
+ *    consecutive bytes (row-by-row copies of the original layout with a
+ *    bank-skewing pad measured 1.6x slower), and in LDS every B read is 16
+ *    lanes x 16 consecutive bytes.  A ring of NS stages, NS-1 ahead.  Wave w owns blocks w,
+ *    w+NW, ... of every chunk and keeps their A operands (x planes) in
+ *    registers for the whole launch.
+ *  - Row partials meet in LDS per tile; the epilogues are the split-K
+ *    kernel's (store_row). */
+typedef int gq_i32x4 __attribute__((ext_vector_type(4)));
+
+struct MmPlan {
+  int nb, cb, nch;  /* blocks per row, per chunk (stage), chunks per row */
+  int bpc;          /* blocks per chunk per wave: ceil(cb / NW) */
+  int ntiles;       /* 16-row tiles over the launch (MV_SWIGLU: 8 gate + 8 up rows) */
+  int rowbytes, crb;
+  int stride;       /* LDS bytes per ring slot */
+  int ns;           /* ring slots */
+  int xs;           /* LDS offset of the waves' x slices (the last xslots ring slots) */
+  int xslots;
+  int xwb;          /* bytes of x slices per wave: 1 KB per block, twice with a norm weight */
+  int xsum, swb;    /* LDS offset of the waves' sub-block sums of x, bytes per wave */
+  int park;         /* LDS offset of the finished outputs (16 floats per tile) */
+  int total;        /* output rows (MV_SWIGLU: gate rows) */
+};
+
+/* Static LDS of the matrix-core kernel: row partials per tile, the RMSNorm
+ * partial sums, the residual ring and the RoPE row. */
+template <int NW>
+struct MmShared {
+  float red[2][16][NW];
+  float red_ss[NW];
+  float rres[kRing][16];
+  float2 scs[256];
+};
+
+__device__ __forceinline__ float gq_row16_max(float v) {
+  v = fmaxf(v, gq_dpp<0x128>(v));
+  v = fmaxf(v, gq_dpp<0x124>(v));
+  v = fmaxf(v, gq_dpp<0x4e>(v));
+  v = fmaxf(v, gq_dpp<0xb1>(v));
+  return v;
+}
+
+/* Byte r of each of four dwords, packed (v_perm: selectors 0-3 take src1's
+ * bytes, 4-7 src0's, 12 a zero byte). */
+__device__ __forceinline__ uint32_t plane4(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3, uint32_t r) {
+  const uint32_t lo = __builtin_amdgcn_perm(d1, d0, r | (4u + r) << 8 | 0x0c0c0000u);
+  const uint32_t hi = __builtin_amdgcn_perm(d3, d2, 0x0c0cu | r << 16 | (4u + r) << 24);
+  return lo | hi;
+}
+
+/* Maximum over the wave (DPP only); every lane receives it. */
+__device__ __forceinline__ float gq_wave_maxf(float v) {
+  v = gq_row16_max(v);
+  int iv = __builtin_bit_cast(int, v);
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(iv, iv, 0x142, 0xa, 0xf, false)));
+  iv = __builtin_bit_cast(int, v);
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(iv, iv, 0x143, 0xc, 0xf, false)));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+/* One wave's blocks of x -> its A operands' source.  Block ai (valid when
+ * bit ai of `valid` is set) was staged at xw + 1024 ai (the norm weight at
+ * xw + 1024 (MAXB + ai) when norm); lane L converts values 4L .. 4L+3:
+ * x (times the norm weight) -> digit planes at pw + 768 ai + 256 r, the
+ * block exponent E[ai] and the sub-block sums (SBW values each) at
+ * sw + 4 (ai * 256/SBW + sub-block).  Returns the wave's sum of raw x^2. */
+template <int SBW, int MAXB>
+__device__ __forceinline__ float mm_wave_x(GQ_LDS uint8_t *lds, uint32_t xw, uint32_t pw, uint32_t sw,
+                                           uint32_t valid, bool norm, int lane, int (&E)[MAXB]) {
+  float ss = 0.f;
+#pragma unroll
+  for (int ai = 0; ai < MAXB; ai++) {
+    E[ai] = 0;
+    if (!(valid >> ai & 1u)) continue;
+    float4 x = lld<float4>(lds, xw + 1024u * ai + 16u * lane);
+    ss = __builtin_fmaf(x.x, x.x, ss), ss = __builtin_fmaf(x.y, x.y, ss);
+    ss = __builtin_fmaf(x.z, x.z, ss), ss = __builtin_fmaf(x.w, x.w, ss);
+    if (norm) {
+      const float4 w = lld<float4>(lds, xw + 1024u * (MAXB + ai) + 16u * lane);
+      x = make_float4(x.x * w.x, x.y * w.y, x.z * w.z, x.w * w.w);
+    }
+    const float mb = gq_wave_maxf(fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w))));
+    /* mb = f 2^E, f in [0.5, 1): x 2^(22-E) stays within 2^22 in magnitude */
+    const int e = mb > 0.f ? 22 - __builtin_amdgcn_frexp_expf(mb) : 0;
+    E[ai] = e;
+    const float xv[4] = {x.x, x.y, x.z, x.w};
+    uint32_t dg[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int xi = (int)rintf(__builtin_amdgcn_ldexpf(xv[k], e));
+      /* balanced base-256 digits d0 + 256 d1 + 65536 d2, each in -128..127:
+       * the bytes of xi + 0x808080, each minus 128 */
+      dg[k] = ((uint32_t)xi + 0x808080u) ^ 0x808080u;
+    }
+#pragma unroll
+    for (uint32_t r = 0; r < 3; r++)
+      lst<uint32_t>(lds, pw + 768u * ai + 256u * r + 4u * lane, plane4(dg[0], dg[1], dg[2], dg[3], r));
+    float su = (x.x + x.y) + (x.z + x.w);
+    if (SBW == 32) {
+      su = gq_row8_sum(su);
+      if ((lane & 7) == 0) lst<float>(lds, sw + 4u * (8 * ai + (lane >> 3)), su);
+    } else {
+      su += gq_dpp<0x4e>(su);
+      su += gq_dpp<0xb1>(su);
+      if ((lane & 3) == 0) lst<float>(lds, sw + 4u * (16 * ai + (lane >> 2)), su);
+    }
+  }
+  return ss;
+}
+
+/* Q4_K block for a 16-row tile.  Lane (row n, k-group g) reads the block's
+ * header and qs[32g .. 32g+31]: low nibbles are weights 64g + i of
+ * sub-block 2g, high nibbles 64g + 32 + i of sub-block 2g+1
+ * (quant_matvec_q4_k.c:93-132).  MFMA j takes weights 64g + 16j .. +15, so
+ * A operand j holds x digits 64g + 16j .. +15 of the block; MFMAs 0, 1
+ * accumulate sub-block 2g, MFMAs 2, 3 sub-block 2g+1. */
+struct MmQ4K {
+  static constexpr int BB = 144, SBW = 32, NA = 4;
+  __device__ static uint32_t aoff(int g, int j) { return 64u * g + 16u * j; }
+  struct Frag {
+    uint4 h, q0, q1;
+  };
+  /* row n's block in the tile-interleaved layout at blk: 16-byte chunk k
+   * at 256 k + 16 n (chunk 0 the header, 1 + 2g and 2 + 2g this lane's
+   * quants): every read is 16 lanes x 16 consecutive bytes */
+  __device__ static void load(Frag &f, const GQ_LDS uint8_t *blk, int n, int g) {
+    f.h = lld<uint4>(blk, 16 * n);
+    f.q0 = lld<uint4>(blk, 256 * (1 + 2 * g) + 16 * n);
+    f.q1 = lld<uint4>(blk, 256 * (2 + 2 * g) + 16 * n);
+  }
+  /* the block's MFMAs: C sets for sub-blocks 2g and 2g+1 */
+  struct Acc {
+    gq_i32x4 c0, c1;
+  };
+  __device__ static void mma(Acc &r, const Frag &f, const gq_i32x4 (&A)[NA]) {
+    const uint4 q0 = f.q0, q1 = f.q1;
+    const int M = 0x0f0f0f0f;
+    const gq_i32x4 b0 = {(int)q0.x & M, (int)q0.y & M, (int)q0.z & M, (int)q0.w & M};
+    const gq_i32x4 b1 = {(int)q1.x & M, (int)q1.y & M, (int)q1.z & M, (int)q1.w & M};
+    const gq_i32x4 b2 = {(int)(q0.x >> 4) & M, (int)(q0.y >> 4) & M, (int)(q0.z >> 4) & M, (int)(q0.w >> 4) & M};
+    const gq_i32x4 b3 = {(int)(q1.x >> 4) & M, (int)(q1.y >> 4) & M, (int)(q1.z >> 4) & M, (int)(q1.w >> 4) & M};
+    const gq_i32x4 z = {0, 0, 0, 0};
+    r.c0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], b0, z, 0, 0, 0);
+    r.c0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[1], b1, r.c0, 0, 0, 0);
+    r.c1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2], b2, z, 0, 0, 0);
+    r.c1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[3], b3, r.c1, 0, 0, 0);
+  }
+  /* the block's contribution to row n from its plane sums */
+  __device__ static float fin(const Acc &r, const Frag &f, int g, float2 xs, int e) {
+    const uint4 h = f.h;
+    const gq_i32x4 c0 = r.c0, c1 = r.c1;
+    /* 6-bit (scale, min) of sub-blocks 2g, 2g+1 (quant_matvec_q4_k.c:47-56),
+     * both at once in bytes 0 and 1 of S and M, as in Tr<GQ_Q4_K>::dot */
+    const uint32_t sh = 16u * (uint32_t)(g & 1);
+    const bool hi = g >= 2;
+    const uint32_t y = h.y >> sh, zz = h.z >> sh, w = h.w >> sh;
+    const uint32_t mlo = hi ? 0x0f0fu : 0x3f3fu, mhi = hi ? 0x3030u : 0u;
+    const uint32_t S = ((hi ? w : y) & mlo) | ((y >> 2) & mhi);
+    const uint32_t Mm = ((hi ? (w >> 4) : zz) & mlo) | ((zz >> 2) & mhi);
+    const float d = gq_h2f(h.x), dm = gq_h2f(h.x >> 16);
+    const float s0 = __builtin_fmaf(65536.f, (float)c0.z, __builtin_fmaf(256.f, (float)c0.y, (float)c0.x));
+    const float s1 = __builtin_fmaf(65536.f, (float)c1.z, __builtin_fmaf(256.f, (float)c1.y, (float)c1.x));
+    float t = (d * (float)(S & 0xffu)) * s0;
+    t = __builtin_fmaf(d * (float)((S >> 8) & 0xffu), s1, t);
+    float r2 = __builtin_amdgcn_ldexpf(t, -e);
+    r2 = __builtin_fmaf(-(dm * (float)(Mm & 0xffu)), xs.x, r2);
+    r2 = __builtin_fmaf(-(dm * (float)((Mm >> 8) & 0xffu)), xs.y, r2);
+    return r2;
+  }
+  /* sums of sub-blocks 2g, 2g+1 of block ai among the wave's sums at sw */
+  __device__ static float2 xsums(const GQ_LDS uint8_t *lds, uint32_t sw, int ai, int g) {
+    return lld<float2>(lds, sw + 4u * (8 * ai + 2 * g));
+  }
+};
+
+
+/* Q6_K block for a 16-row tile (quant_matvec_q6_k.c:62-95: half h = 0, 1 of
+ * 128 weights; for l < 32, weight 128h + l + 32i takes the low (i = 0, 1)
+ * or high (i = 2, 3) nibble of ql[64h + l + 32(i & 1)] and bits 2i, 2i+1 of
+ * qh[32h + l], minus 32, scale sc[8h + 2i + l / 16]).  Lane (row n, k-group
+ * g) takes h = g / 2, l = 16 (g & 1) .. +15: MFMA j covers weights
+ * 128h + 32j + l, one 16-weight sub-block (8h + 2j + (g & 1)) each, into a
+ * C set of its own.  In the tile-interleaved layout the block's chunks are
+ * ql 0..7, qh 8..11, scales 12, and the 16 rows' d at 13 * 256 + 2n. */
+struct MmQ6K {
+  static constexpr int BB = 210, SBW = 16, NA = 4;
+  __device__ static uint32_t aoff(int g, int j) { return 128u * (g >> 1) + 32u * j + 16u * (g & 1); }
+  struct Frag {
+    uint4 a, b, h, sc;
+    uint32_t d;
+  };
+  __device__ static void load(Frag &f, const GQ_LDS uint8_t *blk, int n, int g) {
+    const int h = g >> 1, o = g & 1;
+    f.a = lld<uint4>(blk, 256 * (4 * h + o) + 16 * n);
+    f.b = lld<uint4>(blk, 256 * (4 * h + 2 + o) + 16 * n);
+    f.h = lld<uint4>(blk, 256 * (8 + 2 * h + o) + 16 * n);
+    f.sc = lld<uint4>(blk, 256 * 12 + 16 * n);
+    f.d = lld<uint16_t>(blk, 256 * 13 + 2 * n);
+  }
+  struct Acc {
+    gq_i32x4 c[4];
+  };
+  __device__ static void mma(Acc &r, const Frag &f, const gq_i32x4 (&A)[NA]) {
+    const uint32_t A4[4] = {f.a.x, f.a.y, f.a.z, f.a.w}, B4[4] = {f.b.x, f.b.y, f.b.z, f.b.w};
+    const uint32_t H4[4] = {f.h.x, f.h.y, f.h.z, f.h.w};
+    int u[4][4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const uint32_t M = 0x0f0f0f0fu, Q = 0x30303030u;
+      u[0][k] = (int)((A4[k] & M) | ((H4[k] << 4) & Q));
+      u[1][k] = (int)((B4[k] & M) | ((H4[k] << 2) & Q));
+      u[2][k] = (int)(((A4[k] >> 4) & M) | (H4[k] & Q));
+      u[3][k] = (int)(((B4[k] >> 4) & M) | ((H4[k] >> 2) & Q));
+    }
+    const gq_i32x4 z = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const gq_i32x4 b = {u[j][0], u[j][1], u[j][2], u[j][3]};
+      r.c[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[j], b, z, 0, 0, 0);
+    }
+  }
+  __device__ static float fin(const Acc &r, const Frag &f, int g, float4 xs, int e) {
+    /* scales sc[8h + 2j + (g & 1)], j = 0..3: bytes (g & 1) + 2j of the
+     * half's 8 (dwords 2h, 2h + 1 of the 16 scale bytes) */
+    const uint32_t s0 = (g >> 1) ? f.sc.z : f.sc.x, s1 = (g >> 1) ? f.sc.w : f.sc.y;
+    const uint32_t sh = 8u * (uint32_t)(g & 1);
+    const float xsj[4] = {xs.x, xs.y, xs.z, xs.w};
+    const uint32_t sw[4] = {s0 >> sh, s0 >> (sh + 16), s1 >> sh, s1 >> (sh + 16)};
+    float t = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const gq_i32x4 c = r.c[j];
+      const float sj = __builtin_fmaf(65536.f, (float)c.z, __builtin_fmaf(256.f, (float)c.y, (float)c.x));
+      /* sum (u - 32) x = sum u x - 32 sum x */
+      const float v = __builtin_fmaf(-32.f, xsj[j], __builtin_amdgcn_ldexpf(sj, -e));
+      t = __builtin_fmaf((float)(int8_t)(sw[j] & 0xffu), v, t);
+    }
+    return gq_h2f(f.d) * t;
+  }
+  /* sums of sub-blocks 8h + (g & 1) + 2j, j = 0..3, of block ai */
+  __device__ static float4 xsums(const GQ_LDS uint8_t *lds, uint32_t sw, int ai, int g) {
+    const uint32_t o = sw + 4u * (16 * ai + 8 * (g >> 1));
+    const float4 p = lld<float4>(lds, o), q = lld<float4>(lds, o + 16);
+    return (g & 1) ? make_float4(p.y, p.w, q.y, q.w) : make_float4(p.x, p.z, q.x, q.z);
+  }
+};
+
+template <int DT>
+struct MmTr;
+template <>
+struct MmTr<GQ_Q4_K> {
+  using type = MmQ4K;
+  typedef float2 XS;
+};
+template <>
+struct MmTr<GQ_Q6_K> {
+  using type = MmQ6K;
+  typedef float4 XS;
+};
+
+/* This wave's DMA instructions for stage (tile t, chunk c): cb blocks of
+ * the tile-interleaved tensor, one contiguous range (16 * BB * cb bytes)
+ * into ring slot `buf` in 1 KB instructions; for MV_RESID with c == 0 also
+ * the tile's residual values into rbuf.  Returns their count. */
+template <int MODE, int NW, int BB>
+__device__ __forceinline__ int mm_issue(const MvArgs &a, const MmPlan &pl, int t, int c, GQ_LDS uint8_t *buf,
+                                        GQ_LDS float *rbuf, int wave, int lane) {
+  const int sb = 16 * BB * pl.cb;
+  copy_range(a.mm + ((size_t)t * pl.nb + (size_t)c * pl.cb) * (16 * BB), sb, buf, wave, lane, NW);
+  int cnt = copy_count(sb, wave, NW);
+  if (MODE == MV_RESID && c == 0 && wave == NW - 1) {
+    int s, lr0;
+    locate(a, 16 * t, s, lr0);
+    const int last = a.seg[s].rows - 1;
+    const uint32_t d = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)rbuf);
+    if (lane < 16) dma4(a.seg[s].r + min(lr0 + lane, last), d);
+    cnt++;
+  }
+  return cnt;
+}
+
+template <int DT, int MODE, int NW, int MAXB, int NS>
+__global__ __launch_bounds__(NW * GQ_WAVE) void mvm_kernel(MvArgs a, MmPlan pl) {
+  using T = typename MmTr<DT>::type;
+  static_assert(NS >= 3, "ring of NS stage slots, NS - 1 stages in flight");
+  constexpr int MAXU = 1024 / (NW * GQ_WAVE); /* 256-value blocks of x per thread row (cols <= 16384) */
+  __shared__ MmShared<NW> sh;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  GQ_LDS uint8_t *lds = (GQ_LDS uint8_t *)smem;
+  GQ_LDS float *lres = (GQ_LDS float *)&sh.rres[0][0];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  const int bid = blockIdx.x, nblk = gridDim.x;
+  const int mytiles = bid < pl.ntiles ? (pl.ntiles - 1 - bid) / nblk + 1 : 0;
+  const int nst = mytiles * pl.nch;
+  auto issue = [&](int q) -> int { /* stage q into slot q % NS */
+    const int tl = q / pl.nch;
+    return mm_issue<MODE, NW, T::BB>(a, pl, bid + tl * nblk, q - tl * pl.nch, lds + (q % NS) * pl.stride,
+                                     lres + (tl % kRing) * 16, wave, lane);
+  };
+
+  /* This wave's blocks: ai = c * bpc + s is block c*cb + wave + s*NW.  Its
+   * slices of x (and of the norm weight) go by DMA to the wave's own area
+   * in the last pl.xslots ring slots, ahead of the stages whose slots they
+   * leave free; each wave converts its own blocks there, so the prologue
+   * has no barrier (the RMSNorm sum of squares crosses the loop's first
+   * one, before which no stage lands in those slots). */
+  uint32_t valid = 0;
+  int blk[MAXB];
+#pragma unroll
+  for (int ai = 0; ai < MAXB; ai++) {
+    const int c = ai / pl.bpc, s = ai - c * pl.bpc;
+    const int bl = wave + s * NW;
+    blk[ai] = c * pl.cb + bl;
+    if (c < pl.nch && bl < pl.cb) valid |= 1u << ai;
+  }
+  const bool norm = a.norm_w != nullptr;
+  /* the digit planes of block ai overwrite the wave's x slice of block ai
+   * once it is read (768 <= 1024 bytes per block) */
+  const uint32_t xw = pl.xs + wave * pl.xwb, pw = xw, sw = pl.xsum + wave * pl.swb;
+#pragma unroll
+  for (int ai = 0; ai < MAXB; ai++) {
+    if (!(valid >> ai & 1u)) continue;
+    const uint32_t base = (uint32_t)(uintptr_t)lds;
+    dma16(a.x + 256 * blk[ai] + 4 * lane, __builtin_amdgcn_readfirstlane(base + xw + 1024u * ai));
+    if (norm)
+      dma16(a.norm_w + 256 * blk[ai] + 4 * lane, __builtin_amdgcn_readfirstlane(base + xw + 1024u * (MAXB + ai)));
+  }
+  int pos = 0;
+  if (MODE == MV_STORE && a.rope.cs) {
+    pos = a.rope.pos_dev ? gq_sld<int>(a.rope.pos_dev) : a.rope.pos;
+    const int hd = a.rope.head_dim;
+    if (wave == 0 && pos >= 0 && pos < a.rope.max_seq) {
+      const float *crow = (const float *)(a.rope.cs + (size_t)pos * (hd >> 1));
+      const uint32_t b = (uint32_t)(uintptr_t)(GQ_LDS float2 *)sh.scs;
+      for (int o = 0; o < hd; o += 64)
+        if (lane < hd - o) dma4(crow + o + lane, __builtin_amdgcn_readfirstlane(b + 4u * o));
+    }
+  }
+  /* cnt[j]: this wave's DMA instructions of stage k + j at the top of
+   * iteration k, j = 0 .. NS-2; stages npre .. NS-2 land in x's slots and go
+   * out after the loop's first barrier */
+  int cnt[NS - 1];
+  const int npre = NS - pl.xslots;
+  int issued = 0, sum = 0;
+#pragma unroll
+  for (int j = 0; j < NS - 1; j++) {
+    cnt[j] = 0;
+    if (j < npre && j < nst) cnt[j] = issue(j), issued = j + 1;
+    sum += cnt[j];
+  }
+  /* VMEM loads complete in issue order: with only the stages' copies
+   * outstanding, this wave's x slices have landed */
+  wait_vmcnt(sum);
+  int E[MAXB];
+  float ss = mm_wave_x<T::SBW, MAXB>(lds, xw, pw, sw, valid, norm, lane, E);
+  ss = gq_wave_total(ss);
+  if (lane == 0) sh.red_ss[wave] = ss;
+  /* A operands (x digit planes), sub-block sums and exponents stay in
+   * registers for the whole launch (the wave's LDS writes above are ordered
+   * before these reads) */
+  gq_i32x4 A[MAXB][T::NA];
+  typename MmTr<DT>::XS X[MAXB];
+  const bool nz = (n >> 2) == g && (n & 3) < 3;
+#pragma unroll
+  for (int ai = 0; ai < MAXB; ai++) {
+    const uint32_t po = pw + 768u * ai + 256u * (uint32_t)(n & 3);
+#pragma unroll
+    for (int j = 0; j < T::NA; j++) {
+      gq_i32x4 v = {0, 0, 0, 0};
+      if (nz && (valid >> ai & 1u)) v = lld<gq_i32x4>(lds, po + T::aoff(g, j));
+      A[ai][j] = v;
+    }
+    X[ai] = T::xsums(lds, sw, (valid >> ai & 1u) ? ai : 0, g);
+  }
+  float rscale = 1.f;
+  bool have_rscale = !norm;
+
+  /* Iteration k: wait for stage k, one barrier (stage k landed for every
+   * wave, and every wave is done with stage k-1, whose slot stage k+NS-1
+   * then takes), finish the tile completed at k-1 into the parking area,
+   * compute stage k.  Outputs are stored after the loop: a store inside it
+   * would hold up the next wait on the vector memory counter. */
+  GQ_LDS float *park = (GQ_LDS float *)(lds + pl.park);
+  const bool full = pl.nch == 1 && valid == (1u << MAXB) - 1u;
+  constexpr int RPW = 16 / NW; /* rows of a finished tile each wave completes */
+  float acc = 0.f;
+  for (int k = 0; k <= nst; k++) {
+    if (k < nst) {
+      int pend = 0;
+#pragma unroll
+      for (int j = 1; j < NS - 1; j++) pend += cnt[j];
+      wait_vmcnt(pend);
+    }
+    __syncthreads();
+    if (k < nst) {
+      /* stages up to k + NS - 1 (the first iteration also those x held
+       * back), into the slots of stages already computed */
+#pragma unroll
+      for (int j = 0; j < NS - 2; j++) cnt[j] = cnt[j + 1];
+      cnt[NS - 2] = 0;
+#pragma unroll
+      for (int j = 1; j < NS; j++) {
+        const int q = k + j;
+        if (q < nst && q >= issued && j <= NS - 1) {
+          cnt[j - 1] += issue(q);
+          issued = q + 1;
+        }
+      }
+    }
+    const int c = k < nst ? k % pl.nch : 0;
+    if (!have_rscale) { /* 1/sqrt(mean(x^2) + eps) (kernels_cpu.c:242-253) */
+      float tot = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; w++) tot += sh.red_ss[w];
+      tot = tot / (float)a.cols;
+      tot = tot + a.eps;
+      rscale = 1.0f / sqrtf(tot);
+      have_rscale = true;
+    }
+    if (k > 0 && c == 0 && lane < RPW) { /* rows of the tile completed at k-1 */
+      const int tl = (k - 1) / pl.nch, r = wave * RPW + lane;
+      if (MODE != MV_SWIGLU || r < 8) {
+        const int tp = MODE == MV_SWIGLU ? r + 8 : r ^ 1;
+        float v = 0.f, w = 0.f;
+#pragma unroll
+        for (int j = 0; j < NW; j++) v += sh.red[tl & 1][r][j], w += sh.red[tl & 1][tp][j];
+        v *= rscale, w *= rscale;
+        float out = v;
+        {
+#pragma clang fp contract(off)
+          if (MODE == MV_SWIGLU) {
+            out = silu_mul(v, w);
+          } else if (MODE == MV_RESID) {
+            out = v + sh.rres[tl % kRing][r];
+          } else if (a.rope.cs) {
+            int s, lr0;
+            locate(a, 16 * (bid + tl * nblk), s, lr0);
+            const int kind = a.seg[s].kind;
+            if (kind == SEG_ROPE || kind == SEG_ROPE_KV) {
+              /* adjacent pair rotated by the row of pos
+               * (kernels_cpu.c:415-429); tiles start on even rows */
+              const int d = (lr0 + r) % a.rope.head_dim;
+              const float2 cs = sh.scs[d >> 1];
+              const float x0 = (r & 1) ? w : v, x1 = (r & 1) ? v : w;
+              out = (r & 1) ? x0 * cs.y + x1 * cs.x : x0 * cs.x - x1 * cs.y;
+            }
+          }
+        }
+        park[16 * tl + r] = out;
+      }
+    }
+    if (k == nst) break;
+    /* every LDS read of the stage first, then every MFMA, then the
+     * epilogues: one basic block when the launch has one chunk and every
+     * block slot of the wave is used (uniform: all waves take it) */
+    const GQ_LDS uint8_t *buf = lds + (k % NS) * pl.stride;
+    typename T::Frag f[MAXB];
+    typename T::Acc r[MAXB];
+    if (full) {
+#pragma unroll
+      for (int ai = 0; ai < MAXB; ai++) T::load(f[ai], buf + blk[ai] * (16 * T::BB), n, g);
+#pragma unroll
+      for (int ai = 0; ai < MAXB; ai++) T::mma(r[ai], f[ai], A[ai]);
+#pragma unroll
+      for (int ai = 0; ai < MAXB; ai++) acc += T::fin(r[ai], f[ai], g, X[ai], E[ai]);
+    } else {
+#pragma unroll
+      for (int ai = 0; ai < MAXB; ai++)
+        if (ai / pl.bpc == c && (valid >> ai & 1u)) T::load(f[ai], buf + (blk[ai] - c * pl.cb) * (16 * T::BB), n, g);
+#pragma unroll
+      for (int ai = 0; ai < MAXB; ai++)
+        if (ai / pl.bpc == c && (valid >> ai & 1u)) {
+          T::mma(r[ai], f[ai], A[ai]);
+          acc += T::fin(r[ai], f[ai], g, X[ai], E[ai]);
+        }
+    }
+    if (c == pl.nch - 1) { /* the tile's last chunk: reduce over the k-groups */
+      float v = acc;
+      v += __shfl_xor(v, 16, 64);
+      v += __shfl_xor(v, 32, 64);
+      if (lane < 16) sh.red[(k / pl.nch) & 1][lane][wave] = v;
+      acc = 0.f;
+    }
+  }
+  __syncthreads();
+  /* the parked rows go out */
+  const int prow = MODE == MV_SWIGLU ? 8 : 16;
+  for (int i = threadIdx.x; i < mytiles * 16; i += NW * GQ_WAVE) {
+    const int tl = i >> 4, r = i & 15, t = bid + tl * nblk;
+    if (r >= prow) continue;
+    int s = 0, lr = 8 * t + r;
+    if (MODE != MV_SWIGLU) {
+      locate(a, 16 * t, s, lr);
+      lr += r;
+      if (lr >= a.seg[s].rows) continue;
+    } else if (lr >= pl.total) {
+      continue;
+    }
+    float *dst = rdest<MODE>(a, s, lr, pos);
+    if (dst) gst<float>(dst, park[i]);
+  }
+}
+
 int g_n_cu = 256;
 int g_wg_per_cu = 4;
 constexpr size_t kMaxDynLds = 144 * 1024;
 constexpr size_t kMaxDynLdsW = 152 * 1024;
 /* matvec kernels: 0 register path, 1 split-K LDS, 2 wave-private LDS ring,
- * 3 register ring (each where it fits, falling back down the list), 4 auto */
+ * 3 register ring, 5 matrix cores (each where it fits, falling back down the
+ * list), 4 auto */
 int g_use_lds = 4;
 
 template <int DT, int MODE, int R>
@@ -1669,6 +2199,122 @@ int launch_reg(const MvArgs &a, int total, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
+/* Plan and launch the matrix-core kernel; returns 1 when the shape does not
+ * fit it (a dtype without int8 traits, segments a 16-row tile would
+ * straddle, rows not a multiple of 16 bytes, or x not fitting the ring's
+ * last slot during the prologue). */
+int g_mm_waves = 8;          /* waves per workgroup: 4 or 8 */
+int g_mm_ns = 3;             /* ring slots: 3, 4 or 6 */
+int g_mm_stage_cap = 40960;  /* bytes of weights per stage at most */
+
+template <int DT, int MODE, int NW, int MAXB, int NS>
+int launch_mm_as(const MvArgs &a, const MmPlan &pl, size_t lds, int grid, hipStream_t s) {
+  static bool attr_set = false;
+  auto f = mvm_kernel<DT, MODE, NW, MAXB, NS>;
+  if (!attr_set) {
+    (void)hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLdsW);
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(f, dim3(grid), dim3(NW * GQ_WAVE), lds, s, a, pl);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+template <int DT, int MODE, int NW, int NS>
+int launch_mm_b(int maxb, const MvArgs &a, const MmPlan &pl, size_t lds, int grid, hipStream_t s) {
+  if (maxb <= 1) return launch_mm_as<DT, MODE, NW, 1, NS>(a, pl, lds, grid, s);
+  if (maxb <= 2) return launch_mm_as<DT, MODE, NW, 2, NS>(a, pl, lds, grid, s);
+  return launch_mm_as<DT, MODE, NW, 4, NS>(a, pl, lds, grid, s);
+}
+
+template <int DT, int MODE, int NW>
+int launch_mm_w(const MvArgs &a, int total, hipStream_t s) {
+  using T = typename MmTr<DT>::type;
+  MmPlan pl;
+  pl.nb = a.cols / 256;
+  pl.rowbytes = pl.nb * T::BB;
+  if (MODE == MV_STORE && a.rope.cs && a.rope.head_dim > 512) return 1; /* the RoPE row holds 256 pairs */
+  if (MODE != MV_SWIGLU && a.nseg > 1)
+    for (int i = 0; i < a.nseg; i++)
+      if (a.seg[i].rows % 16) return 1;
+  /* blocks per stage: the whole row when 16 rows fit the cap, else the
+   * largest divisor of the row's blocks that fits */
+  int cb = pl.nb;
+  while (cb > 1 && (16 * cb * T::BB > g_mm_stage_cap || pl.nb % cb)) cb--;
+  pl.cb = cb;
+  pl.crb = cb * T::BB;
+  pl.nch = pl.nb / cb;
+  pl.bpc = (cb + NW - 1) / NW;
+  const int maxb = pl.nch * pl.bpc;
+  if (maxb > 4) return 1; /* eight blocks of A operands per wave spill registers */
+  pl.stride = (16 * pl.crb + 255) / 256 * 256;
+  /* the waves' x slices in the ring's last slots; after the ring their
+   * sub-block sums, then the parked outputs */
+  const int mb2 = maxb <= 1 ? 1 : maxb <= 2 ? 2 : 4; /* the kernel's MAXB */
+  pl.xwb = 1024 * mb2 * (a.norm_w ? 2 : 1);
+  pl.xslots = (NW * pl.xwb + pl.stride - 1) / pl.stride;
+  const int ns = std::max(g_mm_ns >= 6 ? 6 : g_mm_ns == 4 ? 4 : 3, pl.xslots + 1);
+  if (ns > 6) return 1;
+  pl.ns = ns;
+  pl.xs = (ns - pl.xslots) * pl.stride;
+  pl.swb = 4 * mb2 * (256 / T::SBW);
+  pl.xsum = ns * pl.stride;
+  pl.park = pl.xsum + NW * pl.swb;
+  pl.total = total;
+  pl.ntiles = MODE == MV_SWIGLU ? (total + 7) / 8 : (total + 15) / 16;
+  /* workgroups per CU from LDS, then the grid; the parking area holds
+   * every tile a workgroup finishes */
+  const size_t shb = sizeof(MmShared<NW>);
+  int grid = 0;
+  size_t lds = 0;
+  for (int pc = 2; pc >= 1 && !grid; pc--) {
+    const int gr = std::min(pl.ntiles, pc * g_n_cu);
+    const size_t l = (size_t)pl.park + 64 * (size_t)((pl.ntiles + gr - 1) / gr);
+    if (l <= kMaxDynLdsW && pc * (l + shb + 1024) <= 160 * 1024) grid = gr, lds = l;
+  }
+  if (!grid) return 1;
+  if (ns == 3) return launch_mm_b<DT, MODE, NW, 3>(maxb, a, pl, lds, grid, s);
+  if (ns == 4) return launch_mm_b<DT, MODE, NW, 4>(maxb, a, pl, lds, grid, s);
+  return launch_mm_b<DT, MODE, NW, 6>(maxb, a, pl, lds, grid, s);
+}
+
+template <int DT, int MODE>
+int launch_mm(const MvArgs &a, int total, hipStream_t s) {
+  if constexpr (DT != GQ_Q4_K && DT != GQ_Q6_K) {
+    return 1;
+  } else {
+    if (!a.mm) return 1;
+    return g_mm_waves >= 8 ? launch_mm_w<DT, MODE, 8>(a, total, s) : launch_mm_w<DT, MODE, 4>(a, total, s);
+  }
+}
+
+/* ---------------------------------------------------------------- tiling */
+__global__ void mm_tile_kernel(uint8_t *dst, const uint8_t *w0, const uint8_t *w1, int rows, int nb, int bb,
+                               long long units) {
+  /* one thread per (tile, block, row n) */
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= units) return;
+  const int n = (int)(i & 15);
+  const long long tb = i >> 4, tile = tb / nb;
+  const int b = (int)(tb - tile * nb);
+  const uint8_t *src;
+  int row;
+  if (w1) {
+    row = 8 * (int)tile + (n & 7);
+    src = n < 8 ? w0 : w1;
+  } else {
+    row = 16 * (int)tile + n;
+    src = w0;
+  }
+  uint8_t *out = dst + (size_t)tb * 16 * bb;
+  const uint16_t *in = (const uint16_t *)(src + ((size_t)row * nb + b) * bb); /* blocks are 2-byte aligned */
+  const bool ok = row < rows;
+  for (int o = 0; o < bb; o += 2) {
+    const uint16_t v = ok ? in[o >> 1] : (uint16_t)0;
+    const int at = o < 208 ? (o >> 4) * 256 + 16 * n + (o & 15) : 13 * 256 + 2 * n + (o - 208);
+    *(uint16_t *)(out + at) = v;
+  }
+}
+
 template <int DT, int MODE>
 int launch_dm(const MvArgs &a, hipStream_t s) {
   int total = 0;
@@ -1693,6 +2339,14 @@ int launch_dm(const MvArgs &a, hipStream_t s) {
         if (a.seg[i].rows % 4) return -1;
   }
   if (total <= 0) return -1;
+  /* the matrix-core kernel: selected explicitly (5), or by auto (4) for the
+   * launches it measured faster on: gate/up + SwiGLU and the LM head (8B
+   * shape: 16.1 vs 20.3 us and 88 vs 108 us); the split-K kernel stays
+   * faster for q/k/v (10.0 vs 12.1 us), o and down */
+  if (g_use_lds == 5 || (g_use_lds == 4 && (MODE == MV_SWIGLU || (MODE == MV_STORE && total >= 16384)))) {
+    const int rc = launch_mm<DT, MODE>(a, total, s);
+    if (rc <= 0) return rc;
+  }
   if (g_use_lds == 3) {
     const int rc = launch_reg<DT, MODE>(a, total, s);
     if (rc <= 0) return rc;
@@ -1732,7 +2386,7 @@ void gq_matvec_set_cus(int n_cu) {
    * persistent grid (0 = one workgroup per row group); default 4 */
   if (const char *e = getenv("GQ_MV_WG_PER_CU")) g_wg_per_cu = atoi(e);
   /* GQ_MV_LDS=0: register-path kernel only (same as gq_hip_set_matvec_path(0)) */
-  if (const char *e = getenv("GQ_MV_LDS")) g_use_lds = std::min(std::max(atoi(e), 0), 4);
+  if (const char *e = getenv("GQ_MV_LDS")) g_use_lds = std::min(std::max(atoi(e), 0), 5);
   /* wave-private kernel: rows per group (GQ_MV_RW, 2 or 4) and waves per
    * workgroup (GQ_MV_WAVES, 4..16; 0 = chosen per shape) */
   if (const char *e = getenv("GQ_MV_RW")) g_mw_rw = atoi(e) >= 4 ? 4 : 2;
@@ -1746,11 +2400,38 @@ void gq_matvec_set_cus(int n_cu) {
   if (const char *e = getenv("GQ_MV_LDS_WG")) g_lds_wg_per_cu = std::max(atoi(e), 0);
   /* GQ_MV_XL: x through LDS in the split-K kernel (-1 auto, 0 never, 1 when it fits) */
   if (const char *e = getenv("GQ_MV_XL")) g_mv_xl = std::min(std::max(atoi(e), -1), 1);
+  /* matrix-core kernel: waves per workgroup (GQ_MM_WAVES, 4 or 8), ring
+   * slots (GQ_MM_NS, 3, 4 or 6) and bytes of weights per stage
+   * (GQ_MM_STAGE_BYTES, at most 64 KB) */
+  if (const char *e = getenv("GQ_MM_WAVES")) g_mm_waves = atoi(e) >= 8 ? 8 : 4;
+  if (const char *e = getenv("GQ_MM_NS")) g_mm_ns = atoi(e);
+  if (const char *e = getenv("GQ_MM_STAGE_BYTES")) g_mm_stage_cap = std::min(std::max(atoi(e), 2048), 65536);
+}
+
+bool gq_matvec_mm_enabled() { return g_use_lds == 5; }  /* every launch with a tiled copy */
+bool gq_matvec_mm_forced() { return g_use_lds == 5; }
+
+size_t gq_mm_tile_bytes(int dtype, int rows, int cols, bool swiglu) {
+  const int bb = dtype == GQ_Q4_K ? 144 : dtype == GQ_Q6_K ? 210 : 0;
+  if (!bb || cols % 256) return 0;
+  const size_t tiles = swiglu ? (rows + 7) / 8 : (rows + 15) / 16;
+  return tiles * (cols / 256) * 16 * bb;
+}
+
+int gq_launch_mm_tile(void *dst, int dtype, const void *w0, const void *w1, int rows, int cols, hipStream_t s) {
+  const int bb = dtype == GQ_Q4_K ? 144 : dtype == GQ_Q6_K ? 210 : 0;
+  if (!bb || !dst || !w0 || rows <= 0 || cols <= 0 || cols % 256) return -1;
+  const int nb = cols / 256;
+  const long long tiles = w1 ? (rows + 7) / 8 : (rows + 15) / 16;
+  const long long units = tiles * nb * 16;
+  hipLaunchKernelGGL(mm_tile_kernel, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, s, (uint8_t *)dst,
+                     (const uint8_t *)w0, (const uint8_t *)w1, rows, nb, bb, units);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
 extern "C" int gq_hip_set_matvec_path(int path) {
   const int prev = g_use_lds;
-  if (path >= 0 && path <= 4) g_use_lds = path;
+  if (path >= 0 && path <= 5) g_use_lds = path;
   return prev;
 }
 

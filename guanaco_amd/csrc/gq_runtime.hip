@@ -70,6 +70,16 @@ struct gq_ctx {
   bool bound = false;
   gq_model m{};
   std::vector<gq_layer> layers;
+  /* tile-interleaved copies of the bound model's Q4_K/Q6_K weights for the
+   * matrix-core matvec (gq_launch_mm_tile), owned by the context: per layer
+   * the q/k/v groups of op_qkv (same dtype, in order), o, gate+up, down;
+   * NULL where a weight does not take that layout */
+  struct MmLayer {
+    const uint8_t *qkv[3] = {nullptr, nullptr, nullptr};
+    const uint8_t *o = nullptr, *gu = nullptr, *down = nullptr;
+  };
+  std::vector<MmLayer> mm;
+  const uint8_t *mm_lm = nullptr;
   Workspace ws;
   PrefillWs pf;
   SampleWs sw;
@@ -275,13 +285,29 @@ static int check_mv(gq_ctx *c, int dtype, const void *w, int rows, int cols, siz
 }
 
 static int launch_one_mv(gq_ctx *c, int dtype, const void *w, int rows, int cols, const float *x,
-                         float *y) {
+                         float *y, const uint8_t *mm = nullptr) {
   MvArgs a{};
   a.seg[0] = MvSeg{(const uint8_t *)w, y, nullptr, rows};
   a.nseg = 1;
   a.cols = cols;
   a.x = x;
+  a.mm = mm;
   return gq_launch_matvec(dtype, MV_STORE, a, c->stream);
+}
+
+/* The op-level entry points take weights in the reference layout; with the
+ * matrix-core kernel selected explicitly (path 5) they tile a copy for the
+ * call (freed by the caller with gq_hip_free after the stream is done). */
+static const uint8_t *op_tile(gq_ctx *c, int dtype, const void *w, int rows, int cols) {
+  if (!gq_matvec_mm_forced() || (dtype != GQ_Q4_K && dtype != GQ_Q6_K)) return nullptr;
+  const size_t bytes = gq_mm_tile_bytes(dtype, rows, cols, false);
+  if (!bytes) return nullptr;
+  uint8_t *d = (uint8_t *)dev_alloc(c, bytes);
+  if (d && gq_launch_mm_tile(d, dtype, w, nullptr, rows, cols, c->stream)) {
+    gq_hip_free(c, d);
+    return nullptr;
+  }
+  return d;
 }
 
 extern "C" int gq_hip_matvec(gq_ctx *c, int dtype, const void *w, int rows, int cols,
@@ -302,7 +328,9 @@ extern "C" int gq_hip_matvec(gq_ctx *c, int dtype, const void *w, int rows, int 
     c->sy = p, c->sy_cap = rows;
   }
   HIPCHK(c, hipMemcpyAsync(c->sx, x, sizeof(float) * cols, hipMemcpyHostToDevice, c->stream));
-  rc = launch_one_mv(c, dtype, w, rows, cols, c->sx, c->sy);
+  const uint8_t *mm = op_tile(c, dtype, w, rows, cols);
+  rc = launch_one_mv(c, dtype, w, rows, cols, c->sx, c->sy, mm);
+  if (mm) gq_hip_free(c, (void *)mm);
   if (rc) return fail(c, rc, "matvec launch failed");
   HIPCHK(c, hipMemcpyAsync(y, c->sy, sizeof(float) * rows, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));
@@ -314,7 +342,9 @@ extern "C" int gq_hip_matvec_dev(gq_ctx *c, int dtype, const void *w, int rows, 
   if (!c) return -1;
   int rc = check_mv(c, dtype, w, rows, cols, 0, x, y);
   if (rc) return rc;
-  rc = launch_one_mv(c, dtype, w, rows, cols, x, y);
+  const uint8_t *mm = op_tile(c, dtype, w, rows, cols);
+  rc = launch_one_mv(c, dtype, w, rows, cols, x, y, mm);
+  if (mm) gq_hip_free(c, (void *)mm);
   return rc ? fail(c, rc, "matvec launch failed") : 0;
 }
 
@@ -580,6 +610,68 @@ static int check_weight(gq_ctx *c, const gq_weight &w, int rows, int cols, const
   return 0;
 }
 
+static bool mm_tileable(const gq_weight &w) {
+  return (w.dtype == GQ_Q4_K || w.dtype == GQ_Q6_K) && w.cols % 256 == 0 && w.rows > 0;
+}
+
+/* One tile-interleaved tensor for the weights ws[0..n) (stacked in order,
+ * each rows % 16 == 0 when n > 1), or for gate and up together (swiglu);
+ * NULL when they do not take the layout or memory runs out. */
+static const uint8_t *mm_build(gq_ctx *c, const gq_weight *const *ws, int n, bool swiglu) {
+  size_t bytes = 0;
+  for (int i = 0; i < n; i++) {
+    if (!mm_tileable(*ws[i]) || ws[i]->dtype != ws[0]->dtype || ws[i]->cols != ws[0]->cols) return nullptr;
+    if (n > 1 && !swiglu && ws[i]->rows % 16) return nullptr;
+  }
+  if (swiglu) {
+    if (n != 2 || ws[0]->rows != ws[1]->rows) return nullptr;
+    bytes = gq_mm_tile_bytes(ws[0]->dtype, ws[0]->rows, ws[0]->cols, true);
+  } else {
+    for (int i = 0; i < n; i++) bytes += gq_mm_tile_bytes(ws[i]->dtype, ws[i]->rows, ws[i]->cols, false);
+  }
+  uint8_t *d = (uint8_t *)dev_alloc(c, bytes);
+  if (!d) return nullptr;
+  if (swiglu) {
+    if (gq_launch_mm_tile(d, ws[0]->dtype, ws[0]->data, ws[1]->data, ws[0]->rows, ws[0]->cols, c->stream)) return nullptr;
+    return d;
+  }
+  size_t off = 0;
+  for (int i = 0; i < n; i++) {
+    if (gq_launch_mm_tile(d + off, ws[i]->dtype, ws[i]->data, nullptr, ws[i]->rows, ws[i]->cols, c->stream))
+      return nullptr;
+    off += gq_mm_tile_bytes(ws[i]->dtype, ws[i]->rows, ws[i]->cols, false);
+  }
+  return d;
+}
+
+static void mm_free(gq_ctx *c) {
+  auto rel = [&](const uint8_t *&p) {
+    if (p) gq_hip_free(c, (void *)p);
+    p = nullptr;
+  };
+  for (auto &L : c->mm) {
+    for (auto &q : L.qkv) rel(q);
+    rel(L.o), rel(L.gu), rel(L.down);
+  }
+  c->mm.clear();
+  rel(c->mm_lm);
+}
+
+/* The q/k/v groups of one launch each (same dtype, in order q, k, v). */
+static int qkv_groups(const gq_layer &L, const gq_weight *grp[3][3], int nin[3]) {
+  const gq_weight *W[3] = {&L.wq, &L.wk, &L.wv};
+  bool done[3] = {false, false, false};
+  int ng = 0;
+  for (int i = 0; i < 3; i++) {
+    if (done[i]) continue;
+    nin[ng] = 0;
+    for (int j = i; j < 3; j++)
+      if (!done[j] && W[j]->dtype == W[i]->dtype) grp[ng][nin[ng]++] = W[j], done[j] = true;
+    ng++;
+  }
+  return ng;
+}
+
 extern "C" int gq_hip_model_bind(gq_ctx *c, const gq_model *m) {
   if (!c || !m || !m->layers) return fail(c, -1, "model_bind: NULL");
   if (!c->kslab) return fail(c, -1, "model_bind: call gq_hip_kv_init first");
@@ -608,6 +700,26 @@ extern "C" int gq_hip_model_bind(gq_ctx *c, const gq_model *m) {
   c->m = *m;
   c->layers.assign(m->layers, m->layers + m->n_layers);
   c->m.layers = c->layers.data();
+  /* tile-interleaved copies for the matrix-core matvec (ordered on the
+   * stream after whatever wrote the weights) */
+  mm_free(c);
+  c->mm.resize(m->n_layers);
+  for (int l = 0; l < m->n_layers; l++) {
+    const gq_layer &L = c->layers[l];
+    gq_ctx::MmLayer &M = c->mm[l];
+    const gq_weight *grp[3][3];
+    int nin[3];
+    const int ng = qkv_groups(L, grp, nin);
+    for (int gi = 0; gi < ng; gi++) M.qkv[gi] = mm_build(c, grp[gi], nin[gi], false);
+    const gq_weight *o[1] = {&L.wo}, *d[1] = {&L.w_down}, *gu[2] = {&L.w_gate, &L.w_up};
+    M.o = mm_build(c, o, 1, false);
+    M.down = mm_build(c, d, 1, false);
+    if (L.w_gate.dtype == L.w_up.dtype) M.gu = mm_build(c, gu, 2, true);
+  }
+  {
+    const gq_weight *lm[1] = {&m->lm_head};
+    c->mm_lm = mm_build(c, lm, 1, false);
+  }
   Workspace &w = c->ws;
   w.nch = gq_attn_nch(m->n_kv_heads, c->kv_max_seq);
   w.s_max = gq_attn_smax(c->kv_max_seq, w.nch);
@@ -676,6 +788,7 @@ static int op_qkv(gq_ctx *c, int l, int pos, const int *pos_dev, float *hidden) 
     if (done[i]) continue;
     MvArgs &a = g[ng];
     a = MvArgs{};
+    a.mm = (size_t)l < c->mm.size() ? c->mm[l].qkv[ng] : nullptr;
     gdt[ng++] = W[i]->dtype;
     a.cols = m.hidden, a.x = hidden, a.norm_w = L.rms_att, a.eps = m.rms_eps;
     a.rope = MvRope{c->rope, pos_dev, pos, m.head_dim, c->kv_max_seq};
@@ -686,8 +799,9 @@ static int op_qkv(gq_ctx *c, int l, int pos, const int *pos_dev, float *hidden) 
         done[j] = true;
       }
   }
-  /* Q4_K q, k and Q6_K v (the Q4_K_M mix): one paired launch */
-  if (ng == 2) {
+  /* Q4_K q, k and Q6_K v (the Q4_K_M mix): one paired launch (the
+   * matrix-core kernel takes them one by one) */
+  if (ng == 2 && !(gq_matvec_mm_enabled() && g[0].mm && g[1].mm)) {
     const int rc = gq_launch_matvec_pair(gdt[0], g[0], gdt[1], g[1], c->stream);
     if (rc <= 0) {
       if (rc == 0) mark(c, PC_QKV, bytes);
@@ -724,6 +838,7 @@ static int op_o(gq_ctx *c, int l, float *hidden) {
   MvArgs a{};
   a.seg[0] = MvSeg{(const uint8_t *)L.wo.data, hidden, hidden, L.wo.rows};
   a.nseg = 1, a.cols = L.wo.cols, a.x = c->ws.attn;
+  a.mm = (size_t)l < c->mm.size() ? c->mm[l].o : nullptr;
   const int rc = gq_launch_matvec(L.wo.dtype, MV_RESID, a, c->stream);
   if (rc) return rc;
   mark(c, PC_O, mv_bytes(L.wo, 1));
@@ -741,6 +856,7 @@ static int op_gate_up(gq_ctx *c, int l, float *hidden) {
     a.seg[0] = MvSeg{(const uint8_t *)L.w_gate.data, w.act, nullptr, L.w_gate.rows};
     a.seg[1] = MvSeg{(const uint8_t *)L.w_up.data, nullptr, nullptr, L.w_up.rows};
     a.nseg = 2, a.cols = m.hidden, a.x = hidden, a.norm_w = L.rms_ffn, a.eps = m.rms_eps;
+    a.mm = (size_t)l < c->mm.size() ? c->mm[l].gu : nullptr;
     if ((rc = gq_launch_matvec(L.w_gate.dtype, MV_SWIGLU, a, c->stream))) return rc;
     mark(c, PC_GATE_UP, mv_bytes(L.w_gate, 0) + mv_bytes(L.w_up, 0) - 4.0 * m.hidden - 4.0 * m.ff);
     return 0;
@@ -764,6 +880,7 @@ static int op_down(gq_ctx *c, int l, float *hidden) {
   MvArgs a{};
   a.seg[0] = MvSeg{(const uint8_t *)L.w_down.data, hidden, hidden, L.w_down.rows};
   a.nseg = 1, a.cols = L.w_down.cols, a.x = c->ws.act;
+  a.mm = (size_t)l < c->mm.size() ? c->mm[l].down : nullptr;
   const int rc = gq_launch_matvec(L.w_down.dtype, MV_RESID, a, c->stream);
   if (rc) return rc;
   mark(c, PC_DOWN, mv_bytes(L.w_down, 1));
@@ -776,6 +893,7 @@ static int op_lm_head(gq_ctx *c, float *hidden) {
   MvArgs a{};
   a.seg[0] = MvSeg{(const uint8_t *)m.lm_head.data, c->ws.logits, nullptr, m.lm_head.rows};
   a.nseg = 1, a.cols = m.hidden, a.x = hidden, a.norm_w = m.rms_final, a.eps = m.rms_eps;
+  a.mm = c->mm_lm;
   const int rc = gq_launch_matvec(m.lm_head.dtype, MV_STORE, a, c->stream);
   if (rc) return rc;
   mark(c, PC_LM_HEAD, mv_bytes(m.lm_head, 0));
@@ -1144,18 +1262,25 @@ extern "C" float gq_hip_time_matvec(gq_ctx *c, int dtype, const void *const *w_d
                                     int cols, const float *x, float *y, int n_iter) {
   if (!c || !w_devs || n_w <= 0 || n_iter <= 0) return -1.f;
   if (check_mv(c, dtype, w_devs[0], rows, cols, 0, x, y)) return -1.f;
+  /* tiled copies, made before the timed region, when the matrix-core
+   * kernel is selected */
+  std::vector<const uint8_t *> mm(n_w, nullptr);
+  for (int i = 0; i < n_w; i++) mm[i] = op_tile(c, dtype, w_devs[i], rows, cols);
   hipEvent_t e0, e1;
   if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return -1.f;
   (void)hipEventRecord(e0, c->stream);
-  for (int i = 0; i < n_iter; i++)
-    if (launch_one_mv(c, dtype, w_devs[i % n_w], rows, cols, x, y + (size_t)(i % n_w) * rows)) return -1.f;
+  int rc = 0;
+  for (int i = 0; i < n_iter && !rc; i++)
+    rc = launch_one_mv(c, dtype, w_devs[i % n_w], rows, cols, x, y + (size_t)(i % n_w) * rows, mm[i % n_w]);
   (void)hipEventRecord(e1, c->stream);
   (void)hipEventSynchronize(e1);
   float t = 0.f;
   (void)hipEventElapsedTime(&t, e0, e1);
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
-  return t / n_iter;
+  for (const uint8_t *p : mm)
+    if (p) gq_hip_free(c, (void *)p);
+  return rc ? -1.f : t / n_iter;
 }
 
 extern "C" float gq_hip_time_attention(gq_ctx *c, int layer, int pos, const float *q, float *out,

@@ -212,12 +212,13 @@ float gq_hip_time_op(gq_ctx *ctx, int op, int pos, int n_iter);
 float gq_hip_time_matvec(gq_ctx *ctx, int dtype, const void *const *w_devs, int n_w, int rows,
                          int cols, const float *x_dev, float *y_dev, int n_iter);
 /* Selects the matvec kernels for later launches in this process: 4 (default)
- * auto: the wave-private LDS ring for gate/up launches, the split-K LDS
- * kernel for the rest; 3 the register-ring kernel where a wave covers whole
+ * auto: the int8 matrix-core kernel for gate/up and the LM head (when the
+ * bound model has its tile-interleaved copies), the split-K LDS kernel for
+ * the rest; 3 the register-ring kernel where a wave covers whole
  * rows in one column tile; 2 the wave-private LDS-ring kernel where a wave
  * covers whole rows; 1 the split-K LDS-streamed kernel; 0 the register-path
- * kernel only.  Each setting falls back down 3 -> 2 -> 1 -> 0 for shapes it
- * does not fit.  Returns the previous setting.  No reference counterpart: a
+ * kernel only; 5 the int8 matrix-core kernel where it fits, else 1.  Each
+ * setting falls back down 3 -> 2 -> 1 -> 0 for shapes it does not fit.  Returns the previous setting.  No reference counterpart: a
  * switch for the parity tests (every kernel against the oracle) and for
  * timing. */
 int gq_hip_set_matvec_path(int path);
