@@ -7,12 +7,13 @@ KV cache are resident before the timed region.  Steps start at position
 8192 (warm-up steps are run from the same position first and overwritten).
 
 Prints ONE JSON line.  value = tokens/s over exactly --steps tokens between
-two device synchronisations.  roofline = the dominant kernel (the fused
-gate/up + SwiGLU matvec, mvl_kernel<Q4_K, MV_SWIGLU>): its algorithmic bytes
-per launch over its average duration, measured live with HIP events around
-64 back-to-back launches cycling over the 32 layers at the same position;
+two device synchronisations.  roofline = the dominant matvec (the fused
+gate/up + SwiGLU launch, the int8 matrix-core kernel mvm_kernel<Q4_K,
+MV_SWIGLU> on tile-interleaved weights): its algorithmic bytes per launch
+over its average duration, measured live with HIP events around 64
+back-to-back launches cycling over the 32 layers at the same position;
 traffic = its HBM bytes per launch from the committed rocprofv3 counter runs
-(profiles/mvl_gate_up_llama8b_hbm_traffic.md).  cpu_baseline =
+(profiles/mvm_gate_up_llama8b_hbm_traffic.md).  cpu_baseline =
 the reference's own CPU forward() (oracle/_ref/libref.so) timed on this
 host on a bounded sample, or the oracle port when the reference build is
 absent.
@@ -35,7 +36,7 @@ def log(msg):
 
 
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                            "mvl_gate_up_llama8b_hbm_traffic.md")
+                            "mvm_gate_up_llama8b_hbm_traffic.md")
 
 
 def measured_traffic():
@@ -130,8 +131,8 @@ def main():
 
     # per-kernel-class device time of one eager step at the first timed position
     prof = dm.profile_step(start_tok, CTX)
-    # the dominant kernel: the fused gate/up + SwiGLU matvec (one launch per
-    # layer, mvl_kernel<Q4_K, MV_SWIGLU>); algorithmic bytes per launch =
+    # the dominant matvec: the fused gate/up + SwiGLU launch (one per layer,
+    # mvm_kernel<Q4_K, MV_SWIGLU>); algorithmic bytes per launch =
     # 2 x 14336 x 4096 Q4_K weights (144 B per 256) + x, norm weight, output
     gu = prof["gate_up"]
     bytes_per_launch = gu["bytes"] / max(gu["launches"], 1)
@@ -170,7 +171,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(),
-                     "kernel": "mvl_kernel<Q4_K, MV_SWIGLU> (gate/up + SwiGLU, one launch per layer)",
+                     "kernel": "mvm_kernel<Q4_K, MV_SWIGLU> (gate/up + SwiGLU on the int8 matrix cores, "
+                               "one launch per layer)",
                      "avg_launch_ms": round(avg_ms, 5), "bytes_per_launch": int(bytes_per_launch)},
         "per_token": {"weight_bytes": weight_bytes, "kv_bytes_at_8192": kv_bytes,
                       "effective_GB_per_s": round((weight_bytes + kv_bytes) * tok_s / 1e9, 1),

@@ -1483,6 +1483,8 @@ struct MmPlan {
   int xslots;
   int xwb;          /* bytes of x slices per wave: 1 KB per block, twice with a norm weight */
   int xsum, swb;    /* LDS offset of the waves' sub-block sums of x, bytes per wave */
+  int planes, pwb;  /* without AREG: LDS offset of the waves' digit planes, bytes per wave */
+  int eb;           /* without AREG: LDS offset of the waves' block exponents (32 bytes each) */
   int park;         /* LDS offset of the finished outputs (16 floats per tile) */
   int total;        /* output rows (MV_SWIGLU: gate rows) */
 };
@@ -1744,11 +1746,15 @@ __device__ __forceinline__ int mm_issue(const MvArgs &a, const MmPlan &pl, int t
   return cnt;
 }
 
-template <int DT, int MODE, int NW, int MAXB, int NS>
+/* AREG: the wave's A operands live in registers for the whole launch (up to
+ * MAXB blocks, every chunk); otherwise the digit planes stay in LDS (up to
+ * 8 blocks per wave) and each stage loads the A operands of its MAXB
+ * blocks per wave, for rows longer than registers hold. */
+template <int DT, int MODE, int NW, int MAXB, int NS, bool AREG>
 __global__ __launch_bounds__(NW * GQ_WAVE) void mvm_kernel(MvArgs a, MmPlan pl) {
   using T = typename MmTr<DT>::type;
   static_assert(NS >= 3, "ring of NS stage slots, NS - 1 stages in flight");
-  constexpr int MAXU = 1024 / (NW * GQ_WAVE); /* 256-value blocks of x per thread row (cols <= 16384) */
+  constexpr int MAXT = AREG ? MAXB : 8; /* blocks a wave converts */
   __shared__ MmShared<NW> sh;
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   GQ_LDS uint8_t *lds = (GQ_LDS uint8_t *)smem;
@@ -1765,32 +1771,33 @@ __global__ __launch_bounds__(NW * GQ_WAVE) void mvm_kernel(MvArgs a, MmPlan pl) 
                                      lres + (tl % kRing) * 16, wave, lane);
   };
 
-  /* This wave's blocks: ai = c * bpc + s is block c*cb + wave + s*NW.  Its
+  /* This wave's blocks: ti = c * bpc + s is block c*cb + wave + s*NW.  Its
    * slices of x (and of the norm weight) go by DMA to the wave's own area
    * in the last pl.xslots ring slots, ahead of the stages whose slots they
-   * leave free; each wave converts its own blocks there, so the prologue
-   * has no barrier (the RMSNorm sum of squares crosses the loop's first
-   * one, before which no stage lands in those slots). */
+   * leave free; each wave converts its own blocks, so the prologue has no
+   * barrier (the RMSNorm sum of squares crosses the loop's first one,
+   * before which no stage lands in those slots). */
   uint32_t valid = 0;
-  int blk[MAXB];
+  int blk[MAXT];
 #pragma unroll
-  for (int ai = 0; ai < MAXB; ai++) {
-    const int c = ai / pl.bpc, s = ai - c * pl.bpc;
+  for (int ti = 0; ti < MAXT; ti++) {
+    const int c = ti / pl.bpc, s = ti - c * pl.bpc;
     const int bl = wave + s * NW;
-    blk[ai] = c * pl.cb + bl;
-    if (c < pl.nch && bl < pl.cb) valid |= 1u << ai;
+    blk[ti] = c * pl.cb + bl;
+    if (c < pl.nch && bl < pl.cb) valid |= 1u << ti;
   }
   const bool norm = a.norm_w != nullptr;
-  /* the digit planes of block ai overwrite the wave's x slice of block ai
-   * once it is read (768 <= 1024 bytes per block) */
-  const uint32_t xw = pl.xs + wave * pl.xwb, pw = xw, sw = pl.xsum + wave * pl.swb;
+  /* digit planes: AREG, over the wave's x slice of each block once it is
+   * read (768 <= 1024 bytes per block); else in their own region */
+  const uint32_t xw = pl.xs + wave * pl.xwb, pw = AREG ? xw : pl.planes + wave * pl.pwb;
+  const uint32_t sw = pl.xsum + wave * pl.swb, ew = pl.eb + wave * 4 * MAXT;
 #pragma unroll
-  for (int ai = 0; ai < MAXB; ai++) {
-    if (!(valid >> ai & 1u)) continue;
+  for (int ti = 0; ti < MAXT; ti++) {
+    if (!(valid >> ti & 1u)) continue;
     const uint32_t base = (uint32_t)(uintptr_t)lds;
-    dma16(a.x + 256 * blk[ai] + 4 * lane, __builtin_amdgcn_readfirstlane(base + xw + 1024u * ai));
+    dma16(a.x + 256 * blk[ti] + 4 * lane, __builtin_amdgcn_readfirstlane(base + xw + 1024u * ti));
     if (norm)
-      dma16(a.norm_w + 256 * blk[ai] + 4 * lane, __builtin_amdgcn_readfirstlane(base + xw + 1024u * (MAXB + ai)));
+      dma16(a.norm_w + 256 * blk[ti] + 4 * lane, __builtin_amdgcn_readfirstlane(base + xw + 1024u * (MAXT + ti)));
   }
   int pos = 0;
   if (MODE == MV_STORE && a.rope.cs) {
@@ -1818,26 +1825,31 @@ __global__ __launch_bounds__(NW * GQ_WAVE) void mvm_kernel(MvArgs a, MmPlan pl) 
   /* VMEM loads complete in issue order: with only the stages' copies
    * outstanding, this wave's x slices have landed */
   wait_vmcnt(sum);
-  int E[MAXB];
-  float ss = mm_wave_x<T::SBW, MAXB>(lds, xw, pw, sw, valid, norm, lane, E);
+  int E[MAXT];
+  float ss = mm_wave_x<T::SBW, MAXT>(lds, xw, pw, sw, valid, norm, lane, E);
   ss = gq_wave_total(ss);
   if (lane == 0) sh.red_ss[wave] = ss;
-  /* A operands (x digit planes), sub-block sums and exponents stay in
+  /* AREG: A operands (x digit planes), sub-block sums and exponents stay in
    * registers for the whole launch (the wave's LDS writes above are ordered
-   * before these reads) */
-  gq_i32x4 A[MAXB][T::NA];
-  typename MmTr<DT>::XS X[MAXB];
+   * before these reads); else the exponents go to LDS beside the sums */
+  gq_i32x4 A[AREG ? MAXB : 1][T::NA];
+  typename MmTr<DT>::XS X[AREG ? MAXB : 1];
   const bool nz = (n >> 2) == g && (n & 3) < 3;
+  if constexpr (AREG) {
 #pragma unroll
-  for (int ai = 0; ai < MAXB; ai++) {
-    const uint32_t po = pw + 768u * ai + 256u * (uint32_t)(n & 3);
+    for (int ai = 0; ai < MAXB; ai++) {
+      const uint32_t po = pw + 768u * ai + 256u * (uint32_t)(n & 3);
 #pragma unroll
-    for (int j = 0; j < T::NA; j++) {
-      gq_i32x4 v = {0, 0, 0, 0};
-      if (nz && (valid >> ai & 1u)) v = lld<gq_i32x4>(lds, po + T::aoff(g, j));
-      A[ai][j] = v;
+      for (int j = 0; j < T::NA; j++) {
+        gq_i32x4 v = {0, 0, 0, 0};
+        if (nz && (valid >> ai & 1u)) v = lld<gq_i32x4>(lds, po + T::aoff(g, j));
+        A[ai][j] = v;
+      }
+      X[ai] = T::xsums(lds, sw, (valid >> ai & 1u) ? ai : 0, g);
     }
-    X[ai] = T::xsums(lds, sw, (valid >> ai & 1u) ? ai : 0, g);
+  } else if (lane == 0) {
+#pragma unroll
+    for (int ti = 0; ti < MAXT; ti++) lst<int>(lds, ew + 4 * ti, E[ti]);
   }
   float rscale = 1.f;
   bool have_rscale = !norm;
@@ -1848,7 +1860,7 @@ __global__ __launch_bounds__(NW * GQ_WAVE) void mvm_kernel(MvArgs a, MmPlan pl) 
    * compute stage k.  Outputs are stored after the loop: a store inside it
    * would hold up the next wait on the vector memory counter. */
   GQ_LDS float *park = (GQ_LDS float *)(lds + pl.park);
-  const bool full = pl.nch == 1 && valid == (1u << MAXB) - 1u;
+  const bool full = AREG && pl.nch == 1 && valid == (1u << MAXB) - 1u;
   constexpr int RPW = 16 / NW; /* rows of a finished tile each wave completes */
   float acc = 0.f;
   for (int k = 0; k <= nst; k++) {
@@ -1923,7 +1935,27 @@ __global__ __launch_bounds__(NW * GQ_WAVE) void mvm_kernel(MvArgs a, MmPlan pl) 
     const GQ_LDS uint8_t *buf = lds + (k % NS) * pl.stride;
     typename T::Frag f[MAXB];
     typename T::Acc r[MAXB];
-    if (full) {
+    if constexpr (!AREG) {
+      /* this stage's blocks of the wave: A operands, sums and exponents from
+       * the planes in LDS */
+#pragma unroll
+      for (int ai = 0; ai < MAXB; ai++) {
+        const int ti = c * pl.bpc + ai;
+        if (ai >= pl.bpc || !(valid >> ti & 1u)) continue;
+        gq_i32x4 Ab[T::NA];
+        const uint32_t po = pw + 768u * ti + 256u * (uint32_t)(n & 3);
+#pragma unroll
+        for (int j = 0; j < T::NA; j++) {
+          gq_i32x4 v = {0, 0, 0, 0};
+          if (nz) v = lld<gq_i32x4>(lds, po + T::aoff(g, j));
+          Ab[j] = v;
+        }
+        const int eb = __builtin_amdgcn_readfirstlane(lld<int>(lds, ew + 4 * ti));
+        T::load(f[ai], buf + (blk[ti] - c * pl.cb) * (16 * T::BB), n, g);
+        T::mma(r[ai], f[ai], Ab);
+        acc += T::fin(r[ai], f[ai], g, T::xsums(lds, sw, ti, g), eb);
+      }
+    } else if (full) {
 #pragma unroll
       for (int ai = 0; ai < MAXB; ai++) T::load(f[ai], buf + blk[ai] * (16 * T::BB), n, g);
 #pragma unroll
@@ -2204,15 +2236,17 @@ int launch_reg(const MvArgs &a, int total, hipStream_t s) {
  * straddle, rows not a multiple of 16 bytes, or x not fitting the ring's
  * last slot during the prologue). */
 int g_mm_waves = 8;          /* waves per workgroup: 4 or 8 */
+constexpr size_t kMmLds = 160 * 1024; /* LDS of a CU (gfx950) */
 int g_mm_ns = 3;             /* ring slots: 3, 4 or 6 */
 int g_mm_stage_cap = 40960;  /* bytes of weights per stage at most */
 
-template <int DT, int MODE, int NW, int MAXB, int NS>
+template <int DT, int MODE, int NW, int MAXB, int NS, bool AREG = true>
 int launch_mm_as(const MvArgs &a, const MmPlan &pl, size_t lds, int grid, hipStream_t s) {
   static bool attr_set = false;
-  auto f = mvm_kernel<DT, MODE, NW, MAXB, NS>;
+  auto f = mvm_kernel<DT, MODE, NW, MAXB, NS, AREG>;
   if (!attr_set) {
     (void)hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLdsW);
+    (void)hipGetLastError(); /* a refusal shows up as the launch's error instead */
     attr_set = true;
   }
   hipLaunchKernelGGL(f, dim3(grid), dim3(NW * GQ_WAVE), lds, s, a, pl);
@@ -2220,7 +2254,9 @@ int launch_mm_as(const MvArgs &a, const MmPlan &pl, size_t lds, int grid, hipStr
 }
 
 template <int DT, int MODE, int NW, int NS>
-int launch_mm_b(int maxb, const MvArgs &a, const MmPlan &pl, size_t lds, int grid, hipStream_t s) {
+int launch_mm_b(int maxb, bool areg, const MvArgs &a, const MmPlan &pl, size_t lds, int grid, hipStream_t s) {
+  if (!areg) return pl.bpc <= 1 ? launch_mm_as<DT, MODE, NW, 1, NS, false>(a, pl, lds, grid, s)
+                                : launch_mm_as<DT, MODE, NW, 2, NS, false>(a, pl, lds, grid, s);
   if (maxb <= 1) return launch_mm_as<DT, MODE, NW, 1, NS>(a, pl, lds, grid, s);
   if (maxb <= 2) return launch_mm_as<DT, MODE, NW, 2, NS>(a, pl, lds, grid, s);
   return launch_mm_as<DT, MODE, NW, 4, NS>(a, pl, lds, grid, s);
@@ -2245,20 +2281,28 @@ int launch_mm_w(const MvArgs &a, int total, hipStream_t s) {
   pl.nch = pl.nb / cb;
   pl.bpc = (cb + NW - 1) / NW;
   const int maxb = pl.nch * pl.bpc;
-  if (maxb > 4) return 1; /* eight blocks of A operands per wave spill registers */
+  /* up to four blocks per wave keep their A operands in registers (eight
+   * spill); up to eight keep their planes in LDS, two per stage */
+  const bool areg = maxb <= 4;
+  if (!areg && (maxb > 8 || pl.bpc > 2)) return 1;
+  const int mt = areg ? (maxb <= 1 ? 1 : maxb <= 2 ? 2 : 4) : 8; /* the kernel's MAXT */
   pl.stride = (16 * pl.crb + 255) / 256 * 256;
   /* the waves' x slices in the ring's last slots; after the ring their
-   * sub-block sums, then the parked outputs */
-  const int mb2 = maxb <= 1 ? 1 : maxb <= 2 ? 2 : 4; /* the kernel's MAXB */
-  pl.xwb = 1024 * mb2 * (a.norm_w ? 2 : 1);
+   * sub-block sums, (without AREG) their digit planes and exponents, then
+   * the parked outputs */
+  pl.xwb = 1024 * mt * (a.norm_w ? 2 : 1);
   pl.xslots = (NW * pl.xwb + pl.stride - 1) / pl.stride;
-  const int ns = std::max(g_mm_ns >= 6 ? 6 : g_mm_ns == 4 ? 4 : 3, pl.xslots + 1);
+  int ns = std::max(g_mm_ns >= 6 ? 6 : g_mm_ns == 4 ? 4 : 3, pl.xslots + 1);
+  if (ns == 5) ns = 6; /* the kernels are built for 3, 4 and 6 slots */
   if (ns > 6) return 1;
   pl.ns = ns;
   pl.xs = (ns - pl.xslots) * pl.stride;
-  pl.swb = 4 * mb2 * (256 / T::SBW);
+  pl.swb = 4 * (areg ? mt : maxb) * (256 / T::SBW);
   pl.xsum = ns * pl.stride;
-  pl.park = pl.xsum + NW * pl.swb;
+  pl.pwb = areg ? 0 : 768 * maxb;
+  pl.planes = pl.xsum + NW * pl.swb;
+  pl.eb = pl.planes + NW * pl.pwb;
+  pl.park = pl.eb + NW * 4 * mt;
   pl.total = total;
   pl.ntiles = MODE == MV_SWIGLU ? (total + 7) / 8 : (total + 15) / 16;
   /* workgroups per CU from LDS, then the grid; the parking area holds
@@ -2269,12 +2313,12 @@ int launch_mm_w(const MvArgs &a, int total, hipStream_t s) {
   for (int pc = 2; pc >= 1 && !grid; pc--) {
     const int gr = std::min(pl.ntiles, pc * g_n_cu);
     const size_t l = (size_t)pl.park + 64 * (size_t)((pl.ntiles + gr - 1) / gr);
-    if (l <= kMaxDynLdsW && pc * (l + shb + 1024) <= 160 * 1024) grid = gr, lds = l;
+    if (l <= kMaxDynLdsW && pc * (l + shb + 1024) <= kMmLds + 1024) grid = gr, lds = l;
   }
   if (!grid) return 1;
-  if (ns == 3) return launch_mm_b<DT, MODE, NW, 3>(maxb, a, pl, lds, grid, s);
-  if (ns == 4) return launch_mm_b<DT, MODE, NW, 4>(maxb, a, pl, lds, grid, s);
-  return launch_mm_b<DT, MODE, NW, 6>(maxb, a, pl, lds, grid, s);
+  if (ns == 3) return launch_mm_b<DT, MODE, NW, 3>(maxb, areg, a, pl, lds, grid, s);
+  if (ns == 4) return launch_mm_b<DT, MODE, NW, 4>(maxb, areg, a, pl, lds, grid, s);
+  return launch_mm_b<DT, MODE, NW, 6>(maxb, areg, a, pl, lds, grid, s);
 }
 
 template <int DT, int MODE>
