@@ -1871,9 +1871,11 @@ __global__ __launch_bounds__(NW * GQ_WAVE) void mvm_kernel(MvArgs a, MmPlan pl) 
       wait_vmcnt(pend);
     }
     __syncthreads();
-    if (k < nst) {
-      /* stages up to k + NS - 1 (the first iteration also those x held
-       * back), into the slots of stages already computed */
+    /* stages up to k + NS - 1 (the first iteration also those x held back),
+     * into the slots of stages already computed; issued after this stage's
+     * LDS reads and MFMAs, so that the wait for room in the memory pipeline
+     * overlaps the matrix cores instead of holding every wave at once */
+    auto issue_ahead = [&]() {
 #pragma unroll
       for (int j = 0; j < NS - 2; j++) cnt[j] = cnt[j + 1];
       cnt[NS - 2] = 0;
@@ -1885,7 +1887,7 @@ __global__ __launch_bounds__(NW * GQ_WAVE) void mvm_kernel(MvArgs a, MmPlan pl) 
           issued = q + 1;
         }
       }
-    }
+    };
     const int c = k < nst ? k % pl.nch : 0;
     if (!have_rscale) { /* 1/sqrt(mean(x^2) + eps) (kernels_cpu.c:242-253) */
       float tot = 0.f;
@@ -1955,11 +1957,13 @@ __global__ __launch_bounds__(NW * GQ_WAVE) void mvm_kernel(MvArgs a, MmPlan pl) 
         T::mma(r[ai], f[ai], Ab);
         acc += T::fin(r[ai], f[ai], g, T::xsums(lds, sw, ti, g), eb);
       }
+      issue_ahead();
     } else if (full) {
 #pragma unroll
       for (int ai = 0; ai < MAXB; ai++) T::load(f[ai], buf + blk[ai] * (16 * T::BB), n, g);
 #pragma unroll
       for (int ai = 0; ai < MAXB; ai++) T::mma(r[ai], f[ai], A[ai]);
+      issue_ahead();
 #pragma unroll
       for (int ai = 0; ai < MAXB; ai++) acc += T::fin(r[ai], f[ai], g, X[ai], E[ai]);
     } else {
@@ -1968,10 +1972,11 @@ __global__ __launch_bounds__(NW * GQ_WAVE) void mvm_kernel(MvArgs a, MmPlan pl) 
         if (ai / pl.bpc == c && (valid >> ai & 1u)) T::load(f[ai], buf + (blk[ai] - c * pl.cb) * (16 * T::BB), n, g);
 #pragma unroll
       for (int ai = 0; ai < MAXB; ai++)
-        if (ai / pl.bpc == c && (valid >> ai & 1u)) {
-          T::mma(r[ai], f[ai], A[ai]);
-          acc += T::fin(r[ai], f[ai], g, X[ai], E[ai]);
-        }
+        if (ai / pl.bpc == c && (valid >> ai & 1u)) T::mma(r[ai], f[ai], A[ai]);
+      issue_ahead();
+#pragma unroll
+      for (int ai = 0; ai < MAXB; ai++)
+        if (ai / pl.bpc == c && (valid >> ai & 1u)) acc += T::fin(r[ai], f[ai], g, X[ai], E[ai]);
     }
     if (c == pl.nch - 1) { /* the tile's last chunk: reduce over the k-groups */
       float v = acc;
