@@ -964,30 +964,39 @@ __device__ __forceinline__ void mvl_body(const MvArgs &a, const MvPlan &pl, int 
                             : 0; /* mygroups >= 1 */
   }
 
-  /* Stage k's copies are issued at iteration k-(NS-1), before that
-   * iteration's wait, into the slot stage k-NS used (computed at iteration
-   * k-NS, before the barrier closing it); at iteration k they are waited
-   * for, computed and at iteration k+1 its rows are finished (reduced,
-   * stored). */
+  /* Stage k's copies are issued at iteration k-(NS-1) into the slot stage
+   * k-NS used (computed at iteration k-NS, before the barrier closing it):
+   * before that iteration's wait, or with x read from global memory (the
+   * long rows of the down projection) after its arithmetic, where the wait
+   * for room in the memory pipeline does not hold the arithmetic up
+   * (16.1 against 16.6 us for the 8B down; the short-row launches measured
+   * 0.1 us slower that way).  At iteration k they are waited for, computed
+   * and at iteration k+1 its rows are finished (reduced, stored). */
+  constexpr bool LATE = !XL;
   const int hrows = MODE == MV_SWIGLU ? pl.rs / 2 : pl.rs;
   const int rpw = pl.rs / pl.nteam; /* rows per team and stage, a multiple of RW */
   int slot = 0;                     /* k % NS */
   for (int k = 0; k <= mygroups; k++) {
-    if (k < mygroups) {
+    auto issue_ahead = [&]() {
       const int kn = k + NS - 1, sn = slot == 0 ? NS - 1 : slot - 1; /* kn % NS */
       const int nn = kn < mygroups ? issue_stage<MODE>(a, pl, bid + kn * nblk, lds + sn * pl.stride,
                                                        lres + (kn % kRing) * 32, wave, lane)
                                    : 0;
-      /* VMEM loads complete in issue order: with at most stages k+1 ..
-       * k+NS-1 outstanding, this wave's copies of stage k have landed; the
-       * barrier extends that to every wave's */
-      int pend = nn;
-#pragma unroll
-      for (int j = 1; j < NS - 1; j++) pend += cnt[j];
-      wait_vmcnt(pend);
 #pragma unroll
       for (int j = 0; j < NS - 2; j++) cnt[j] = cnt[j + 1];
       cnt[NS - 2] = nn;
+      return nn;
+    };
+    if (k < mygroups) {
+      /* VMEM loads complete in issue order: with only the copies of later
+       * stages outstanding (k+1 .. k+NS-1, or k+NS-2 when issued late),
+       * this wave's copies of stage k have landed; the barrier extends that
+       * to every wave's */
+      int pend = 0;
+#pragma unroll
+      for (int j = 1; j < NS - 1; j++) pend += cnt[j]; /* stages k+1 .. k+NS-2 */
+      if constexpr (!LATE) pend += issue_ahead();
+      wait_vmcnt(pend);
     }
     __syncthreads();
     if (k > 0) { /* finish the rows of stage k-1: row t on lane t/4 of wave t%4 */
@@ -1036,6 +1045,7 @@ __device__ __forceinline__ void mvl_body(const MvArgs &a, const MvPlan &pl, int 
           for (int r = 0; r < RW; r++) red[k & 1][i0 + r][wj * 4 + (lane >> 4)] = acc[r];
       }
     }
+    if constexpr (LATE) issue_ahead();
     __syncthreads();
     slot = slot == NS - 1 ? 0 : slot + 1;
   }
