@@ -1941,9 +1941,10 @@ __global__ __launch_bounds__(NW * GQ_WAVE) void mvm_kernel(MvArgs a, MmPlan pl) 
       }
     }
     if (k == nst) break;
-    /* every LDS read of the stage first, then every MFMA, then the
-     * epilogues: one basic block when the launch has one chunk and every
-     * block slot of the wave is used (uniform: all waves take it) */
+    /* every LDS read of the stage first, then every MFMA, then the copies of
+     * the stages ahead, then the epilogues (the fast path when the launch
+     * has one chunk and every block slot of the wave is used; uniform: all
+     * waves take it) */
     const GQ_LDS uint8_t *buf = lds + (k % NS) * pl.stride;
     typename T::Frag f[MAXB];
     typename T::Acc r[MAXB];
