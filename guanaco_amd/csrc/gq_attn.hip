@@ -282,9 +282,11 @@ int gq_launch_attention(const AttnArgs &a, hipStream_t s, hipEvent_t mid) {
   if (a.hd == 128 && G == 4) rc = launch_partial<128, 4>(a, s);
   else if (a.hd == 128 && G == 8) rc = launch_partial<128, 8>(a, s);
   else if (a.hd == 128 && G == 1) rc = launch_partial<128, 1>(a, s);
+  else if (a.hd == 128 && G == 2) rc = launch_partial<128, 2>(a, s);
   else if (a.hd == 64 && G == 4) rc = launch_partial<64, 4>(a, s);
   else if (a.hd == 64 && G == 8) rc = launch_partial<64, 8>(a, s);
   else if (a.hd == 64 && G == 1) rc = launch_partial<64, 1>(a, s);
+  else if (a.hd == 64 && G == 2) rc = launch_partial<64, 2>(a, s);
   if (rc) return rc;
   if (mid) (void)hipEventRecord(mid, s);
   hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_heads, a.hd / 32), dim3(kThreads),

@@ -60,11 +60,72 @@ struct MvArgs {
   const uint8_t *mm;
 };
 
+/* silu(g) * u as the reference computes it: silu(g) = g * (1 / (1 + expf(-g)))
+ * (kernels_cpu.c:322-336), then the product (elemwise_mul, :367-389) */
+__device__ __forceinline__ float gq_silu_mul(float g, float u) {
+  const float sig = 1.0f / (1.0f + expf(0.0f - g));
+  return (g * sig) * u;
+}
+
+/* The segments of a launch as plain values, read from the kernel
+ * arguments once with constant indices and pinned in scalar registers: a
+ * runtime index into the argument struct (or a select between its fields,
+ * which the compiler may turn into a load through a selected address)
+ * compiles to a copy of the struct in scratch memory or a global load with a
+ * full vmcnt(0) wait. */
+struct MvSegs {
+  const uint8_t *w0, *w1, *w2;
+  float *y0, *y1, *y2;
+  const float *r0, *r1, *r2;
+  int n0, n1, n2;
+  int k0, k1, k2;
+  int nseg;
+};
+
+template <class T>
+__device__ __forceinline__ T gq_pin(T v) {
+  asm volatile("" : "+s"(v));
+  return v;
+}
+
+__device__ __forceinline__ MvSegs gq_mv_segs(const MvArgs &a) {
+  MvSegs s;
+  s.w0 = gq_pin(a.seg[0].w), s.w1 = gq_pin(a.seg[1].w), s.w2 = gq_pin(a.seg[2].w);
+  s.y0 = gq_pin(a.seg[0].y), s.y1 = gq_pin(a.seg[1].y), s.y2 = gq_pin(a.seg[2].y);
+  s.r0 = gq_pin(a.seg[0].r), s.r1 = gq_pin(a.seg[1].r), s.r2 = gq_pin(a.seg[2].r);
+  s.n0 = gq_pin(a.seg[0].rows), s.n1 = gq_pin(a.seg[1].rows), s.n2 = gq_pin(a.seg[2].rows);
+  s.k0 = gq_pin(a.seg[0].kind), s.k1 = gq_pin(a.seg[1].kind), s.k2 = gq_pin(a.seg[2].kind);
+  s.nseg = gq_pin(a.nseg);
+  return s;
+}
+
+/* segment and local row of output row gr of a launch */
+__device__ __forceinline__ void gq_mv_locate(const MvSegs &v, int gr, int &s, int &lr) {
+  s = 0;
+  lr = gr;
+  if (v.nseg > 1 && lr >= v.n0) {
+    lr -= v.n0, s = 1;
+    if (v.nseg > 2 && lr >= v.n1) lr -= v.n1, s = 2;
+  }
+}
+__device__ __forceinline__ const uint8_t *gq_mv_w(const MvSegs &v, int s) { return s == 0 ? v.w0 : s == 1 ? v.w1 : v.w2; }
+__device__ __forceinline__ float *gq_mv_y(const MvSegs &v, int s) { return s == 0 ? v.y0 : s == 1 ? v.y1 : v.y2; }
+__device__ __forceinline__ const float *gq_mv_r(const MvSegs &v, int s) { return s == 0 ? v.r0 : s == 1 ? v.r1 : v.r2; }
+__device__ __forceinline__ int gq_mv_rows(const MvSegs &v, int s) { return s == 0 ? v.n0 : s == 1 ? v.n1 : v.n2; }
+__device__ __forceinline__ int gq_mv_kind(const MvSegs &v, int s) { return s == 0 ? v.k0 : s == 1 ? v.k1 : v.k2; }
+
+/* Any dtype and shape the reference's matvec takes (cols % 256, Q8_0
+ * cols % 32): the matrix-core kernel where the path setting picks it and
+ * a.mm is set, else the vector-ALU kernel (gq_mvx.hip).  0, -1 bad
+ * arguments, -2 cols, -4 launch error. */
 int gq_launch_matvec(int dtype, int mode, const MvArgs &a, hipStream_t s);
+/* The matrix-core kernel alone (a.mm required); 1 when the shape does not
+ * fit it. */
+int gq_launch_mm(int dtype, int mode, const MvArgs &a, hipStream_t s);
 /* Two MV_STORE matvecs of different dtypes (Q4_K, then Q6_K) over the same
  * x in one launch; 1 when the pair is not supported (launch them apart). */
 int gq_launch_matvec_pair(int dt0, const MvArgs &a0, int dt1, const MvArgs &a1, hipStream_t s);
-/* workgroups the matvec launcher puts on the device at most (persistent grid) */
+/* compute units of the device (sizes the matrix-core kernel's grid) */
 void gq_matvec_set_cus(int n_cu);
 
 /* Tile-interleaved copy of a Q4_K or Q6_K weight for the matrix-core matvec.
@@ -76,10 +137,9 @@ void gq_matvec_set_cus(int n_cu);
  * same rows of w1.  Bytes: gq_mm_tile_bytes. */
 size_t gq_mm_tile_bytes(int dtype, int rows, int cols, bool swiglu);
 int gq_launch_mm_tile(void *dst, int dtype, const void *w0, const void *w1, int rows, int cols, hipStream_t s);
-/* whether the matvec launcher uses the matrix-core kernel (where MvArgs.mm
- * is set); forced: selected explicitly (gq_hip_set_matvec_path(5)), which
- * makes the op-level entry points tile their weights per call */
-bool gq_matvec_mm_enabled();
+/* whether the matrix-core kernel is selected for every launch it fits
+ * (gq_hip_set_matvec_path(2)): the op-level entry points then tile their
+ * weights per call */
 bool gq_matvec_mm_forced();
 
 /* ---- attention -------------------------------------------------------- */

@@ -39,6 +39,7 @@ struct Workspace {
  * for up to `cap` tokens; attention partials grow with the context. */
 struct PrefillWs {
   int cap = 0;
+  int H = 0, F = 0, kvd = 0; /* hidden, ff and n_kv_heads * head_dim the buffers were sized for */
   float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr; /* fp32: hidden, q/k/v for RoPE */
   __bf16 *xn = nullptr, *att = nullptr, *act = nullptr;          /* bf16 GEMM inputs */
   __bf16 *xb = nullptr; /* op-level entry: bf16 copy of its fp32 x */
@@ -70,13 +71,11 @@ struct gq_ctx {
   bool bound = false;
   gq_model m{};
   std::vector<gq_layer> layers;
-  /* tile-interleaved copies of the bound model's Q4_K/Q6_K weights for the
-   * matrix-core matvec (gq_launch_mm_tile), owned by the context: per layer
-   * the q/k/v groups of op_qkv (same dtype, in order), o, gate+up, down;
+  /* tile-interleaved copies of the bound model's gate+up pairs and LM head
+   * for the matrix-core matvec (gq_launch_mm_tile), owned by the context;
    * NULL where a weight does not take that layout */
   struct MmLayer {
-    const uint8_t *qkv[3] = {nullptr, nullptr, nullptr};
-    const uint8_t *o = nullptr, *gu = nullptr, *down = nullptr;
+    const uint8_t *gu = nullptr;
   };
   std::vector<MmLayer> mm;
   const uint8_t *mm_lm = nullptr;
@@ -95,6 +94,7 @@ struct gq_ctx {
 };
 
 static int fail(gq_ctx *c, int code, const char *fmt, ...) __attribute__((format(printf, 3, 4)));
+static void pf_release(gq_ctx *c);
 static int fail(gq_ctx *c, int code, const char *fmt, ...) {
   if (c) {
     va_list ap;
@@ -280,7 +280,6 @@ static int check_mv(gq_ctx *c, int dtype, const void *w, int rows, int cols, siz
   if (cols % qk) return fail(c, -2, "matvec: cols %d not a multiple of %d", cols, qk);
   if (byte_size && (size_t)rows * (size_t)(cols / qk) * bb > byte_size)
     return fail(c, -3, "matvec: byte_size %zu too small", byte_size);
-  if (cols > 16384) return fail(c, -1, "matvec: cols %d above 16384", cols);
   return 0;
 }
 
@@ -353,31 +352,44 @@ static size_t layer_floats(const gq_ctx *c) {
   return (size_t)c->kv_heads * c->kv_max_seq * c->kv_hd;
 }
 
+/* Free the K/V slabs and the RoPE table and forget the cache geometry: every
+ * entry point that checks c->kslab then sees no cache. */
+static void kv_release(gq_ctx *c) {
+  (void)hipStreamSynchronize(c->stream);
+  if (c->kslab) gq_hip_free(c, c->kslab);
+  if (c->vslab) gq_hip_free(c, c->vslab);
+  if (c->rope) gq_hip_free(c, c->rope);
+  c->kslab = c->vslab = nullptr;
+  c->rope = nullptr;
+  c->kv_layers = c->kv_heads = c->kv_hd = c->kv_max_seq = 0;
+  c->bound = false;
+}
+
 extern "C" int gq_hip_kv_init(gq_ctx *c, int n_layers, int n_kv_heads, int head_dim, int max_seq,
                               float rope_theta) {
   if (!c || n_layers <= 0 || n_kv_heads <= 0 || head_dim <= 0 || (head_dim & 1) || max_seq <= 0)
     return fail(c, -1, "kv_init: bad geometry");
   (void)hipSetDevice(c->dev);
-  if (c->kslab) {
-    gq_hip_free(c, c->kslab);
-    gq_hip_free(c, c->vslab);
-    gq_hip_free(c, c->rope);
-    c->kslab = c->vslab = nullptr;
-    c->rope = nullptr;
-  }
+  kv_release(c);
   free_graph(c);
   c->bound = false;
-  c->kv_layers = n_layers, c->kv_heads = n_kv_heads, c->kv_hd = head_dim, c->kv_max_seq = max_seq;
-  c->theta = rope_theta;
-  const size_t bytes = sizeof(float) * layer_floats(c) * n_layers;
+  const size_t bytes = sizeof(float) * (size_t)n_kv_heads * max_seq * head_dim * n_layers;
+  const size_t half = (size_t)head_dim / 2;
   c->kslab = (float *)dev_alloc(c, bytes);
   c->vslab = (float *)dev_alloc(c, bytes);
-  const size_t half = (size_t)head_dim / 2;
   c->rope = (float2 *)dev_alloc(c, sizeof(float2) * half * max_seq);
-  if (!c->kslab || !c->vslab || !c->rope) return -4;
+  if (!c->kslab || !c->vslab || !c->rope) { /* nothing half-made stays behind */
+    kv_release(c);
+    return fail(c, -4, "kv_init: out of device memory for %zu-byte K/V slabs", bytes);
+  }
+  c->kv_layers = n_layers, c->kv_heads = n_kv_heads, c->kv_hd = head_dim, c->kv_max_seq = max_seq;
+  c->theta = rope_theta;
   /* zeroed like kv_cache_create (kv_cache.c:73-75) */
-  HIPCHK(c, hipMemsetAsync(c->kslab, 0, bytes, c->stream));
-  HIPCHK(c, hipMemsetAsync(c->vslab, 0, bytes, c->stream));
+  if (hipMemsetAsync(c->kslab, 0, bytes, c->stream) != hipSuccess ||
+      hipMemsetAsync(c->vslab, 0, bytes, c->stream) != hipSuccess) {
+    kv_release(c);
+    return fail(c, -4, "kv_init: clearing the K/V slabs failed");
+  }
   /* RoPE table with the reference's fp32 expressions (kernels_cpu.c:409-413) */
   std::vector<float2> tab(half * max_seq);
   std::vector<float> freq(half);
@@ -388,9 +400,12 @@ extern "C" int gq_hip_kv_init(gq_ctx *c, int n_layers, int n_kv_heads, int head_
       const float a = (float)p * freq[i];
       tab[(size_t)p * half + i] = make_float2(cosf(a), sinf(a));
     }
-  HIPCHK(c, hipMemcpyAsync(c->rope, tab.data(), sizeof(float2) * tab.size(), hipMemcpyHostToDevice,
-                           c->stream));
-  HIPCHK(c, hipStreamSynchronize(c->stream));
+  if (hipMemcpyAsync(c->rope, tab.data(), sizeof(float2) * tab.size(), hipMemcpyHostToDevice, c->stream) !=
+          hipSuccess ||
+      hipStreamSynchronize(c->stream) != hipSuccess) {
+    kv_release(c);
+    return fail(c, -4, "kv_init: uploading the RoPE table failed");
+  }
   return 0;
 }
 
@@ -649,27 +664,9 @@ static void mm_free(gq_ctx *c) {
     if (p) gq_hip_free(c, (void *)p);
     p = nullptr;
   };
-  for (auto &L : c->mm) {
-    for (auto &q : L.qkv) rel(q);
-    rel(L.o), rel(L.gu), rel(L.down);
-  }
+  for (auto &L : c->mm) rel(L.gu);
   c->mm.clear();
   rel(c->mm_lm);
-}
-
-/* The q/k/v groups of one launch each (same dtype, in order q, k, v). */
-static int qkv_groups(const gq_layer &L, const gq_weight *grp[3][3], int nin[3]) {
-  const gq_weight *W[3] = {&L.wq, &L.wk, &L.wv};
-  bool done[3] = {false, false, false};
-  int ng = 0;
-  for (int i = 0; i < 3; i++) {
-    if (done[i]) continue;
-    nin[ng] = 0;
-    for (int j = i; j < 3; j++)
-      if (!done[j] && W[j]->dtype == W[i]->dtype) grp[ng][nin[ng]++] = W[j], done[j] = true;
-    ng++;
-  }
-  return ng;
 }
 
 extern "C" int gq_hip_model_bind(gq_ctx *c, const gq_model *m) {
@@ -679,8 +676,14 @@ extern "C" int gq_hip_model_bind(gq_ctx *c, const gq_model *m) {
     return fail(c, -1, "model_bind: model and KV geometry differ");
   if (m->n_heads % m->n_kv_heads || m->hidden != m->n_heads * m->head_dim)
     return fail(c, -1, "model_bind: head geometry");
-  if (m->hidden > 16384 || m->ff > 16384 || (m->hidden & 255) || (m->ff & 255))
-    return fail(c, -1, "model_bind: hidden/ff must be multiples of 256 up to 16384");
+  {
+    const int G = m->n_heads / m->n_kv_heads;
+    if ((m->head_dim != 64 && m->head_dim != 128) || (G != 1 && G != 2 && G != 4 && G != 8))
+      return fail(c, -1, "model_bind: attention kernels take head_dim 64 or 128 with 1, 2, 4 or 8 query heads per KV head (got %d, %d)",
+                  m->head_dim, G);
+  }
+  if ((m->hidden & 255) || (m->ff & 255))
+    return fail(c, -1, "model_bind: hidden and ff must be multiples of 256");
   const int H = m->hidden, F = m->ff, kvd = m->n_kv_heads * m->head_dim;
   for (int l = 0; l < m->n_layers; l++) {
     const gq_layer &L = m->layers[l];
@@ -697,24 +700,19 @@ extern "C" int gq_hip_model_bind(gq_ctx *c, const gq_model *m) {
     return fail(c, -1, "embed: F32, Q8_0 or Q4_K (vocab x hidden)");
   if (!m->rms_final) return fail(c, -1, "rms_final");
   free_graph(c);
+  pf_release(c); /* sized for the previous model */
   c->m = *m;
   c->layers.assign(m->layers, m->layers + m->n_layers);
   c->m.layers = c->layers.data();
-  /* tile-interleaved copies for the matrix-core matvec (ordered on the
-   * stream after whatever wrote the weights) */
+  /* tile-interleaved copies for the matrix-core matvec, for the launches
+   * the decode step runs on it (gate/up + SwiGLU, the LM head); ordered on
+   * the stream after whatever wrote the weights */
   mm_free(c);
   c->mm.resize(m->n_layers);
   for (int l = 0; l < m->n_layers; l++) {
     const gq_layer &L = c->layers[l];
-    gq_ctx::MmLayer &M = c->mm[l];
-    const gq_weight *grp[3][3];
-    int nin[3];
-    const int ng = qkv_groups(L, grp, nin);
-    for (int gi = 0; gi < ng; gi++) M.qkv[gi] = mm_build(c, grp[gi], nin[gi], false);
-    const gq_weight *o[1] = {&L.wo}, *d[1] = {&L.w_down}, *gu[2] = {&L.w_gate, &L.w_up};
-    M.o = mm_build(c, o, 1, false);
-    M.down = mm_build(c, d, 1, false);
-    if (L.w_gate.dtype == L.w_up.dtype) M.gu = mm_build(c, gu, 2, true);
+    const gq_weight *gu[2] = {&L.w_gate, &L.w_up};
+    if (L.w_gate.dtype == L.w_up.dtype) c->mm[l].gu = mm_build(c, gu, 2, true);
   }
   {
     const gq_weight *lm[1] = {&m->lm_head};
@@ -788,7 +786,6 @@ static int op_qkv(gq_ctx *c, int l, int pos, const int *pos_dev, float *hidden) 
     if (done[i]) continue;
     MvArgs &a = g[ng];
     a = MvArgs{};
-    a.mm = (size_t)l < c->mm.size() ? c->mm[l].qkv[ng] : nullptr;
     gdt[ng++] = W[i]->dtype;
     a.cols = m.hidden, a.x = hidden, a.norm_w = L.rms_att, a.eps = m.rms_eps;
     a.rope = MvRope{c->rope, pos_dev, pos, m.head_dim, c->kv_max_seq};
@@ -799,9 +796,8 @@ static int op_qkv(gq_ctx *c, int l, int pos, const int *pos_dev, float *hidden) 
         done[j] = true;
       }
   }
-  /* Q4_K q, k and Q6_K v (the Q4_K_M mix): one paired launch (the
-   * matrix-core kernel takes them one by one) */
-  if (ng == 2 && !(gq_matvec_mm_enabled() && g[0].mm && g[1].mm)) {
+  /* Q4_K q, k and Q6_K v (the Q4_K_M mix): one paired launch */
+  if (ng == 2) {
     const int rc = gq_launch_matvec_pair(gdt[0], g[0], gdt[1], g[1], c->stream);
     if (rc <= 0) {
       if (rc == 0) mark(c, PC_QKV, bytes);
@@ -838,7 +834,6 @@ static int op_o(gq_ctx *c, int l, float *hidden) {
   MvArgs a{};
   a.seg[0] = MvSeg{(const uint8_t *)L.wo.data, hidden, hidden, L.wo.rows};
   a.nseg = 1, a.cols = L.wo.cols, a.x = c->ws.attn;
-  a.mm = (size_t)l < c->mm.size() ? c->mm[l].o : nullptr;
   const int rc = gq_launch_matvec(L.wo.dtype, MV_RESID, a, c->stream);
   if (rc) return rc;
   mark(c, PC_O, mv_bytes(L.wo, 1));
@@ -880,7 +875,6 @@ static int op_down(gq_ctx *c, int l, float *hidden) {
   MvArgs a{};
   a.seg[0] = MvSeg{(const uint8_t *)L.w_down.data, hidden, hidden, L.w_down.rows};
   a.nseg = 1, a.cols = L.w_down.cols, a.x = c->ws.act;
-  a.mm = (size_t)l < c->mm.size() ? c->mm[l].down : nullptr;
   const int rc = gq_launch_matvec(L.w_down.dtype, MV_RESID, a, c->stream);
   if (rc) return rc;
   mark(c, PC_DOWN, mv_bytes(L.w_down, 1));
@@ -1064,11 +1058,26 @@ static int pf_ensure(gq_ctx *c, T *&p, size_t &cap, size_t n) {
   return 0;
 }
 
+/* Release the prefill activations (a model of another shape is bound, or
+ * the cache was re-made). */
+static void pf_release(gq_ctx *c) {
+  PrefillWs &w = c->pf;
+  void *bufs[8] = {w.x, w.q, w.k, w.v, w.xn, w.att, w.act, w.tok};
+  for (void *p : bufs)
+    if (p) gq_hip_free(c, p);
+  w.x = w.q = w.k = w.v = nullptr;
+  w.xn = w.att = w.act = nullptr;
+  w.tok = nullptr;
+  w.cap = w.H = w.F = w.kvd = 0;
+}
+
 static int pf_alloc(gq_ctx *c) {
   PrefillWs &w = c->pf;
-  if (w.cap) return 0;
   const gq_model &m = c->m;
-  const size_t T = kPrefillChunk, H = m.hidden, F = m.ff, kvd = (size_t)m.n_kv_heads * m.head_dim;
+  const int kvd_m = m.n_kv_heads * m.head_dim;
+  if (w.cap && w.H == m.hidden && w.F == m.ff && w.kvd == kvd_m) return 0;
+  pf_release(c);
+  const size_t T = kPrefillChunk, H = m.hidden, F = m.ff, kvd = (size_t)kvd_m;
   float **f32[4] = {&w.x, &w.q, &w.k, &w.v};
   const size_t nf[4] = {T * H, T * H, T * kvd, T * kvd};
   for (int i = 0; i < 4; i++)
@@ -1079,6 +1088,7 @@ static int pf_alloc(gq_ctx *c) {
     if (!(*b16[i] = (__bf16 *)dev_alloc(c, sizeof(__bf16) * nb[i]))) return -4;
   if (!(w.tok = (int *)dev_alloc(c, sizeof(int) * T))) return -4;
   w.cap = kPrefillChunk;
+  w.H = m.hidden, w.F = m.ff, w.kvd = kvd_m;
   return 0;
 }
 

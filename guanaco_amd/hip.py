@@ -104,18 +104,16 @@ def _load():
 lib, EXPORTS = _load()
 NCLASS = 7
 CLASS_NAMES = ("qkv", "attention", "o_proj", "gate_up", "down", "lm_head", "other")
-MATVEC_PATHS = ("register", "lds", "wave", "ring", "auto", "mfma")
+MATVEC_PATHS = ("valu", "auto", "mfma")
 
 
 class matvec_path:
     """Context manager selecting the matvec kernels: "auto" (default) the
     int8 matrix-core kernel for gate/up and the LM head of a bound model and
-    the split-K LDS kernel for the rest; "ring" the register-ring kernel where a wave covers whole rows
-    in one column tile; "wave" the wave-private LDS-ring kernel where a wave
-    covers whole rows; "lds" the split-K LDS-streamed kernel; "register" the
-    register-path kernel only; "mfma" the int8 matrix-core kernel where it
-    fits (Q4_K), else the split-K kernel.  Each choice falls back down the
-    list ring -> wave -> lds -> register for shapes it does not fit."""
+    the vector-ALU kernel for the rest; "valu" the vector-ALU kernel for
+    every launch; "mfma" the int8 matrix-core kernel wherever it fits
+    (Q4_K/Q6_K; the op-level entry points tile their weights per call),
+    else the vector-ALU kernel."""
 
     def __init__(self, name):
         self.lds = MATVEC_PATHS.index(name)

@@ -211,16 +211,14 @@ float gq_hip_time_op(gq_ctx *ctx, int op, int pos, int n_iter);
  * (to defeat the MALL) with per-buffer outputs. */
 float gq_hip_time_matvec(gq_ctx *ctx, int dtype, const void *const *w_devs, int n_w, int rows,
                          int cols, const float *x_dev, float *y_dev, int n_iter);
-/* Selects the matvec kernels for later launches in this process: 4 (default)
- * auto: the int8 matrix-core kernel for gate/up and the LM head (when the
- * bound model has its tile-interleaved copies), the split-K LDS kernel for
- * the rest; 3 the register-ring kernel where a wave covers whole
- * rows in one column tile; 2 the wave-private LDS-ring kernel where a wave
- * covers whole rows; 1 the split-K LDS-streamed kernel; 0 the register-path
- * kernel only; 5 the int8 matrix-core kernel where it fits, else 1.  Each
- * setting falls back down 3 -> 2 -> 1 -> 0 for shapes it does not fit.  Returns the previous setting.  No reference counterpart: a
- * switch for the parity tests (every kernel against the oracle) and for
- * timing. */
+/* Selects the matvec kernels for later launches in this process: 1
+ * (default) the int8 matrix-core kernel for gate/up + SwiGLU and the LM head
+ * (where the bound model has their tile-interleaved copies) and the
+ * vector-ALU kernel for every other launch; 0 the vector-ALU kernel for
+ * every launch; 2 the matrix-core kernel wherever it fits (the op-level
+ * entry points then tile their weights per call), else the vector-ALU
+ * kernel.  Returns the previous setting.  No reference counterpart: a switch
+ * for the parity tests (each kernel against the oracle) and for timing. */
 int gq_hip_set_matvec_path(int path);
 /* Device time of n launches of the attention kernels for one layer. */
 float gq_hip_time_attention(gq_ctx *ctx, int layer, int pos, const float *q_dev, float *out_dev,

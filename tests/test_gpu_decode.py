@@ -24,7 +24,7 @@ def tiny(ctx, orc):
     return spec, ms, pre, hm, dm
 
 
-@pytest.mark.parametrize("path", ["auto", "ring", "wave", "lds", "register", "mfma"])
+@pytest.mark.parametrize("path", ["auto", "valu", "mfma"])
 def test_forward_per_layer_and_tokens(ctx, orc, tiny, path):
     import guanaco_amd.hip as H
     spec, ms, pre, hm, dm = tiny

@@ -42,7 +42,7 @@ SHAPES = [
 ]
 
 
-@pytest.mark.parametrize("path", ["auto", "ring", "wave", "lds", "register", "mfma"])
+@pytest.mark.parametrize("path", ["auto", "valu", "mfma"])
 @pytest.mark.parametrize("dt,rows,cols", SHAPES)
 def test_matvec_vs_oracle(ctx, orc, dt, rows, cols, path):
     import guanaco_amd.hip as H
