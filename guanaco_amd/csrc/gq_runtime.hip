@@ -19,6 +19,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <vector>
 
 #include "gq_internal.h"
@@ -81,6 +82,7 @@ struct gq_ctx {
   const uint8_t *mm_lm = nullptr;
   Workspace ws;
   PrefillWs pf;
+  float *scratch = nullptr; /* this device's address of the file-scope `scratch` array */
   SampleWs sw;
   int *d_sample = nullptr; /* sampled token (device) */
   /* graph */
@@ -130,6 +132,35 @@ extern "C" int gq_hip_device_count(void) {
   return n;
 }
 
+/* ------------------------------------------------------------ scratch
+ * Device memory of gq_hip_attention_dev_noalloc (split-K partials): a
+ * file-scope array that every GPU the library runs on holds until the
+ * process ends, so that entry point needs no allocation.  On the host the
+ * name is only a stand-in for the symbol, never an address: each device's
+ * address comes from hipGetSymbolAddress, taken once per device with that
+ * device current (at its first context creation) and kept in scratch_addr. */
+constexpr size_t kScratchFloats = (size_t)2 << 20; /* 8 MiB */
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kMaxDevices = 64;
+static std::mutex scratch_mu;
+static float *scratch_addr[kMaxDevices];
+
+/* the calling thread's current device is `dev` */
+static float *scratch_setup(int dev) {
+  if (dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lk(scratch_mu);
+  if (!scratch_addr[dev]) {
+    void *p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    scratch_addr[dev] = (float *)p;
+  }
+  return scratch_addr[dev];
+}
+
 extern "C" gq_ctx *gq_hip_create(int device_id) {
   int n = gq_hip_device_count();
   if (device_id < 0 || device_id >= n) return nullptr;
@@ -146,6 +177,7 @@ extern "C" gq_ctx *gq_hip_create(int device_id) {
     snprintf(c->name, sizeof c->name, "%s", p.gcnArchName);
     gq_matvec_set_cus(c->n_cu);
   }
+  c->scratch = scratch_setup(device_id); /* NULL: the allocation-free entry point reports it */
   return c;
 }
 
@@ -1366,11 +1398,27 @@ extern "C" int gq_hip_rope_append_dev(gq_ctx *c, int layer, int pos, int n_heads
   return gq_launch_rope_append(ra, c->stream) ? fail(c, -4, "rope_append launch") : 0;
 }
 
-extern "C" int gq_hip_attention_dev(gq_ctx *c, int layer, int pos, int n_heads, const float *q, float *out) {
+static int attention_check(gq_ctx *c, int layer, int pos, int n_heads, const float *q, const float *out) {
   if (!c || !c->kslab || !q || !out || layer < 0 || layer >= c->kv_layers || n_heads <= 0 ||
       n_heads % c->kv_heads)
     return fail(c, -1, "attention: bad argument");
   if (pos < 0 || pos >= c->kv_max_seq) return fail(c, -5, "attention: position outside the cache");
+  if (c->bound && n_heads != c->m.n_heads) return fail(c, -1, "attention: n_heads differs from the bound model");
+  return 0;
+}
+
+static int attention_launch(gq_ctx *c, int layer, int pos, int n_heads, const float *q, float *out, float *part_o,
+                            float *part_ml, int nch) {
+  AttnArgs aa{};
+  aa.q = q, aa.k = gq_hip_kv_k(c, layer), aa.v = gq_hip_kv_v(c, layer);
+  aa.part_o = part_o, aa.part_ml = part_ml, aa.out = out, aa.pos = pos;
+  aa.n_heads = n_heads, aa.n_kv = c->kv_heads, aa.hd = c->kv_hd, aa.max_seq = c->kv_max_seq;
+  aa.nch = nch, aa.s_max = gq_attn_smax(c->kv_max_seq, nch), aa.scale = 1.0f / sqrtf((float)c->kv_hd);
+  return gq_launch_attention(aa, c->stream, nullptr) ? fail(c, -1, "attention launch (unsupported head_dim/group?)") : 0;
+}
+
+extern "C" int gq_hip_attention_dev(gq_ctx *c, int layer, int pos, int n_heads, const float *q, float *out) {
+  if (int rc = attention_check(c, layer, pos, n_heads, q, out)) return rc;
   Workspace &w = c->ws;
   const int nch = gq_attn_nch(c->kv_heads, c->kv_max_seq);
   const size_t need_o = (size_t)n_heads * nch * c->kv_hd, need_ml = (size_t)n_heads * nch * 2;
@@ -1386,15 +1434,22 @@ extern "C" int gq_hip_attention_dev(gq_ctx *c, int layer, int pos, int n_heads, 
     }
     w.nch = nch;
     w.s_max = gq_attn_smax(c->kv_max_seq, nch);
-  } else if (n_heads != c->m.n_heads) {
-    return fail(c, -1, "attention: n_heads differs from the bound model");
   }
-  AttnArgs aa{};
-  aa.q = q, aa.k = gq_hip_kv_k(c, layer), aa.v = gq_hip_kv_v(c, layer);
-  aa.part_o = w.part_o, aa.part_ml = w.part_ml, aa.out = out, aa.pos = pos;
-  aa.n_heads = n_heads, aa.n_kv = c->kv_heads, aa.hd = c->kv_hd, aa.max_seq = c->kv_max_seq;
-  aa.nch = w.nch, aa.s_max = w.s_max, aa.scale = 1.0f / sqrtf((float)c->kv_hd);
-  return gq_launch_attention(aa, c->stream, nullptr) ? fail(c, -1, "attention launch (unsupported head_dim/group?)") : 0;
+  return attention_launch(c, layer, pos, n_heads, q, out, w.part_o, w.part_ml, w.nch);
+}
+
+extern "C" int gq_hip_attention_dev_noalloc(gq_ctx *c, int layer, int pos, int n_heads, const float *q, float *out) {
+  if (int rc = attention_check(c, layer, pos, n_heads, q, out)) return rc;
+  if (!c->scratch) return fail(c, -4, "attention_noalloc: no scratch address on device %d", c->dev);
+  const int nch = gq_attn_nch(c->kv_heads, c->kv_max_seq);
+  const size_t need_o = (size_t)n_heads * nch * c->kv_hd, need_ml = (size_t)n_heads * nch * 2;
+  const size_t off_ml = (need_o + 63) & ~(size_t)63; /* 256-byte aligned (m, l) pairs */
+  if (off_ml + need_ml > kScratchFloats)
+    return fail(c, -1, "attention_noalloc: %d heads x %d chunks x (head_dim %d + 2) floats exceed the %zu-float scratch",
+                n_heads, nch, c->kv_hd, kScratchFloats);
+  /* nothing in the partials needs to start at zero: the merge reads only
+   * the chunks this launch writes */
+  return attention_launch(c, layer, pos, n_heads, q, out, c->scratch, c->scratch + off_ml, nch);
 }
 
 extern "C" int gq_hip_prefill_attention_dev(gq_ctx *c, int layer, int pos, int T, int n_heads, float *q,

@@ -80,6 +80,7 @@ def _load():
         "gq_hip_rmsnorm_dev": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, C.c_float]),
         "gq_hip_rope_append_dev": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp]),
         "gq_hip_attention_dev": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]),
+        "gq_hip_attention_dev_noalloc": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp]),
         "gq_hip_qkv_rope_dev": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp, C.c_int]),
         "gq_hip_embed_dev": (C.c_int, [_vp, C.c_int, _vp, C.c_int, C.c_int, _vp]),
         "gq_hip_argmax_dev": (C.c_int, [_vp, _vp, C.c_int, _vp]),
@@ -314,6 +315,11 @@ class Context:
 
     def attention_dev(self, layer, pos, n_heads, q_buf, out_buf):
         return lib.gq_hip_attention_dev(self.h, layer, pos, n_heads, q_buf.ptr, out_buf.ptr)
+
+    def attention_dev_noalloc(self, layer, pos, n_heads, q_buf, out_buf):
+        """gq_hip_attention_dev with the partials in the library's static
+        device scratch: no allocation, calls on one GPU must not overlap."""
+        return lib.gq_hip_attention_dev_noalloc(self.h, layer, pos, n_heads, q_buf.ptr, out_buf.ptr)
 
     def prefill_attention_dev(self, layer, pos, T, n_heads, q_buf, k_buf, v_buf, out_buf):
         return lib.gq_hip_prefill_attention_dev(self.h, layer, pos, T, n_heads, q_buf.ptr, k_buf.ptr,

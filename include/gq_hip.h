@@ -237,6 +237,19 @@ int gq_hip_rope_append_dev(gq_ctx *ctx, int layer, int pos, int n_heads, float *
  * (engine.c:433-509): q (n_heads x hd) -> out (n_heads x hd). */
 int gq_hip_attention_dev(gq_ctx *ctx, int layer, int pos, int n_heads, const float *q,
                          float *out);
+/* Allocation-free form of gq_hip_attention_dev.  It has no counterpart in
+ * the reference; it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The split-K partials go to a static 8 MiB device array that
+ * the library holds on every GPU it runs on until the process ends, so the
+ * call allocates nothing.  They take n_heads x nch x (head_dim + 2) floats,
+ * nch = ceil(max_seq / 64) up to max_seq 12288 and ceil(max_seq / 128) past
+ * it (the 8B shape fits up to max_seq 64512); -1 with an error message when
+ * they do not fit.  Every call on one GPU shares that array and leaves its
+ * partials there: calls that overlap on one GPU (other streams or contexts
+ * of the same device) race. */
+int gq_hip_attention_dev_noalloc(gq_ctx *ctx, int layer, int pos, int n_heads, const float *q,
+                                 float *out);
 /* q/k/v projections of a bound layer from a device hidden vector with the
  * layer's RMSNorm, RoPE and K/V append: fused != 0 runs the decode path's
  * single fused epilogue, fused == 0 plain matvecs followed by the standalone
