@@ -466,13 +466,7 @@ __global__ void to_bf16_kernel(const float *x, __bf16 *y, size_t n) {
  * four MFMAs) for Q4_K-only launches whose grid still gives every CU a
  * workgroup (gate/up at 512 tokens), else of 64; then 2 K-splits when the
  * grid has at most one workgroup per CU (a second wave per SIMD comes from
- * the split), 1 when it has more.  GQ_PG_TT and GQ_PG_KS override (for
- * timing). */
-int env_int(const char *name) {
-  const char *e = getenv(name);
-  return e ? atoi(e) : 0;
-}
-
+ * the split), 1 when it has more. */
 int n_cus() {
   static const int cus = [] {
     int dev = 0, n = 0;
@@ -498,15 +492,11 @@ int launch_shape(const PgArgs &a, int row_tiles, size_t lds, hipStream_t s) {
 
 template <int MODE>
 int launch_mode(const PgArgs &a, int row_tiles, hipStream_t s) {
-  static const int force_tt = env_int("GQ_PG_TT"), force_ks = env_int("GQ_PG_KS");
   bool q4 = false, q6 = false;
   for (int i = 0; i < a.nseg; i++) q4 |= a.seg[i].dtype == GQ_Q4_K, q6 |= a.seg[i].dtype == GQ_Q6_K;
-  const int tt = q6                                ? 2
-                 : force_tt == 2 || force_tt == 4 ? force_tt
-                 : row_tiles * ((a.T + 127) / 128) >= n_cus() ? 4
-                                                              : 2;
+  const int tt = !q6 && row_tiles * ((a.T + 127) / 128) >= n_cus() ? 4 : 2;
   const int wgs = row_tiles * ((a.T + 32 * tt - 1) / (32 * tt));
-  int ks = force_ks == 1 || force_ks == 2 ? force_ks : wgs <= n_cus() ? 2 : 1;
+  int ks = wgs <= n_cus() ? 2 : 1;
   if ((a.K / kBK) % 2) ks = 1;
   if (tt == 4) {
     const size_t lds = ks == 2 ? ring_bytes<GQ_Q4_K, 2, 4>() : ring_bytes<GQ_Q4_K, 1, 4>();

@@ -379,6 +379,24 @@ extern "C" int gq_hip_matvec_dev(gq_ctx *c, int dtype, const void *w, int rows, 
   return rc ? fail(c, rc, "matvec launch failed") : 0;
 }
 
+/* y = W (rmsnorm(x) * norm_w) with the RMSNorm fused into the matvec's x
+ * staging, as the decode step runs it before q/k/v, gate/up and the LM head
+ * (cpu_rmsnorm + linear_dispatch, engine.c:356-366, :582-590). */
+extern "C" int gq_hip_matvec_norm_dev(gq_ctx *c, int dtype, const void *w, int rows, int cols,
+                                      const float *x, const float *norm_w, float eps, float *y) {
+  if (!c) return -1;
+  int rc = check_mv(c, dtype, w, rows, cols, 0, x, y);
+  if (rc) return rc;
+  if (!norm_w) return fail(c, -1, "matvec_norm: no norm weight");
+  const uint8_t *mm = op_tile(c, dtype, w, rows, cols);
+  MvArgs a{};
+  a.seg[0] = MvSeg{(const uint8_t *)w, y, nullptr, rows};
+  a.nseg = 1, a.cols = cols, a.x = x, a.norm_w = norm_w, a.eps = eps, a.mm = mm;
+  rc = gq_launch_matvec(dtype, MV_STORE, a, c->stream);
+  if (mm) gq_hip_free(c, (void *)mm);
+  return rc ? fail(c, rc, "matvec_norm launch failed") : 0;
+}
+
 /* ------------------------------------------------------------ KV cache */
 static size_t layer_floats(const gq_ctx *c) {
   return (size_t)c->kv_heads * c->kv_max_seq * c->kv_hd;
@@ -617,6 +635,18 @@ extern "C" int gq_hip_lctx_load(gq_ctx *c, const char *path, int *current_pos, i
   if (tokens) *tokens = tok;
   else free(tok);
   return 0;
+}
+
+/* The frozen-prefix prompt cache (session.c:192-251): the .lctx format with
+ * current_pos = prefix_len and no token history, every layer at the full
+ * max_seq stride; load is kv_cache_load without the tokens. */
+extern "C" int gq_hip_prompt_cache_save(gq_ctx *c, int prefix_len, const char *path) {
+  if (!c || !path || prefix_len <= 0) return fail(c, -1, "prompt_cache_save: bad argument");
+  return gq_hip_lctx_save(c, path, prefix_len, nullptr, 0);
+}
+
+extern "C" int gq_hip_prompt_cache_load(gq_ctx *c, const char *path, int *prefix_len) {
+  return gq_hip_lctx_load(c, path, prefix_len, nullptr, nullptr);
 }
 
 extern "C" int gq_hip_lctx_restore_image(gq_ctx *c, const void *image, size_t size, int *current_pos,

@@ -46,6 +46,7 @@ def _load():
         "gq_hip_synth_norm_weight": (C.c_int, [_vp, _vp, C.c_size_t, C.c_uint64]),
         "gq_hip_matvec": (C.c_int, [_vp, C.c_int, _vp, C.c_int, C.c_int, C.c_size_t, _fp, _fp]),
         "gq_hip_matvec_dev": (C.c_int, [_vp, C.c_int, _vp, C.c_int, C.c_int, _vp, _vp]),
+        "gq_hip_matvec_norm_dev": (C.c_int, [_vp, C.c_int, _vp, C.c_int, C.c_int, _vp, _vp, C.c_float, _vp]),
         "gq_hip_kv_init": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]),
         "gq_hip_kv_k": (_vp, [_vp, C.c_int]),
         "gq_hip_kv_v": (_vp, [_vp, C.c_int]),
@@ -56,6 +57,8 @@ def _load():
         "gq_hip_kv_prefill_synth": (C.c_int, [_vp, C.c_uint64, C.c_uint64, C.c_int]),
         "gq_hip_kv_fetch": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _fp, _fp, C.c_int, C.c_int]),
         "gq_hip_lctx_save": (C.c_int, [_vp, C.c_char_p, C.c_int, C.POINTER(C.c_int32), C.c_int]),
+        "gq_hip_prompt_cache_save": (C.c_int, [_vp, C.c_int, C.c_char_p]),
+        "gq_hip_prompt_cache_load": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_int)]),
         "gq_hip_lctx_load": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_int),
                                        C.POINTER(C.POINTER(C.c_int32)), C.POINTER(C.c_int)]),
         "gq_hip_lctx_restore_image": (C.c_int, [_vp, _vp, C.c_size_t, C.POINTER(C.c_int),
@@ -258,6 +261,10 @@ class Context:
         self.check(lib.gq_hip_matvec_dev(self.h, dtype, w_ptr, rows, cols, x_buf.ptr, y_buf.ptr),
                    "matvec_dev")
 
+    def matvec_norm_dev(self, dtype, w_ptr, rows, cols, x_buf, nw_buf, eps, y_buf):
+        self.check(lib.gq_hip_matvec_norm_dev(self.h, dtype, w_ptr, rows, cols, x_buf.ptr, nw_buf.ptr,
+                                              eps, y_buf.ptr), "matvec_norm_dev")
+
     def rmsnorm_dev(self, x_buf, w_buf, out_buf, dim, eps):
         self.check(lib.gq_hip_rmsnorm_dev(self.h, x_buf.ptr, w_buf.ptr if w_buf else None,
                                           out_buf.ptr, dim, eps), "rmsnorm")
@@ -342,6 +349,14 @@ class Context:
         if n.value > 0:
             C.CDLL(None).free(toks)
         return 0, pos.value, t
+
+    def prompt_cache_save(self, path, prefix_len):
+        return lib.gq_hip_prompt_cache_save(self.h, prefix_len, path.encode())
+
+    def prompt_cache_load(self, path):
+        n = C.c_int(-1)
+        rc = lib.gq_hip_prompt_cache_load(self.h, path.encode(), C.byref(n))
+        return rc, n.value
 
     def lctx_restore_image(self, image_ptr, size):
         pos = C.c_int(-1)

@@ -83,6 +83,11 @@ int gq_hip_matvec(gq_ctx *ctx, int dtype, const void *w_dev, int rows, int cols,
 /* Same, device x / y, asynchronous on the context stream. */
 int gq_hip_matvec_dev(gq_ctx *ctx, int dtype, const void *w_dev, int rows, int cols,
                       const float *x_dev, float *y_dev);
+/* y = W (rmsnorm(x) * norm_w): the reference's cpu_rmsnorm followed by its
+ * matvec (engine.c:356-366, :582-590), with the norm fused into the matvec's
+ * x staging as the decode step runs it.  Device pointers, asynchronous. */
+int gq_hip_matvec_norm_dev(gq_ctx *ctx, int dtype, const void *w_dev, int rows, int cols,
+                           const float *x_dev, const float *norm_w_dev, float eps, float *y_dev);
 
 /* ------------------------------------------------------- KV cache
  * Device-resident fp32 cache in the reference layout
@@ -126,6 +131,12 @@ int gq_hip_lctx_save(gq_ctx *ctx, const char *path, int current_pos, const int32
                      int n_tokens);
 int gq_hip_lctx_load(gq_ctx *ctx, const char *path, int *current_pos, int32_t **tokens,
                      int *n_tokens);
+/* Frozen-prefix prompt cache (prompt_cache_save / prompt_cache_load,
+ * session.c:192-251): the .lctx format with current_pos = prefix_len and
+ * n_tokens = 0, gathered from / restored into the device cache; save
+ * rejects prefix_len <= 0 with -1 as the reference does. */
+int gq_hip_prompt_cache_save(gq_ctx *ctx, int prefix_len, const char *path);
+int gq_hip_prompt_cache_load(gq_ctx *ctx, const char *path, int *prefix_len);
 /* Restore K/V from a .lctx image already in host memory (e.g. pinned),
  * returns the milliseconds the host->device copy took (HIP events). */
 int gq_hip_lctx_restore_image(gq_ctx *ctx, const void *image, size_t size, int *current_pos,

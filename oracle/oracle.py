@@ -333,6 +333,11 @@ class Ref:
                                     C.POINTER(C.c_int), C.POINTER(C.POINTER(C.c_int)),
                                     C.POINTER(C.c_int), C.c_char_p]
         L.kv_cache_load.restype = C.c_int
+        L.prompt_cache_save.argtypes = [C.c_void_p, C.POINTER(RModelConfig), C.c_int, C.c_int, C.c_char_p]
+        L.prompt_cache_save.restype = C.c_int
+        L.prompt_cache_load.argtypes = [C.c_void_p, C.POINTER(RModelConfig), C.c_int,
+                                        C.POINTER(C.c_int), C.c_char_p]
+        L.prompt_cache_load.restype = C.c_int
         L.forward.argtypes = [C.POINTER(RModelWeights), C.c_void_p, C.c_void_p,
                               C.POINTER(C.c_int), C.c_int, C.c_int, C.c_void_p]
         L.forward.restype = C.POINTER(RTensor)

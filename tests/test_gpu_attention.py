@@ -1,6 +1,6 @@
 """Split-K GQA decode attention against the oracle's restatement of the
 reference (engine.c:433-509) on seeded N(0,1) K/V and N(0,1) queries (the
-config-4 setting), at the 8B shape up to 16384 positions (64- and
+config-4 setting), at the 8B shape up to 32768 positions (64- and
 128-position chunks), the TinyLlama shape and edge lengths.  Tolerance:
 relative L2 <= 1e-5."""
 import numpy as np
@@ -23,6 +23,7 @@ pytestmark = pytest.mark.gpu
     (64, 8, 128, 1000, 1024),   # G = 8 at head_dim 128
     (32, 8, 128, 12289, 12400),  # 128-position chunks (caches past 12288)
     (32, 8, 128, 16384, 16384),  # config 4 at ctx 16384, cache exactly full
+    (32, 8, 128, 32768, 32768),  # config 4 at ctx 32768: 256 chunks of 128 in the merge
     (32, 4, 64, 13000, 13000),   # 128-position chunks at head_dim 64
 ])
 def test_attention_vs_oracle(ctx, orc, nh, nkv, hd, L, ms):

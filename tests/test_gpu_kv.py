@@ -104,20 +104,24 @@ def test_lctx_rejects_mismatch(ctx, tmp_path):
     assert ctx.lctx_load(path)[0] == -1
 
 
-@pytest.mark.parametrize("nh,nkv,hd,pos", [(8, 2, 64, 5), (32, 8, 128, 8191), (32, 4, 64, 639)])
-def test_rope_append_bitexact(ctx, orc, nh, nkv, hd, pos):
+@pytest.mark.parametrize("nh,nkv,hd,pos,theta", [
+    (8, 2, 64, 5, 500000.0), (32, 8, 128, 8191, 500000.0), (32, 4, 64, 639, 500000.0),
+    # TinyLlama's rope theta (config 2) at its shape, and at the 8B shape
+    (32, 4, 64, 639, 10000.0), (32, 4, 64, 2047, 10000.0), (32, 8, 128, 4095, 10000.0),
+])
+def test_rope_append_bitexact(ctx, orc, nh, nkv, hd, pos, theta):
     """Fused RoPE + append: rotated q and the cached K row equal the
     reference's rope() + kv_cache_append bit for bit (table from the same fp32
     expressions, no contraction)."""
     ms = pos + 1
-    ctx.kv_init(1, nkv, hd, ms, 500000.0)
+    ctx.kv_init(1, nkv, hd, ms, theta)
     rng = np.random.default_rng(pos)
     q = rng.standard_normal(nh * hd).astype(np.float32) * np.float32(30)
     k = rng.standard_normal(nkv * hd).astype(np.float32) * np.float32(30)
     v = rng.standard_normal(nkv * hd).astype(np.float32)
     qb, kb, vb = ctx.upload(q), ctx.upload(k), ctx.upload(v)
     assert ctx.rope_append_dev(0, pos, nh, qb, kb, vb) == 0
-    q2, k2 = orc.rope(q, k, nh, nkv, hd, pos, 500000.0)
+    q2, k2 = orc.rope(q, k, nh, nkv, hd, pos, theta)
     assert np.array_equal(bits(qb.download()), bits(q2))
     dk, dv = ctx.kv_read_layer(0)
     dk = dk.reshape(nkv, ms, hd)

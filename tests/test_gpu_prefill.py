@@ -101,6 +101,43 @@ def _gemm_case(ctx, orc, dtype, T, N, K, mode):
     xd.free(), yd.free()
 
 
+@pytest.mark.parametrize("dtype,N,K,mode", [
+    (S.Q4_K, 4096, 4096, 0),    # q / o
+    (S.Q4_K, 14336, 4096, 0),   # gate / up
+    (S.Q4_K, 4096, 14336, 1),   # down + residual
+    (S.Q6_K, 4096, 14336, 1),   # the Q6_K down of the Q4_K_M mix
+])
+def test_prefill_gemm_config5_shapes(ctx, orc, dtype, N, K, mode):
+    """Config 5's full 512-token GEMMs on the 8B projection shapes; every
+    token is checked on 384 sampled output rows (first and last included)
+    against the exact-input fp64 reference (1e-5) and the full-precision one
+    (1e-2)."""
+    import guanaco_amd.hip as H
+    T = 512
+    seed = 0xC0F5 ^ (N << 8) ^ K ^ (dtype << 28)
+    print(f"prefill GEMM {T}x{N}x{K} dtype {dtype} mode {mode}", flush=True)
+    w = orc.synth_quant(dtype, seed, N, K)
+    x = orc.synth_normal(seed + 1, T * K).reshape(T, K)
+    r = orc.synth_normal(seed + 2, T * N).reshape(T, N)
+    wd, xd = ctx.upload_weight(w), ctx.upload(x)
+    yd = ctx.upload(r) if mode == 1 else ctx.alloc(4 * T * N)
+    assert H.lib.gq_hip_prefill_gemm_dev(ctx.h, dtype, mode, wd, N, K, xd.ptr, T, yd.ptr,
+                                         yd.ptr if mode == 1 else None) == 0
+    y = yd.download(count=T * N).reshape(T, N)
+    H.lib.gq_hip_free(ctx.h, wd)
+    xd.free(), yd.free()
+    idx = np.unique(np.concatenate([[0, N - 1], np.random.default_rng(seed).choice(N, 382, replace=False)]))
+    ws = np.ascontiguousarray(w.reshape(N, -1)[idx]).reshape(-1)
+    n = idx.size
+    wf = dequant_q4k_f64(ws, n, K) if dtype == S.Q4_K else dequant_q6k_f64(ws, n, K)
+    wk = q4k_dequant_kernel_order(ws, n, K) if dtype == S.Q4_K else wf.astype(np.float32)
+    base = r[:, idx].astype(np.float64) if mode == 1 else 0.0
+    ys = y[:, idx]
+    exact_in = bf16_round(x).astype(np.float64) @ bf16_round(wk).astype(np.float64).T
+    assert rel_l2(ys, base + exact_in) < 1e-5
+    assert rel_l2(ys - base, x.astype(np.float64) @ wf.T) < 1e-2
+
+
 def test_prefill_gemm_rejects_bad_shapes(ctx):
     import guanaco_amd.hip as H
     buf = ctx.alloc(1 << 20)

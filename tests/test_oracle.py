@@ -245,6 +245,34 @@ def test_lctx_bytes_match_reference(orc, ref, tmp_path):
     rm.close()
 
 
+def test_prompt_cache_bytes_match_reference(orc, ref, tmp_path):
+    """prompt_cache_save's file (session.c:192-237) is the oracle's .lctx
+    image with current_pos = prefix_len and no tokens; prefix_len <= 0 is
+    refused; prompt_cache_load returns prefix_len and the K/V."""
+    import ctypes as C
+    from oracle import u8ptr
+    hm = HostModel(orc, S.TINY_TEST, 32)
+    rm = RefModel(ref, hm)
+    kv = hm.new_kv()
+    kv.prefill(orc, S.TINY_TEST, 13)
+    rm.load_kv(kv)
+    path = str(tmp_path / "p.lctx")
+    assert ref.lib.prompt_cache_save(rm.kv, C.byref(rm.mw.config), 32, 0, path.encode()) == -1
+    assert ref.lib.prompt_cache_save(rm.kv, C.byref(rm.mw.config), 32, 13, path.encode()) == 0
+    n = orc.lib.orc_lctx_size(C.byref(kv.s), 0)
+    img = np.zeros(n, np.uint8)
+    orc.lib.orc_lctx_write(C.byref(kv.s), 13, None, 0, u8ptr(img), n)
+    assert np.array_equal(np.fromfile(path, np.uint8), img)
+    for l in range(S.TINY_TEST.n_layers):
+        rm.slab("k", l)[:] = 0
+    got = C.c_int(-1)
+    assert ref.lib.prompt_cache_load(rm.kv, C.byref(rm.mw.config), 32, C.byref(got), path.encode()) == 0
+    assert got.value == 13
+    n1 = kv.k.size // S.TINY_TEST.n_layers
+    assert np.array_equal(rm.slab("k", 1), kv.k[n1:2 * n1])
+    rm.close()
+
+
 def test_forward_bitexact_vs_reference(orc, ref):
     """Whole decode steps: the oracle's logits equal the reference forward()'s."""
     hm = HostModel(orc, S.TINY_TEST, 64)
