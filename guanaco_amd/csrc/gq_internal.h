@@ -108,11 +108,20 @@ __device__ __forceinline__ void gq_mv_locate(const MvSegs &v, int gr, int &s, in
     if (v.nseg > 2 && lr >= v.n1) lr -= v.n1, s = 2;
   }
 }
-__device__ __forceinline__ const uint8_t *gq_mv_w(const MvSegs &v, int s) { return s == 0 ? v.w0 : s == 1 ? v.w1 : v.w2; }
-__device__ __forceinline__ float *gq_mv_y(const MvSegs &v, int s) { return s == 0 ? v.y0 : s == 1 ? v.y1 : v.y2; }
-__device__ __forceinline__ const float *gq_mv_r(const MvSegs &v, int s) { return s == 0 ? v.r0 : s == 1 ? v.r1 : v.r2; }
-__device__ __forceinline__ int gq_mv_rows(const MvSegs &v, int s) { return s == 0 ? v.n0 : s == 1 ? v.n1 : v.n2; }
-__device__ __forceinline__ int gq_mv_kind(const MvSegs &v, int s) { return s == 0 ? v.k0 : s == 1 ? v.k1 : v.k2; }
+/* A field of segment s.  The three values are pinned in registers before
+ * the select: a select between fields of the struct would otherwise be
+ * folded into a load at a computed offset, which keeps the struct in
+ * scratch memory for the whole launch. */
+template <class T>
+__device__ __forceinline__ T gq_mv_sel(T a, T b, T c, int s) {
+  a = gq_pin(a), b = gq_pin(b), c = gq_pin(c);
+  return s == 0 ? a : s == 1 ? b : c;
+}
+__device__ __forceinline__ const uint8_t *gq_mv_w(const MvSegs &v, int s) { return gq_mv_sel(v.w0, v.w1, v.w2, s); }
+__device__ __forceinline__ float *gq_mv_y(const MvSegs &v, int s) { return gq_mv_sel(v.y0, v.y1, v.y2, s); }
+__device__ __forceinline__ const float *gq_mv_r(const MvSegs &v, int s) { return gq_mv_sel(v.r0, v.r1, v.r2, s); }
+__device__ __forceinline__ int gq_mv_rows(const MvSegs &v, int s) { return gq_mv_sel(v.n0, v.n1, v.n2, s); }
+__device__ __forceinline__ int gq_mv_kind(const MvSegs &v, int s) { return gq_mv_sel(v.k0, v.k1, v.k2, s); }
 
 /* Any dtype and shape the reference's matvec takes (cols % 256, Q8_0
  * cols % 32): the matrix-core kernel where the path setting picks it and

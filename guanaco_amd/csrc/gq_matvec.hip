@@ -603,21 +603,22 @@ __global__ __launch_bounds__(NW * GQ_WAVE) void mvm_kernel(MvArgs a, MmPlan pl) 
     }
   }
   __syncthreads();
-  /* the parked rows go out */
+  /* the parked rows go out: wave w stores tiles w, w + NW, ..., so the
+   * segment of a tile is uniform across the wave */
   const int prow = MODE == MV_SWIGLU ? 8 : 16;
-  for (int i = threadIdx.x; i < mytiles * 16; i += NW * GQ_WAVE) {
-    const int tl = i >> 4, r = i & 15, t = bid + tl * nblk;
-    if (r >= prow) continue;
+  for (int tl = wave; tl < mytiles; tl += NW) {
+    const int t = bid + tl * nblk, r = lane;
     int s = 0, lr = 8 * t + r;
     if (MODE != MV_SWIGLU) {
       gq_mv_locate(sv, 16 * t, s, lr);
-      lr += r;
-      if (lr >= gq_mv_rows(sv, s)) continue;
-    } else if (lr >= pl.total) {
+      s = __builtin_amdgcn_readfirstlane(s);
+      lr = __builtin_amdgcn_readfirstlane(lr) + r;
+      if (r >= prow || lr >= gq_mv_rows(sv, s)) continue;
+    } else if (r >= prow || lr >= pl.total) {
       continue;
     }
     float *dst = rdest<MODE>(a, sv, s, lr, pos);
-    if (dst) gst<float>(dst, park[i]);
+    if (dst) gst<float>(dst, park[16 * tl + r]);
   }
 }
 

@@ -515,7 +515,9 @@ int rows_out(const MvArgs &a, int mode) {
  * group from the measured shapes (8B decode on MI355X): 8 for launches of
  * >= 4096 output rows (4096 x 4096 Q4_K: 4.7 us against 4.8 with 4), 6 for
  * such Q6_K launches (four waves per SIMD; down 15 us against 18 at three),
- * else 4 (1024-row Q6_K v: 3.6 us against 4.3 with 8). */
+ * else 4 (1024-row Q6_K v: 3.6 us against 4.3 with 8); in 1024-thread
+ * launches (rows of more than 16384 columns) 4 for Q4_K and 2 for Q6_K and
+ * Q8_0, whose 4-row groups spill past the 128 VGPRs such launches allow. */
 void plan(int dt, int mode, const MvArgs &a, int total, MxPlan &p, int &r, int &segw, int &maxnt) {
   p.upr = a.cols / 32;
   p.nt = (p.upr + 1023) / 1024;
@@ -524,7 +526,9 @@ void plan(int dt, int mode, const MvArgs &a, int total, MxPlan &p, int &r, int &
   p.G = p.L <= 128 ? 256 / p.L : 1;
   const int nt = p.G * p.L;
   maxnt = nt <= 256 ? 256 : nt <= 512 ? 512 : 1024;
-  if (maxnt == 1024 || dt == GQ_Q8_0)
+  if (maxnt == 1024)
+    r = dt == GQ_Q4_K ? 4 : 2; /* 1024 threads leave 128 VGPRs: 4 rows of Q6_K or Q8_0 spill */
+  else if (dt == GQ_Q8_0)
     r = 4;
   else if (dt == GQ_Q6_K && total >= 4096)
     r = 6; /* 8 rows of Q6_K quants do not fit 128 VGPRs */
@@ -536,7 +540,10 @@ void plan(int dt, int mode, const MvArgs &a, int total, MxPlan &p, int &r, int &
         if (a.seg[i].rows % rr) return false;
       return true;
     };
-    if (!fits(r)) r = fits(4) ? 4 : fits(6) && maxnt != 1024 && dt != GQ_Q8_0 ? 6 : 0;
+    if (!fits(r)) {
+      if (maxnt == 1024 && dt != GQ_Q4_K) r = fits(2) ? 2 : 0;
+      else r = fits(4) ? 4 : fits(6) && maxnt != 1024 && dt != GQ_Q8_0 ? 6 : 0;
+    }
   }
   p.total = total;
   const int per = mode == MV_SWIGLU ? r / 2 : r;
@@ -572,13 +579,14 @@ int launch_fl(const MvArgs &a, const MxPlan &p, hipStream_t s) {
 template <int DT, int MODE, int R>
 int launch_r(const MvArgs &a, const MxPlan &p, int segw, int maxnt, hipStream_t s) {
   if (maxnt == 1024) {
-    if constexpr (R == 4) {
+    if constexpr ((R == 4 && DT == GQ_Q4_K) || (R == 2 && DT != GQ_Q4_K)) {
       if (p.nt > 1)
-        return segw == 16 ? launch_fl<DT, MODE, 4, 16, 1024, kMT>(a, p, s) : launch_fl<DT, MODE, 4, 8, 1024, kMT>(a, p, s);
-      return segw == 16 ? launch_fl<DT, MODE, 4, 16, 1024, 0>(a, p, s) : launch_fl<DT, MODE, 4, 8, 1024, 0>(a, p, s);
+        return segw == 16 ? launch_fl<DT, MODE, R, 16, 1024, kMT>(a, p, s) : launch_fl<DT, MODE, R, 8, 1024, kMT>(a, p, s);
+      return segw == 16 ? launch_fl<DT, MODE, R, 16, 1024, 0>(a, p, s) : launch_fl<DT, MODE, R, 8, 1024, 0>(a, p, s);
     }
     return -1;
   }
+  if constexpr (R == 2) return -1;
   if (maxnt == 512)
     return segw == 16 ? launch_fl<DT, MODE, R, 16, 512, 0>(a, p, s) : launch_fl<DT, MODE, R, 8, 512, 0>(a, p, s);
   return segw == 16 ? launch_fl<DT, MODE, R, 16, 256, 0>(a, p, s) : launch_fl<DT, MODE, R, 8, 256, 0>(a, p, s);
@@ -600,10 +608,12 @@ int launch_mvx(const MvArgs &a, int total, hipStream_t s) {
     return 0;
   }
   if constexpr (DT == GQ_Q8_0) {
-    return launch_r<DT, MODE, 4>(a, p, segw, maxnt, s);
+    return r == 2 ? launch_r<DT, MODE, 2>(a, p, segw, maxnt, s) : launch_r<DT, MODE, 4>(a, p, segw, maxnt, s);
   } else {
     if (r == 8) return launch_r<DT, MODE, 8>(a, p, segw, maxnt, s);
     if (r == 6) return launch_r<DT, MODE, 6>(a, p, segw, maxnt, s);
+    if constexpr (DT == GQ_Q6_K)
+      if (r == 2) return launch_r<DT, MODE, 2>(a, p, segw, maxnt, s);
     return launch_r<DT, MODE, 4>(a, p, segw, maxnt, s);
   }
 }

@@ -94,9 +94,26 @@ TINYLLAMA = ModelSpec("tinyllama-1.1b-shape", n_layers=22, hidden=2048, ff=5632,
                       n_heads=32, n_kv_heads=4, vocab=32000,
                       layer_dtypes=dict(wv=Q6_K, wd=Q6_K))
 
+# TinyLlama shape with every weight Q8_0 (embedding and LM head included):
+# zero-mean weights.  The Q4_K generator's weights have a positive mean
+# (d sc q - dmin m with q in 0..15), which gives every hidden state a large
+# common component; the LM head then ranks tokens by a fixed per-row bias and
+# the greedy chain repeats one or two tokens.  This variant's tokens vary at
+# every step with top-2 margins of O(1)-O(10) on logits of standard
+# deviation ~100, so token identity discriminates.
+TINYLLAMA_Q8 = ModelSpec("tinyllama-1.1b-shape-q8_0", n_layers=22, hidden=2048, ff=5632,
+                         n_heads=32, n_kv_heads=4, vocab=32000,
+                         layer_dtypes={k: Q8_0 for k in LAYER_WEIGHTS}, embed_dtype=Q8_0,
+                         lm_head_dtype=Q8_0)
+
 # small model used by the quick parity tests: same mixed-dtype rule as the 8B
 # shape, GQA 4:1 like both presets, head_dim 64
 TINY_TEST = ModelSpec("tiny-test", n_layers=2, hidden=512, ff=1024, n_heads=8,
                       n_kv_heads=2, vocab=1000, layer_dtypes=_q6k_on_even)
 
-PRESETS = {s.name: s for s in (LLAMA8B, TINYLLAMA, TINY_TEST)}
+# the tiny model with a 28672-wide FFN (Llama-2-70B's ff): the down
+# projection's rows are longer than 16384 columns
+WIDE_FF_TEST = ModelSpec("wide-ff-test", n_layers=2, hidden=512, ff=28672, n_heads=8,
+                         n_kv_heads=2, vocab=1000, layer_dtypes=_q6k_on_even)
+
+PRESETS = {s.name: s for s in (LLAMA8B, TINYLLAMA, TINYLLAMA_Q8, TINY_TEST, WIDE_FF_TEST)}

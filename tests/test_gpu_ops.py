@@ -39,6 +39,10 @@ SHAPES = [
     (Q6_K, 1, 256), (Q6_K, 8, 512), (Q6_K, 64, 1024), (Q6_K, 37, 5632), (Q6_K, 1024, 4096),
     (Q6_K, 4096, 4096), (Q6_K, 301, 14336), (Q6_K, 2048, 5632),
     (Q8_0, 1, 32), (Q8_0, 8, 512), (Q8_0, 33, 1024), (Q8_0, 64, 4096),
+    # rows longer than 16384 columns: 1024-thread groups (28672: an ff-28672
+    # down projection), then several column tiles per lane (40960, 65536)
+    (Q4_K, 64, 28672), (Q6_K, 64, 28672), (Q8_0, 40, 28672),
+    (Q4_K, 33, 65536), (Q6_K, 48, 40960), (Q8_0, 24, 40960),
 ]
 
 

@@ -117,6 +117,54 @@ def test_reference_engine_through_hip_vtable(host, ref, orc):
 
 
 @pytest.mark.gpu
+def test_wide_ff_through_hip_vtable_and_bound_decode(host, ref, orc):
+    """ff = 28672 (down rows of 28672 columns, Q6_K and Q4_K; the
+    reference's matvec takes any cols % 256, quant_matvec_q4_k.c:143-158):
+    every weight device-resident, the reference's forward() through the HIP
+    vtable (linear_dispatch, engine.c:119-152) and the device decode of the
+    bound model (fused SwiGLU and residual launches at that width) both
+    match the all-CPU reference."""
+    import guanaco_amd.hip as H
+    from oracle import RModelWeights
+    spec, ms, pre = S.WIDE_FF_TEST, 32, 9
+    b = host.backend_create(C.byref(RBackendConfig(BACKEND_HIP, 4, 0, spec.n_layers)))
+    assert b, "HIP backend unavailable on a GPU box"
+    host.hip_backend_bind_model.argtypes = [C.c_void_p, C.POINTER(RModelWeights), C.c_void_p]
+    hm = HostModel(orc, spec, ms)
+    cpu, gpu = RefModel(ref, hm), RefModel(ref, hm)
+    kv = hm.new_kv()
+    kv.prefill(orc, spec, pre)
+    cpu.load_kv(kv)
+    gpu.load_kv(kv)
+    for l in range(spec.n_layers):
+        for f in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down"):
+            assert host.hip_backend_upload(b, getattr(gpu.mw.layers[l], f)) == 0
+            assert getattr(gpu.mw.layers[l], f).contents.device_residency == 1
+    assert gpu.mw.layers[0].w_down.contents.shape[1] == 28672
+    assert host.hip_backend_upload(b, gpu.mw.lm_head) == 0
+    hip_vt = C.cast(host.backend_kernels(b), C.c_void_p)
+    tok_c = tok_g = 5
+    for step in range(2):
+        tok_c, lc = cpu.forward(tok_c, pre + step)
+        out = ref.lib.forward(C.byref(gpu.mw), gpu.kv, gpu.scratch, (C.c_int * 1)(tok_g), 1,
+                              pre + step, hip_vt)
+        lg = np.ctypeslib.as_array(C.cast(out.contents.data, C.POINTER(C.c_float)),
+                                   shape=(spec.vocab,)).copy()
+        tok_g = int(ref.lib.sample_greedy(fptr(lg), spec.vocab))
+        assert rel_l2(lg, lc) < 1e-3 and tok_g == tok_c, step
+    # the bound model decodes the next step on the device from the same cache
+    assert host.hip_backend_bind_model(b, C.byref(gpu.mw), gpu.kv) == 0
+    t_c, lc = cpu.forward(tok_c, pre + 2)
+    ld = np.empty(spec.vocab, np.float32)
+    t_d = H.lib.gq_hip_forward_token(host.hip_backend_context(b), tok_c, pre + 2,
+                                     ld.ctypes.data_as(C.POINTER(C.c_float)), None)
+    assert rel_l2(ld, lc) < 1e-3 and t_d == t_c
+    cpu.close()
+    gpu.close()
+    host.backend_destroy(b)
+
+
+@pytest.mark.gpu
 def test_bind_model_and_gpu_prefill_slot(host, ref, orc):
     """The whole model bound from the reference's own ModelWeights
     (hip_backend_bind_model) and the gpu_prefill slot (hip_backend_prefill,
