@@ -22,7 +22,7 @@
 #include <stdlib.h>
 #include <string.h>
 
-#include "../../include/gq_hip.h"
+#include "gq_hip.h"
 
 typedef struct {
   gq_ctx *ctx;
@@ -98,8 +98,7 @@ struct gq_ctx *hip_backend_context(const Backend *b) {
   return ((HipImpl *)b->impl)->ctx;
 }
 
-int hip_backend_upload(Backend *b, Tensor *t) {
-  gq_ctx *ctx = hip_backend_context(b);
+static int upload_to(gq_ctx *ctx, Tensor *t) {
   if (!t) return -1;
   if (!ctx || !t->data || !t->byte_size ||
       (t->dtype != DTYPE_Q4_K && t->dtype != DTYPE_Q6_K && t->dtype != DTYPE_Q8_0)) {
@@ -115,6 +114,8 @@ int hip_backend_upload(Backend *b, Tensor *t) {
   t->device_residency = 1;
   return 0;
 }
+
+int hip_backend_upload(Backend *b, Tensor *t) { return upload_to(hip_backend_context(b), t); }
 
 int hip_backend_finish(Backend *b) {
   gq_ctx *ctx = hip_backend_context(b);
@@ -215,3 +216,33 @@ int hip_backend_prefill(const Backend *backend, ModelWeights *model, KVCache *kv
       return -1;
   return 0;
 }
+
+/* ------------------------------------------------------------ engine and loader hooks
+ * transformer_layer and load_model see no Backend, as the CUDA build's
+ * direct hooks do not (cuda_upload_weight, cuda_transformer_layer_gpu,
+ * cuda_sync_kv_cache, cuda_finish_layer): these act on the live HIP
+ * backend. */
+
+int hip_upload_weight(Tensor *t) { return upload_to(g_hip ? g_hip->ctx : NULL, t); }
+
+int hip_layer_ready(const LayerWeights *lw) {
+  if (!g_hip || !lw) return 0;
+  const Tensor *t[7] = {lw->wq, lw->wk, lw->wv, lw->wo, lw->w_gate, lw->w_up, lw->w_down};
+  for (int i = 0; i < 7; i++)
+    if (!t[i] || t[i]->device_residency != 1 || !t[i]->d_data) return 0;
+  return 1;
+}
+
+int hip_backend_layer(int layer, int pos, float *hidden, KVCache *kv) {
+  if (!g_hip || !hidden || !kv) return -1;
+  return gq_hip_transformer_layer(g_hip->ctx, layer, pos, hidden, kv_cache_raw_k(kv, layer),
+                                  kv_cache_raw_v(kv, layer), kv_cache_head_stride(kv));
+}
+
+int hip_backend_kv_sync(KVCache *kv, int layer, int pos, int T, int max_seq) {
+  if (!g_hip || !kv) return -1;
+  return gq_hip_kv_sync(g_hip->ctx, layer, pos, T, kv_cache_raw_k(kv, layer), kv_cache_raw_v(kv, layer),
+                        kv_cache_head_stride(kv), max_seq);
+}
+
+int hip_backend_sync(void) { return g_hip ? gq_hip_sync(g_hip->ctx) : 0; }

@@ -40,4 +40,30 @@ int hip_backend_bind_model(Backend *b, ModelWeights *mw, KVCache *kv);
 int hip_backend_prefill(const Backend *backend, ModelWeights *model, KVCache *kv, Scratch *scr,
                         const int *token_ids, int n_tokens, int pos);
 
+/* ---- engine and loader hooks (no Backend argument: the live HIP backend,
+ * as the CUDA build's direct hooks use its global device state) ---- */
+
+/* The loader's upload (cuda_upload_weight, loader.c:701-728): Q4_K, Q6_K and
+ * Q8_0 go to the device (d_data, device_residency 1); anything else, or a
+ * failure, leaves the tensor CPU-resident (device_residency 0), -1. */
+int hip_upload_weight(Tensor *t);
+
+/* 1 when a HIP backend is live and all seven projections of the layer are
+ * device-resident (the IS_GPU_READY test of engine.c:324-328). */
+int hip_layer_ready(const LayerWeights *lw);
+
+/* One decode step (T = 1) of `layer` on the device, as engine.c:330-349 runs
+ * cuda_transformer_layer_gpu: hidden (host, hidden_dim floats) in and out,
+ * the new K/V row written to the device cache and to the host cache slabs.
+ * Needs hip_backend_bind_model.  0, or non-zero for the CPU path. */
+int hip_backend_layer(int layer, int pos, float *hidden, KVCache *kv);
+
+/* After the CPU path appended T rows at pos of a device-resident layer (a
+ * prompt, or a device error), copy them to the device cache
+ * (cuda_sync_kv_cache, engine.c:394-405). */
+int hip_backend_kv_sync(KVCache *kv, int layer, int pos, int T, int max_seq);
+
+/* Wait for queued device work before a CPU layer (cuda_finish_layer). */
+int hip_backend_sync(void);
+
 #endif

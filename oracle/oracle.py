@@ -299,10 +299,11 @@ def ref_available():
 class Ref:
     """The reference CPU path (compiled, unmodified) — pins the oracle."""
 
-    def __init__(self, threads=8):
-        if not ref_available():
-            raise FileNotFoundError(REF_SO)
-        L = self.lib = C.CDLL(REF_SO, mode=C.RTLD_GLOBAL)
+    def __init__(self, threads=8, path=REF_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        # only the unmodified reference goes into the global namespace
+        L = self.lib = C.CDLL(path, mode=C.RTLD_GLOBAL if path == REF_SO else C.RTLD_LOCAL)
         for n in ("matvec_q4k_f32", "matvec_q6k_f32", "matvec_q8_0_f32"):
             getattr(L, n).argtypes = [C.POINTER(RTensor), _fp, _fp]
             getattr(L, n).restype = C.c_int

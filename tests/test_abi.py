@@ -37,16 +37,52 @@ def test_no_device_means_null_context():
         H.Context(0)
 
 
-def test_host_backend_exports(ref):
-    """libgq_host.so (the HIP backend behind the reference's KernelVTable)
-    exports the reference's factory (backend.h:41-52) and every hook
-    guanaco_amd/host/include/hip_backend.h declares.  Its CPU backend is
-    resolved from the reference's objects, so libref.so is loaded first."""
-    src = open(os.path.join(ROOT, "guanaco_amd", "host", "include", "hip_backend.h")).read()
+def test_reference_patch_applies_and_builds(tmp_path):
+    """The drop-in as a maintainer applies it: guanaco_amd/host/reference-hip.patch
+    applies to the reference's src/ tree as it is, and with hip_backend.c /
+    .h added the tree compiles with -DUSE_HIP=1 (the HIP backend under
+    -Wall -Wextra -Werror) into the engine library and the command-line
+    program, which export the factory (backend.h:41-52) and every hook
+    hip_backend.h declares."""
+    import subprocess
+    from oracle import ref_available
+    if not ref_available():
+        pytest.skip("reference sources / oracle/_ref not present")
+    out = tmp_path / "ref_hip"
+    r = subprocess.run(["sh", os.path.join(ROOT, "oracle", "build_ref_hip.sh"), str(out)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    src = open(os.path.join(ROOT, "guanaco_amd", "host", "hip_backend.h")).read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
-    names = sorted(set(re.findall(r"\b(hip_backend_\w+)\s*\(", src)))
-    assert {"hip_backend_upload", "hip_backend_bind_model", "hip_backend_prefill"} <= set(names)
-    lib = ctypes.CDLL(os.path.join(ROOT, "guanaco_amd", "libgq_host.so"))
-    missing = [n for n in names + ["backend_create", "backend_kernels", "backend_destroy"]
+    names = sorted(set(re.findall(r"\b(hip_\w+|backend_hip_\w+)\s*\(", src)))
+    assert {"hip_backend_upload", "hip_backend_bind_model", "hip_backend_prefill", "hip_layer_ready",
+            "hip_backend_layer", "hip_backend_kv_sync", "hip_upload_weight"} <= set(names)
+    lib = ctypes.CDLL(str(out / "libref_hip.so"))
+    missing = [n for n in names + ["backend_create", "backend_kernels", "backend_destroy", "backend_hip_create",
+                                   "forward", "transformer_layer", "gpu_prefill", "kv_cache_load"]
                if not hasattr(lib, n)]
     assert not missing, missing
+    patched = {l.split()[1][2:] for l in open(os.path.join(ROOT, "guanaco_amd", "host", "reference-hip.patch"))
+               if l.startswith("+++ ")}
+    assert {"backend/backend.c", "backend/backend_internal.h", "include/backend.h", "include/tokenizer.h",
+            "tokenizer/tokenizer.c", "main.c", "engine/loader.c", "engine/engine.c", "engine/generate.c",
+            "engine/chat.c", "engine/gpu_prefill.c"} <= patched
+
+
+def test_patched_cli_device_switch(tmp_path):
+    """--device hip in the patched command line (tokenizer.c:337-343,
+    :385-392, :420-433; main.c:14-42): an unknown kind is refused and names
+    hip among the kinds; without a GPU the HIP backend request fails with a
+    message instead of falling back."""
+    import subprocess
+    cli = os.path.join(ROOT, "oracle", "_ref", "guanaco_hip")
+    if not os.path.exists(cli):
+        pytest.skip("oracle/_ref/guanaco_hip not built")
+    r = subprocess.run([cli, "--device", "bogus", "--model", "x"], capture_output=True, text=True, cwd=tmp_path)
+    assert r.returncode == 1 and "auto|cpu|cuda|hip" in r.stderr
+    import guanaco_amd.hip as H
+    if H.device_count() > 0:
+        pytest.skip("a GPU is present")
+    r = subprocess.run([cli, "--device", "hip", "--model", str(tmp_path / "none.gguf")], capture_output=True,
+                       text=True, cwd=tmp_path)
+    assert "HIP backend requested but unavailable" in r.stderr

@@ -281,6 +281,31 @@ def test_prefill_model_vs_oracle(ctx, orc, pre, T, ms):
     print(f"prefill T={T} pre={pre}: logits rel {rel_l2(lg, lc):.2e}, device {ms_dev:.3f} ms")
 
 
+def test_prefill_after_rebinding_larger_models(orc):
+    """One context binds a small model and prefills, then binds models with
+    a wider FFN and a wider hidden size and prefills again: the prefill
+    workspace is sized for the model bound last (it had kept the first
+    model's sizes), each prompt against the oracle."""
+    import guanaco_amd.hip as H
+    from oracle import HostModel
+    wide_h = S.ModelSpec("tiny-wide-hidden", n_layers=2, hidden=1024, ff=2048, n_heads=16, n_kv_heads=4,
+                         vocab=1000, layer_dtypes=S._q6k_on_even)
+    c = H.Context(0)
+    try:
+        for spec in (S.TINY_TEST, S.WIDE_FF_TEST, wide_h, S.TINY_TEST):
+            print(f"prefill on a rebound context: {spec.name}", flush=True)
+            hm = HostModel(orc, spec, 64)
+            dm = H.DeviceModel(c, spec, 64)
+            toks = np.random.default_rng(spec.hidden + spec.ff).integers(0, spec.vocab, 40).astype(np.int32)
+            nxt, lg, _, _ = dm.prefill(toks, 0)
+            kv = hm.new_kv()
+            for t in range(len(toks)):
+                t_cpu, lc, _ = hm.forward(kv, int(toks[t]), t)
+            assert rel_l2(lg, lc) < PF_TOL and nxt == t_cpu, spec.name
+    finally:
+        c.close()
+
+
 def test_prefill_token_by_token_fallback(ctx, orc):
     """A model whose Q6_K projections have cols % 512 != 0 (hidden 768) is
     not taken by the GEMM: the prefill runs the decode step per token, so

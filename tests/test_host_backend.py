@@ -1,4 +1,5 @@
-"""BACKEND_HIP behind the reference's KernelVTable (guanaco_amd/host).
+"""BACKEND_HIP behind the reference's KernelVTable (guanaco_amd/host), in
+the reference built with guanaco_amd/host/reference-hip.patch applied.
 
 The CPU tests check the factory conventions of backend.c:5-66 and
 test_backend.c: a HIP request without a device is NULL, AUTO falls back to
@@ -19,7 +20,9 @@ from guanaco_amd import spec as S
 from util import rel_l2
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HOST_SO = os.path.join(ROOT, "guanaco_amd", "libgq_host.so")
+# the reference with the HIP backend dropped in (oracle/build_ref_hip.sh):
+# the patched factory, engine and loader plus hip_backend.c
+HOST_SO = os.path.join(ROOT, "oracle", "_ref", "libref_hip.so")
 BACKEND_AUTO, BACKEND_CPU, BACKEND_HIP = -1, 0, 2
 
 
@@ -31,6 +34,8 @@ class VTable(C.Structure):  # backend.h:20-39
 
 @pytest.fixture(scope="module")
 def host(ref):
+    if not os.path.exists(HOST_SO):
+        pytest.skip("oracle/_ref/libref_hip.so not built (reference sources absent)")
     lib = C.CDLL(HOST_SO)
     lib.backend_create.argtypes = [C.POINTER(RBackendConfig)]
     lib.backend_create.restype = C.c_void_p
@@ -264,3 +269,88 @@ def test_n_gpu_layers_split(host, ref, orc):
     cpu.close()
     mix.close()
     host.backend_destroy(b)
+
+
+@pytest.fixture(scope="module")
+def ref_hip(ref):
+    from oracle import Ref
+    if not os.path.exists(HOST_SO):
+        pytest.skip("oracle/_ref/libref_hip.so not built")
+    r = Ref(threads=4, path=HOST_SO)
+    r.lib.hip_upload_weight.argtypes = [C.POINTER(RTensor)]
+    r.lib.hip_backend_bind_model.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p]
+    return r
+
+
+def _logits(out, vocab):
+    return np.ctypeslib.as_array(C.cast(out.contents.data, C.POINTER(C.c_float)), shape=(vocab,)).copy()
+
+
+@pytest.mark.gpu
+def test_patched_engine_prompt_then_device_decode(ref, ref_hip, orc, tmp_path):
+    """The reference's own engine with the patch: layer 0 device-resident
+    through the loader's hook (hip_upload_weight), the model bound, then
+
+    * a 7-token prompt through the patched forward(): T > 1 takes the CPU
+      path, whose new rows of the device-resident layer go to the device
+      cache (hip_backend_kv_sync, as cuda_sync_kv_cache at engine.c:394-405);
+    * decode steps: layer 0 runs on the device (hip_backend_layer, reading
+      those prompt rows from the device cache), layer 1 on the CPU;
+    * the session saved by kv_cache_save, loaded into a fresh cache by
+      kv_cache_load and the model bound again after the restore (the
+      generate.c order): the device cache carries the restored prefix.
+
+    Each step's logits within 1e-3 of the all-CPU reference and the same
+    greedy token."""
+    from oracle import HostModel, RModelWeights
+    spec, ms, pre = S.TINY_TEST, 64, 24
+    lib = ref_hip.lib
+    b = lib.backend_create(C.byref(RBackendConfig(BACKEND_HIP, 4, 0, 1)))
+    assert b, "HIP backend unavailable on a GPU box"
+    lib.backend_kernels.restype = C.c_void_p
+    hip_vt = C.c_void_p(lib.backend_kernels(b))
+    hm = HostModel(orc, spec, ms)
+    cpu, mix = RefModel(ref, hm), RefModel(ref_hip, hm)
+    kv = hm.new_kv()
+    kv.prefill(orc, spec, pre)
+    cpu.load_kv(kv)
+    mix.load_kv(kv)
+    for f in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down"):  # --n-gpu-layers 1
+        assert lib.hip_upload_weight(getattr(mix.mw.layers[0], f)) == 0
+    lib.hip_layer_ready.argtypes = [C.c_void_p]
+    assert lib.hip_layer_ready(C.addressof(mix.mw.layers[0])) == 1
+    assert lib.hip_layer_ready(C.addressof(mix.mw.layers[1])) == 0
+    assert lib.hip_backend_bind_model(b, C.addressof(mix.mw), mix.kv) == 0
+    prompt = np.random.default_rng(3).integers(0, spec.vocab, 7).astype(np.int32)
+    pc = (C.c_int * 7)(*[int(t) for t in prompt])
+    lc = _logits(ref.lib.forward(C.byref(cpu.mw), cpu.kv, cpu.scratch, pc, 7, pre, ref.vtable), spec.vocab)
+    lm = _logits(lib.forward(C.byref(mix.mw), mix.kv, mix.scratch, pc, 7, pre, hip_vt), spec.vocab)
+    assert rel_l2(lm, lc) < 1e-3
+    tok = int(ref.lib.sample_greedy(fptr(lc), spec.vocab))
+    pos = pre + 7
+    for step in range(4):
+        t_c, lc = cpu.forward(tok, pos)
+        lm = _logits(lib.forward(C.byref(mix.mw), mix.kv, mix.scratch, (C.c_int * 1)(tok), 1, pos, hip_vt),
+                     spec.vocab)
+        t_m = int(ref.lib.sample_greedy(fptr(lm), spec.vocab))
+        assert rel_l2(lm, lc) < 1e-3 and t_m == t_c, step
+        tok, pos = t_c, pos + 1
+    # the session through the reference's files, restored, then bound again
+    path = str(tmp_path / "s.lctx")
+    assert lib.kv_cache_save(mix.kv, C.byref(mix.mw.config), ms, pos, None, 0, path.encode()) == 0
+    rest = RefModel(ref_hip, hm)
+    for f in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down"):
+        assert lib.hip_upload_weight(getattr(rest.mw.layers[0], f)) == 0
+    got = C.c_int(-1)
+    assert lib.kv_cache_load(rest.kv, C.byref(rest.mw.config), ms, C.byref(got), None, None, path.encode()) == 0
+    assert got.value == pos
+    assert lib.hip_backend_bind_model(b, C.addressof(rest.mw), rest.kv) == 0
+    for step in range(3):
+        t_c, lc = cpu.forward(tok, pos)
+        lm = _logits(lib.forward(C.byref(rest.mw), rest.kv, rest.scratch, (C.c_int * 1)(tok), 1, pos, hip_vt),
+                     spec.vocab)
+        assert rel_l2(lm, lc) < 1e-3 and int(ref.lib.sample_greedy(fptr(lm), spec.vocab)) == t_c, step
+        tok, pos = t_c, pos + 1
+    cpu.close(), mix.close(), rest.close()
+    lib.backend_destroy(b)
+
