@@ -83,6 +83,9 @@ struct gq_ctx {
   Workspace ws;
   PrefillWs pf;
   float *scratch = nullptr; /* this device's address of the file-scope `scratch` array */
+  /* host -> device staging: two pinned slots, allocated on first upload */
+  void *stage[2] = {nullptr, nullptr};
+  hipEvent_t stage_ev[2] = {nullptr, nullptr};
   SampleWs sw;
   int *d_sample = nullptr; /* sampled token (device) */
   /* graph */
@@ -195,6 +198,10 @@ extern "C" void gq_hip_destroy(gq_ctx *c) {
   free_graph(c);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
   for (void *p : c->allocs) (void)hipFree(p);
+  for (int i = 0; i < 2; i++) {
+    if (c->stage[i]) (void)hipHostFree(c->stage[i]);
+    if (c->stage_ev[i]) (void)hipEventDestroy(c->stage_ev[i]);
+  }
   (void)hipStreamDestroy(c->stream);
   delete c;
 }
@@ -254,20 +261,58 @@ extern "C" int gq_hip_d2h(gq_ctx *c, void *host, const void *dev, size_t bytes) 
   return 0;
 }
 
+/* Host -> device through two pinned staging slots of kStageBytes: the CPU
+ * copies chunk i + 1 into one slot while the DMA of chunk i drains the
+ * other.  The source is only ever read by the CPU, so a private file mapping
+ * (the loader's mmap) never meets the DMA engine, which is why the reference
+ * stages through a heap copy (matvec_q4k_cuda.cu:115-133). */
+constexpr size_t kStageBytes = (size_t)32 << 20;
+
+static int staged_h2d(gq_ctx *c, void *dst, const void *src, size_t bytes) {
+  for (int i = 0; i < 2; i++) {
+    if (!c->stage[i] && hipHostMalloc(&c->stage[i], kStageBytes, hipHostMallocDefault) != hipSuccess) {
+      c->stage[i] = nullptr;
+      return fail(c, -4, "upload: pinned staging buffer");
+    }
+    if (!c->stage_ev[i] && hipEventCreateWithFlags(&c->stage_ev[i], hipEventDisableTiming) != hipSuccess) {
+      c->stage_ev[i] = nullptr;
+      return fail(c, -4, "upload: staging event");
+    }
+  }
+  size_t off = 0;
+  for (int k = 0; off < bytes; k ^= 1) {
+    const size_t n = std::min(kStageBytes, bytes - off);
+    HIPCHK(c, hipEventSynchronize(c->stage_ev[k])); /* the slot's previous DMA is done */
+    memcpy(c->stage[k], (const char *)src + off, n);
+    HIPCHK(c, hipMemcpyAsync((char *)dst + off, c->stage[k], n, hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipEventRecord(c->stage_ev[k], c->stream));
+    off += n;
+  }
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return 0;
+}
+
 extern "C" void *gq_hip_upload_weight(gq_ctx *c, const void *host, size_t bytes) {
   if (!c || !host || !bytes) return nullptr;
   (void)hipSetDevice(c->dev);
   void *d = dev_alloc(c, bytes);
   if (!d) return nullptr;
-  /* staged by the runtime from pageable memory: no DMA straight out of a
-   * private file mapping (matvec_q4k_cuda.cu:119-121) */
-  if (hipMemcpy(d, host, bytes, hipMemcpyHostToDevice) != hipSuccess ||
-      hipMemset((char *)d + bytes, 0, kPad) != hipSuccess) {
+  if (staged_h2d(c, d, host, bytes) || hipMemsetAsync((char *)d + bytes, 0, kPad, c->stream) != hipSuccess ||
+      hipStreamSynchronize(c->stream) != hipSuccess) {
     gq_hip_free(c, d);
     fail(c, -4, "weight upload of %zu bytes failed", bytes);
     return nullptr;
   }
   return d;
+}
+
+extern "C" int gq_hip_mem_info(int device_id, size_t *free_bytes, size_t *total_bytes) {
+  if (device_id < 0 || device_id >= gq_hip_device_count() || hipSetDevice(device_id) != hipSuccess) return -1;
+  size_t f = 0, t = 0;
+  if (hipMemGetInfo(&f, &t) != hipSuccess) return -4;
+  if (free_bytes) *free_bytes = f;
+  if (total_bytes) *total_bytes = t;
+  return 0;
 }
 
 extern "C" void *gq_hip_host_alloc_pinned(size_t bytes) {

@@ -37,6 +37,7 @@ def _load():
         "gq_hip_sync": (C.c_int, [_vp]),
         "gq_hip_device_info": (C.c_int, [_vp, C.POINTER(C.c_int), C.c_char_p, C.c_int]),
         "gq_hip_upload_weight": (_vp, [_vp, _vp, C.c_size_t]),
+        "gq_hip_mem_info": (C.c_int, [C.c_int, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]),
         "gq_hip_malloc": (_vp, [_vp, C.c_size_t]),
         "gq_hip_free": (None, [_vp, _vp]),
         "gq_hip_h2d": (C.c_int, [_vp, _vp, _vp, C.c_size_t]),
@@ -144,6 +145,14 @@ class GqModel(C.Structure):
                                       "head_dim", "vocab")] + [
         ("rope_theta", C.c_float), ("rms_eps", C.c_float), ("layers", C.POINTER(GqLayer)),
         ("embed", GqWeight), ("lm_head", GqWeight), ("rms_final", _vp)]
+
+
+def mem_info(device_id=0):
+    """(free, total) bytes of the device (hipMemGetInfo)."""
+    f, t = C.c_size_t(0), C.c_size_t(0)
+    if lib.gq_hip_mem_info(device_id, C.byref(f), C.byref(t)) != 0:
+        raise HipError(f"mem_info({device_id}) failed")
+    return f.value, t.value
 
 
 def device_count() -> int:

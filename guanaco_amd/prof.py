@@ -25,6 +25,11 @@
         causal attention of the 512 tokens, and forward() of a 512-token
         prompt through the whole 32-layer model.
 
+    python3 -m guanaco_amd.prof upload
+        the 8B shape's 4.6 GB of weights uploaded tensor by tensor from
+        pageable host memory (gq_hip_upload_weight's pinned staging): GB/s,
+        and hipMemGetInfo before, while resident and after gq_hip_destroy.
+
     python3 -m guanaco_amd.prof sample --vocab 128256 --iters 50
         on-device sampling (gq_hip_sample_dev) of N(0, 3^2) logits already
         in HBM: greedy, top-k 40, top-p 0.9 and plain temperature, each the
@@ -277,6 +282,40 @@ def run_configs():
     config4_restore()
 
 
+def run_upload():
+    """Weight upload of the 8B shape's per-layer tensors (4.6 GB in all) from
+    pageable host memory through gq_hip_upload_weight (pinned staging),
+    tensor by tensor as the loader uploads them: GB/s over the whole model,
+    and hipMemGetInfo before the context, with the weights resident, and
+    after gq_hip_destroy."""
+    spec = S.LLAMA8B
+    sizes = []
+    for l in range(spec.n_layers):
+        for k, dt in spec.dtypes(l).items():
+            sizes.append(S.qbytes(dt, *spec.shape(k)))
+    sizes.append(S.qbytes(spec.lm_head_dtype, *spec.shape("lm_head")))
+    sizes.append(S.qbytes(spec.embed_dtype, *spec.shape("embed")))
+    host = np.random.default_rng(0).integers(0, 256, max(sizes), dtype=np.uint8)
+    warm = H.Context(0)
+    H.lib.gq_hip_upload_weight(warm.h, host.ctypes.data, 1 << 20)
+    warm.close()
+    free0, total = H.mem_info(0)
+    ctx = H.Context(0)
+    t0 = time.perf_counter()
+    for n in sizes:
+        if not H.lib.gq_hip_upload_weight(ctx.h, host.ctypes.data, n):
+            ctx.raise_last("upload")
+    dt = time.perf_counter() - t0
+    free1, _ = H.mem_info(0)
+    ctx.close()
+    free2, _ = H.mem_info(0)
+    tot = sum(sizes)
+    emit(what="weight upload, Llama-3.1-8B-shape Q4_K_M, tensor by tensor from pageable host memory "
+              "(pinned double-buffered staging)", tensors=len(sizes), bytes=tot, seconds=round(dt, 3),
+         GB_per_s=round(tot / dt / 1e9, 2), free_before=free0, free_resident=free1, free_after_destroy=free2,
+         returned_all=free2 == free0, total=total)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -288,6 +327,7 @@ def main():
     smp.add_argument("--vocab", type=int, default=128256)
     smp.add_argument("--iters", type=int, default=50)
     sub.add_parser("config5")
+    sub.add_parser("upload")
     g = sub.add_parser("gemm")
     g.add_argument("--dtype", type=int, default=S.Q4_K)
     g.add_argument("--rows", type=int, default=4096)
@@ -303,6 +343,8 @@ def main():
         run_sample(a.vocab, a.iters)
     elif a.cmd == "config5":
         config5(H.Context(0))
+    elif a.cmd == "upload":
+        run_upload()
     elif a.cmd == "gemm":
         run_gemm(a.dtype, a.rows, a.cols, a.tokens, a.iters)
 

@@ -53,11 +53,17 @@ int gq_hip_device_info(gq_ctx *ctx, int *n_cu, char *name, int name_len);
 
 /* ------------------------------------------------------- device memory
  * Replaces cuda_upload_weight (matvec_q4k_cuda.cu:115-133): allocates and
- * copies `bytes` from host memory (a private file mapping is fine: the copy
- * is staged), returns the device pointer or NULL (the loader then keeps the
- * tensor CPU-resident, loader.c:711-717).  Allocations carry 256 bytes of
- * tail padding so block loads never leave the buffer. */
+ * copies `bytes` from host memory, returns the device pointer or NULL (the
+ * loader then keeps the tensor CPU-resident, loader.c:711-717).  The copy
+ * goes through two 32 MiB pinned staging slots of the context (CPU copy of
+ * one chunk overlapping the DMA of the previous one), so the source may be a
+ * private file mapping, which the reference stages through a heap copy for.
+ * Allocations carry 256 bytes of tail padding so block loads never leave the
+ * buffer. */
 void *gq_hip_upload_weight(gq_ctx *ctx, const void *host, size_t bytes);
+/* hipMemGetInfo of a device: free and total bytes (no counterpart in the
+ * reference; shows that gq_hip_destroy returns every byte). */
+int gq_hip_mem_info(int device_id, size_t *free_bytes, size_t *total_bytes);
 void *gq_hip_malloc(gq_ctx *ctx, size_t bytes);
 void gq_hip_free(gq_ctx *ctx, void *dev);
 int gq_hip_h2d(gq_ctx *ctx, void *dev, const void *host, size_t bytes);
