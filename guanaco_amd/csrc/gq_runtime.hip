@@ -1612,6 +1612,47 @@ extern "C" int gq_hip_forward_sample(gq_ctx *c, int token, int pos, float temper
   return sample_on_device(c, c->ws.logits, c->m.vocab, temperature, top_k, top_p, rnd);
 }
 
+/* One turn of the chat REPL (chat_repl, chat.c:157-263) on the device: the
+ * caller's tokens (BOS first only when the conversation starts, as chat.c
+ * tokenizes, :157-163) through the prefill at *current_pos, then the reply
+ * sampled one token at a time (greedy when temperature <= 0, else the
+ * device sampler with rnd[i] as the i-th rand() value) until max_tokens,
+ * kChatMaxReply tokens or eos.  *current_pos advances by the prompt and by
+ * the reply tokens as chat.c counts them: the last sampled token (eos
+ * included) is counted but not fed, so its position stays unwritten. */
+constexpr int kChatMaxReply = 512; /* CHAT_MAX_OUTPUT_TOKENS, chat.c:14 */
+
+extern "C" int gq_hip_chat_turn(gq_ctx *c, const int32_t *tokens, int n_tokens, int *current_pos, int max_tokens,
+                                int eos_token, float temperature, int top_k, float top_p, const int *rnd,
+                                int32_t *reply) {
+  if (!c || !c->bound || !tokens || n_tokens <= 0 || !current_pos || max_tokens <= 0 || !reply ||
+      (temperature > 0.0f && !rnd))
+    return fail(c, -1, "chat_turn: bad argument");
+  const int p0 = *current_pos;
+  if (p0 < 0 || p0 + n_tokens >= c->kv_max_seq - 1) /* chat.c:169 */
+    return fail(c, -6, "chat_turn: %d tokens at %d do not fit the %d-position context", n_tokens, p0,
+                c->kv_max_seq);
+  int next = gq_hip_prefill(c, tokens, n_tokens, p0, nullptr, nullptr, nullptr);
+  if (next < 0) return next;
+  int used = 0;
+  if (temperature > 0.0f && (next = sample_on_device(c, c->ws.logits, c->m.vocab, temperature, top_k, top_p,
+                                                     rnd[used++])) < 0)
+    return next;
+  const int cur = p0 + n_tokens;
+  int n = 0;
+  reply[n++] = next;
+  for (int i = 1; i < max_tokens && n < kChatMaxReply; i++) {
+    const int pos = cur + i - 1;
+    next = temperature > 0.0f ? gq_hip_forward_sample(c, next, pos, temperature, top_k, top_p, rnd[used++])
+                              : gq_hip_forward_token(c, next, pos, nullptr, nullptr);
+    if (next < 0) return next;
+    reply[n++] = next;
+    if (next == eos_token) break;
+  }
+  *current_pos = cur + n;
+  return n;
+}
+
 /* fp32 x -> the bf16 copy the GEMM reads */
 static const __bf16 *pf_x16(gq_ctx *c, const float *x, size_t n) {
   PrefillWs &w = c->pf;

@@ -96,6 +96,8 @@ def _load():
                                                  _vp]),
         "gq_hip_prefill_attention_dev": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp,
                                                    _vp, _vp]),
+        "gq_hip_chat_turn": (C.c_int, [_vp, C.POINTER(C.c_int32), C.c_int, C.POINTER(C.c_int), C.c_int, C.c_int,
+                                          C.c_float, C.c_int, C.c_float, C.POINTER(C.c_int), C.POINTER(C.c_int32)]),
         "gq_hip_prefill": (C.c_int, [_vp, C.POINTER(C.c_int32), C.c_int, C.c_int, _fp, _fp,
                                      C.POINTER(C.c_float)]),
     }
@@ -440,6 +442,22 @@ class DeviceModel:
         if tok < 0:
             self.ctx.raise_last("prefill", tok)
         return tok, logits, hid, ms.value
+
+    def chat_turn(self, tokens, current_pos, max_tokens, eos_token, temperature=0.0, top_k=40, top_p=0.9,
+                  rnd=None):
+        """gq_hip_chat_turn: (status, reply tokens, new current_pos); status
+        -6 when the turn does not fit (restart the conversation)."""
+        toks = np.ascontiguousarray(tokens, np.int32)
+        pos = C.c_int(current_pos)
+        reply = np.zeros(max(1, max_tokens), np.int32)
+        r = None if rnd is None else np.ascontiguousarray(rnd, np.int32)
+        n = lib.gq_hip_chat_turn(self.ctx.h, toks.ctypes.data_as(C.POINTER(C.c_int32)), toks.size, C.byref(pos),
+                                 max_tokens, eos_token, temperature, top_k, top_p,
+                                 r.ctypes.data_as(C.POINTER(C.c_int)) if r is not None else None,
+                                 reply.ctypes.data_as(C.POINTER(C.c_int32)))
+        if n < 0:
+            return n, None, current_pos
+        return 0, reply[:n].copy(), pos.value
 
     def decode_loop(self, token, pos, n_steps, use_graph=True):
         out = np.zeros(n_steps, np.int32)

@@ -321,6 +321,21 @@ int gq_hip_prefill_gate_up_dev(gq_ctx *ctx, int dtype, const void *w_gate, const
  * the cache. */
 int gq_hip_prefill_attention_dev(gq_ctx *ctx, int layer, int pos, int T, int n_heads, float *q,
                                  const float *k, const float *v, float *out);
+/* One turn of the chat REPL (chat_repl, chat.c:157-263) on the bound model,
+ * KV reused across turns: tokens (BOS first only on a conversation's first
+ * turn, as chat.c:157-163 tokenizes) go through the prefill at
+ * *current_pos; the reply is sampled until max_tokens, 512 tokens
+ * (CHAT_MAX_OUTPUT_TOKENS) or eos_token, greedy when temperature <= 0, else
+ * as gq_hip_sample_dev with rnd[i] the i-th rand() value (max_tokens
+ * values).  reply receives the tokens (eos included when sampled, up to
+ * min(max_tokens, 512)); *current_pos advances as chat.c's current_pos
+ * does (the prompt, then every reply token, the last of which is never
+ * fed).  Returns the reply length; -6 when *current_pos + n_tokens >=
+ * max_seq - 1, where chat.c restarts the conversation (:169-190: the caller
+ * sets *current_pos = 0 and re-tokenizes with BOS); -5 when the reply runs
+ * past the cache (the reference wraps, kv_cache.c:101; the device does not). */
+int gq_hip_chat_turn(gq_ctx *ctx, const int32_t *tokens, int n_tokens, int *current_pos, int max_tokens,
+                     int eos_token, float temperature, int top_k, float top_p, const int *rnd, int32_t *reply);
 /* forward(model, kv, scr, tokens, n_tokens, pos) of the bound model
  * (engine.c:559-595): the whole prompt through every layer in chunks of
  * up to 512 tokens, filling the device KV cache at pos .. pos+n_tokens-1;

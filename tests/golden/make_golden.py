@@ -12,12 +12,13 @@ What comes from where (the README next to this script says the same):
                       test_forward_bitexact_vs_reference: whole-step logits)
   kv_tiny.npz/.lctx   slabs after kv_cache_append (with wrap) and the file
                       kv_cache_save writes, from the reference
-  tinyllama_greedy.npz / llama8b_greedy.npz
-                      greedy tokens and top-2 logit margins from the
+  tinyllama_greedy.npz / tinyllama_q8_greedy.npz / llama8b_greedy.npz
+                      greedy tokens, top-2 logit margins and the 16 largest
+                      logits (indices and values) of every step from the
                       reference's forward() + sample_greedy; per-layer hidden
-                      states from the oracle, run in lock step (its logits are
-                      asserted bit-identical to the reference's at every step
-                      it runs)
+                      states at steps 0, 63 and 127 from the oracle, run in
+                      lock step (its logits are asserted bit-identical to the
+                      reference's at every step)
 Inputs are the deterministic generator of guanaco_amd/csrc/gq_synth.h
 (GENERATOR_VERSION below); each file records seeds and SHA-256 of weights.
 """
@@ -44,6 +45,7 @@ MATVEC_CASES = [(Q4_K, 1, 256), (Q4_K, 8, 512), (Q4_K, 64, 1024), (Q4_K, 4096, 4
                 (Q6_K, 1, 256), (Q6_K, 8, 512), (Q6_K, 64, 1024),
                 (Q8_0, 1, 256), (Q8_0, 8, 512), (Q8_0, 64, 1024)]
 NAMES = {Q4_K: "q4_k", Q6_K: "q6_k", Q8_0: "q8_0"}
+TOPK = 16  # reference logits recorded per greedy step (largest first)
 
 
 def log(m):
@@ -129,13 +131,16 @@ def make_greedy(orc, ref, spec, max_seq, prefill, start, steps, hidden_steps, na
     rm = RefModel(ref, hm)
     rm.load_kv(kv)
     log(f"{name}: model built in {time.time() - t0:.0f}s")
-    toks, margins, hidden = [], [], {}
+    toks, margins, hidden, top_idx, top_val = [], [], {}, [], []
     tok = start
     for i in range(steps):
         pos = prefill + i
         t_ref, logits = rm.forward(tok, pos)
         top2 = np.sort(logits)[-2:]
         margins.append(float(top2[1] - top2[0]))
+        idx = np.argsort(logits, kind="stable")[::-1][:TOPK]
+        top_idx.append(idx.astype(np.int32))
+        top_val.append(logits[idx].astype(np.float32))
         if check_every or i in hidden_steps or i == 0:
             t_orc, l_orc, hid = hm.forward(kv, tok, pos, want_hidden=i in hidden_steps)
             assert t_orc == t_ref and np.array_equal(l_orc.view(np.uint32), logits.view(np.uint32)), \
@@ -149,6 +154,7 @@ def make_greedy(orc, ref, spec, max_seq, prefill, start, steps, hidden_steps, na
     out = dict(generator_version=np.int64(GENERATOR_VERSION), model_seed=np.int64(spec.seed),
                start_token=np.int32(start), prefill=np.int32(prefill), max_seq=np.int32(max_seq),
                tokens=np.array(toks, np.int32), margins=np.array(margins, np.float32),
+               top_idx=np.stack(top_idx), top_logits=np.stack(top_val),
                embed_sha256=np.array(sha(hm.embed)), lm_head_sha256=np.array(sha(hm.lm_head)))
     for i, h in hidden.items():
         out[f"hidden_step{i}"] = h
@@ -173,10 +179,11 @@ def main():
     if not only or "kv" in only:
         make_kv_tiny(orc, ref)
     if not only or "tinyllama" in only:
-        make_greedy(orc, ref, S.TINYLLAMA, 640, 512, 1, 128, (0, 127), "tinyllama_greedy")
+        make_greedy(orc, ref, S.TINYLLAMA, 640, 512, 1, 128, (0, 63, 127), "tinyllama_greedy")
+    if not only or "tinyllama_q8" in only:
+        make_greedy(orc, ref, S.TINYLLAMA_Q8, 640, 512, 1, 128, (0, 63, 127), "tinyllama_q8_greedy")
     if (not only or "llama8b" in only) and not a.skip_8b:
-        make_greedy(orc, ref, S.LLAMA8B, 8320, 8192, 128000, 128, (0,), "llama8b_greedy",
-                    check_every=False)
+        make_greedy(orc, ref, S.LLAMA8B, 8320, 8192, 128000, 128, (0, 63, 127), "llama8b_greedy")
 
 
 if __name__ == "__main__":

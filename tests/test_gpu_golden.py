@@ -3,7 +3,9 @@ reference (tests/golden/make_golden.py): matvec y, attention, KV slabs and
 .lctx bytes, and the north-star bar on the benchmark shapes — identical
 greedy tokens for 128 steps and per-layer hidden states within 1e-3
 relative L2 — for the TinyLlama-shape (config 2) and Llama-3.1-8B-shape
-(config 3, KV filled to 8192) models."""
+(config 3, KV filled to 8192) models, plus the 16 largest logits of every
+step, and a TinyLlama-shape variant with all weights Q8_0 whose tokens vary
+from step to step."""
 import os
 
 import numpy as np
@@ -18,6 +20,16 @@ GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 DT = {"q4_k": S.Q4_K, "q6_k": S.Q6_K, "q8_0": S.Q8_0}
 MV_TOL = 1e-5     # per matvec (a correct kernel differs from the CPU order by ~1e-7)
 LAYER_TOL = 1e-3  # per layer
+# the 16 largest logits of each step: the median step within LOGIT_TOL
+# (observed ~1e-6), every step within LOGIT_MAX.  The Q8_0 model's q and k
+# entries are ~80, so its attention scores reach ~1e4, where one fp32 ulp is
+# ~1e-3: at a near-tie between two positions (step 86: a top-2 gap of 0.17
+# in a layer-0 head, scores of standard deviation ~3900) the GPU's and the
+# CPU's summation orders move ~1e-3 of softmax weight between them, and that
+# step's logits differ by 1.2e-3 with the same greedy token.  Steps without
+# such a tie stay at ~1e-6.
+LOGIT_TOL = 1e-5
+LOGIT_MAX = 5e-3
 
 
 def load(name):
@@ -97,10 +109,12 @@ def test_kv_append_and_lctx_vs_reference(tmp_path):
         c.close()
 
 
-def run_greedy(spec, g, check_last_hidden):
-    """Greedy decode on the device from the fixture's start: step 0 with
-    per-layer hidden states, the 128-step graph loop, and (optionally) step
-    127 again with hidden states."""
+def run_greedy(spec, g):
+    """Greedy decode on the device from the fixture's start, two ways:
+    eager forward_token steps, each step's 16 largest reference logits
+    compared (LOGIT_TOL) and the per-layer hidden states at every step the
+    fixture holds (LAYER_TOL); then the graph-replayed decode loop.  Both
+    must produce the reference's tokens at every step."""
     import guanaco_amd.hip as H
     from guanaco_amd.synth import tensor_seed
     c = H.Context(0)
@@ -108,32 +122,46 @@ def run_greedy(spec, g, check_last_hidden):
         pre, ms = int(g["prefill"]), int(g["max_seq"])
         dm = H.DeviceModel(c, spec, ms, prefill=pre)
         seeds = (tensor_seed(spec.seed, -1, 13), tensor_seed(spec.seed, -1, 14))
-        tokens = g["tokens"]
-        start = int(g["start_token"])
-        t0, _, h0 = dm.forward(start, pre, want_hidden=True)
-        assert t0 == int(tokens[0])
-        worst = max(rel_l2(h0[l], g["hidden_step0"][l]) for l in range(spec.n_layers))
-        assert worst < LAYER_TOL, worst
+        tokens, top_idx, top_val = g["tokens"], g["top_idx"], g["top_logits"]
+        hsteps = {int(k[len("hidden_step"):]) for k in g.files if k.startswith("hidden_step")}
+        n, tok = len(tokens), int(g["start_token"])
+        worst_h = worst_l = 0.0
+        el, eh = [], {}
+        for i in range(n):
+            t, logits, hid = dm.forward(tok, pre + i, want_hidden=i in hsteps)
+            el.append(rel_l2(logits[top_idx[i]], top_val[i]))
+            worst_l = max(worst_l, el[-1])
+            if hid is not None:
+                eh[i] = [rel_l2(hid[l], g[f"hidden_step{i}"][l]) for l in range(spec.n_layers)]
+                worst_h = max(worst_h, max(eh[i]))
+            assert t == int(tokens[i]), f"eager step {i}: token {t} vs {int(tokens[i])} (margin {g['margins'][i]:.3g})"
+            tok = t
+        print(f"{spec.name}: top-16 logits rel L2 per step: max {max(el):.3g} at step {int(np.argmax(el))}, "
+              f"median {float(np.median(el)):.3g}, steps 0-7 {[f'{e:.2g}' for e in el[:8]]}")
+        for i, e in sorted(eh.items()):
+            print(f"  hidden step {i}: per-layer rel L2 {[f'{x:.2g}' for x in e]}")
+        assert float(np.median(el)) < LOGIT_TOL and worst_l < LOGIT_MAX, (float(np.median(el)), worst_l)
+        assert worst_h < LAYER_TOL, worst_h
         c.kv_prefill_synth(*seeds, pre)
-        toks, _ = dm.decode_loop(start, pre, len(tokens), use_graph=True)
-        mism = [i for i in range(len(tokens)) if toks[i] != tokens[i]]
-        assert not mism, f"first mismatch at step {mism[0]}: {toks[mism[0]]} vs {tokens[mism[0]]}"
-        if check_last_hidden:
-            n = len(tokens)
-            c.kv_prefill_synth(*seeds, pre)
-            dm.decode_loop(start, pre, n - 1, use_graph=True)
-            tl, _, hl = dm.forward(int(tokens[n - 2]), pre + n - 1, want_hidden=True)
-            assert tl == int(tokens[n - 1])
-            worst = max(worst, max(rel_l2(hl[l], g[f"hidden_step{n - 1}"][l]) for l in range(spec.n_layers)))
-            assert worst < LAYER_TOL, worst
-        print(f"{spec.name}: 128 tokens identical; worst per-layer rel L2 {worst:.3g}")
+        toks, _ = dm.decode_loop(int(g["start_token"]), pre, n, use_graph=True)
+        mism = [i for i in range(n) if toks[i] != tokens[i]]
+        assert not mism, f"graph: first mismatch at step {mism[0]}: {toks[mism[0]]} vs {tokens[mism[0]]}"
+        print(f"{spec.name}: {n} tokens identical ({len(set(tokens.tolist()))} distinct, min margin "
+              f"{float(g['margins'].min()):.3g}); top-16 logits worst rel L2 {worst_l:.3g}; hidden states "
+              f"at steps {sorted(hsteps)} worst per-layer rel L2 {worst_h:.3g}")
     finally:
         c.close()
 
 
 def test_tinyllama_128_greedy_steps_vs_reference():
-    run_greedy(S.TINYLLAMA, load("tinyllama_greedy.npz"), check_last_hidden=True)
+    run_greedy(S.TINYLLAMA, load("tinyllama_greedy.npz"))
+
+
+def test_tinyllama_q8_0_128_greedy_steps_vs_reference():
+    """The non-degenerate variant: every weight Q8_0 (zero-mean), a different
+    token at nearly every step, top-2 margins down to O(1)."""
+    run_greedy(S.TINYLLAMA_Q8, load("tinyllama_q8_greedy.npz"))
 
 
 def test_llama8b_128_greedy_steps_vs_reference():
-    run_greedy(S.LLAMA8B, load("llama8b_greedy.npz"), check_last_hidden=False)
+    run_greedy(S.LLAMA8B, load("llama8b_greedy.npz"))
