@@ -110,7 +110,7 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(AttnArgs a) {
   const int dg = tid % DG, pg = tid / DG;
   float4 vr[VIT];
 #pragma unroll
-  for (int k = 0; k < VIT; k++) vr[k] = gld<float4>(V + (size_t)min(pg + NPG * k, n - 1) * HD + 4 * dg);
+  for (int k = 0; k < VIT; k++) vr[k] = gld_nt<float4>(V + (size_t)min(pg + NPG * k, n - 1) * HD + 4 * dg);
   /* query slices and K rows of phase 1 */
   const int sub = tid % LPP, pw = tid / LPP;
   const int d0 = 4 * sub, d1 = HD / 2 + 4 * sub;
@@ -124,8 +124,8 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(AttnArgs a) {
 #pragma unroll
   for (int k = 0; k < KIT; k++) {
     const float *kr = K + (size_t)min(pw + PPI * k, n - 1) * HD;
-    ka[k] = gld<float4>(kr + d0);
-    kb[k] = gld<float4>(kr + d1);
+    ka[k] = gld_nt<float4>(kr + d0);
+    kb[k] = gld_nt<float4>(kr + d1);
   }
 
   /* phase 1: scores (q . k) * 1/sqrt(hd) */

@@ -53,6 +53,15 @@ __device__ __forceinline__ T gld(const void *p) {
   return __builtin_bit_cast(T, *(const GQ_GLOBAL N *)p);
 }
 
+/* Non-temporal load (the `nt` cache policy): for streams read once per
+ * launch, such as the K/V cache, so that they do not evict lines that other
+ * waves still reuse. */
+template <class T>
+__device__ __forceinline__ T gld_nt(const void *p) {
+  typedef typename gq_native<sizeof(T)>::type N;
+  return __builtin_bit_cast(T, __builtin_nontemporal_load((const GQ_GLOBAL N *)p));
+}
+
 /* 12-byte load (three dwords, 4-byte aligned) */
 __device__ __forceinline__ uint3 gld12(const void *p) {
   typedef unsigned int N __attribute__((ext_vector_type(3), aligned(4)));

@@ -272,28 +272,34 @@ __device__ __forceinline__ void mvx_body(const MvArgs &a, const MxPlan &p, int b
   constexpr int P = MODE == MV_SWIGLU ? R / 2 : R; /* output rows per group */
   constexpr int NV = R + 1;                        /* row sums, sum of x^2 */
   const int tid = threadIdx.x;
-  /* every kernel-argument field this body uses, read once at entry (one
-   * batch of scalar loads, one wait; fields the compiler fetched lazily cost
-   * a scalar-cache round trip each before the first weight load) */
-  const float *const xp = gq_pin(a.x), *const nw = gq_pin(a.norm_w);
-  const int cols = gq_pin(a.cols);
-  const float eps = gq_pin(a.eps);
-  const float2 *const rcs = gq_pin(a.rope.cs);
-  const int *const rpd = gq_pin(a.rope.pos_dev);
-  const int rpos = gq_pin(a.rope.pos), hd = gq_pin(a.rope.head_dim), msq = gq_pin(a.rope.max_seq);
-  const int L = gq_pin(p.L), upr = gq_pin(p.upr), nt = gq_pin(p.nt), rowbytes = gq_pin(p.rowbytes);
+  /* every kernel-argument field this body uses, read at entry and pinned
+   * into scalar registers by ONE asm statement: one batch of scalar loads
+   * and one wait (pinned one by one, the compiler issued them in three
+   * batches, each a kernel-argument round trip before the first weight
+   * load).  Pinned values keep selects between segments as selects of
+   * registers (see MvSegs). */
+  const float *xp = a.x, *nw = a.norm_w;
+  int cols = a.cols;
+  float eps = a.eps;
+  const float2 *rcs = a.rope.cs;
+  const int *rpd = a.rope.pos_dev;
+  int rpos = a.rope.pos, hd = a.rope.head_dim, msq = a.rope.max_seq;
+  int L = p.L, upr = p.upr, nt = p.nt, rowbytes = p.rowbytes, G = p.G, total = p.total;
+  const uint8_t *sw0 = a.seg[0].w, *sw1 = a.seg[1].w, *sw2 = a.seg[2].w;
+  float *sy0 = a.seg[0].y, *sy1 = a.seg[1].y, *sy2 = a.seg[2].y;
+  const float *sr0 = a.seg[0].r; /* MV_RESID launches have one segment */
+  int sn0 = a.seg[0].rows, sn1 = a.seg[1].rows, nseg = a.nseg;
+  int sk0 = a.seg[0].kind, sk1 = a.seg[1].kind, sk2 = a.seg[2].kind;
+  asm volatile(""
+               : "+s"(xp), "+s"(nw), "+s"(cols), "+s"(eps), "+s"(rcs), "+s"(rpd), "+s"(rpos), "+s"(hd),
+                 "+s"(msq), "+s"(L), "+s"(upr), "+s"(nt), "+s"(rowbytes), "+s"(G), "+s"(total), "+s"(sw0),
+                 "+s"(sw1), "+s"(sw2), "+s"(sy0), "+s"(sy1), "+s"(sy2), "+s"(sr0), "+s"(sn0), "+s"(sn1),
+                 "+s"(nseg), "+s"(sk0), "+s"(sk1), "+s"(sk2));
   /* UNI: row groups are whole waves (L % 64 == 0), so the group, its rows
    * and their addresses are wave-uniform (scalar registers) */
   const int g = UNI ? __builtin_amdgcn_readfirstlane(tid / L) : tid / L;
   const int ul = tid - g * L;
   constexpr bool norm = (FL & kNorm) != 0, MT = (FL & kMT) != 0;
-  /* the segments as separate pinned values (selects between them stay
-   * selects of registers; see MvSegs) */
-  const uint8_t *const sw0 = gq_pin(a.seg[0].w), *const sw1 = gq_pin(a.seg[1].w), *const sw2 = gq_pin(a.seg[2].w);
-  float *const sy0 = gq_pin(a.seg[0].y), *const sy1 = gq_pin(a.seg[1].y), *const sy2 = gq_pin(a.seg[2].y);
-  const float *const sr0 = gq_pin(a.seg[0].r); /* MV_RESID launches have one segment */
-  const int sn0 = gq_pin(a.seg[0].rows), sn1 = gq_pin(a.seg[1].rows), nseg = gq_pin(a.nseg);
-  const int sk0 = gq_pin(a.seg[0].kind), sk1 = gq_pin(a.seg[1].kind), sk2 = gq_pin(a.seg[2].kind);
 #define GQ_SEL3(s, a0, a1, a2) ((s) == 0 ? (a0) : (s) == 1 ? (a1) : (a2))
 #define GQ_LOCATE(gr, s, lr)                                                                                \
   do {                                                                                                      \
@@ -304,17 +310,15 @@ __device__ __forceinline__ void mvx_body(const MvArgs &a, const MxPlan &p, int b
     }                                                                                                       \
   } while (0)
 
-  const int G = gq_pin(p.G), total = gq_pin(p.total);
   /* the epilogue role of this thread (tid < G * P finishes output row i of
-   * group gg): its residual (MV_RESID launches have one segment) and the
-   * device position are loaded first, with nothing waiting on them before
-   * the epilogue */
+   * group gg): its residual (MV_RESID launches have one segment) is loaded
+   * first, with nothing waiting on it before the epilogue */
   float e_res = 0.f;
   if (MODE == MV_RESID && tid < G * P) {
     const int erow = (bid * G + tid / P) * P + tid % P;
     if (erow < total) e_res = gld<float>(sr0 + erow);
   }
-  const int epos = MODE == MV_STORE && rcs ? (rpd ? gq_sld<int>(rpd) : rpos) : 0;
+  int epos = 0; /* the device position, read behind the first tile's weights */
   /* weight rows of this group (rows past the end clamp to the last: loaded,
    * never stored) */
   const uint8_t *rp[R];
@@ -386,10 +390,12 @@ __device__ __forceinline__ void mvx_body(const MvArgs &a, const MxPlan &p, int b
 #pragma unroll
         for (int k = 0; k < R; k++) raw[k] = T::load(rp[k] + T::boff(u), u & 7);
       }
-      /* the RoPE row of pos, behind the weights (kept in a register until
-       * the reduction puts it in LDS) */
-      if (MODE == MV_STORE && t == 0 && rcs && tid < (hd >> 1) && epos >= 0 && epos < msq)
-        cs_pre = gld<float2>(rcs + (size_t)epos * (hd >> 1) + tid);
+      /* the device position and its RoPE row, behind the weights (kept in a
+       * register until the reduction puts it in LDS) */
+      if (MODE == MV_STORE && t == 0 && rcs) {
+        epos = rpd ? gq_sld<int>(rpd) : rpos;
+        if (tid < (hd >> 1) && epos >= 0 && epos < msq) cs_pre = gld<float2>(rcs + (size_t)epos * (hd >> 1) + tid);
+      }
       if (!act) continue;
       const float sxl = (sum4(xl[0]) + sum4(xl[1])) + (sum4(xl[2]) + sum4(xl[3]));
       const float sxh = (sum4(xh[0]) + sum4(xh[1])) + (sum4(xh[2]) + sum4(xh[3]));
