@@ -47,7 +47,7 @@ CLASS_KERNELS = {
     "attention": "attn_partial_kernel<128, 4, 64> + attn_merge_kernel (split-K partials, merge)",
     "o_proj": "mvx_kernel<Q4_K, RESID> (o + residual)",
     "gate_up": "mvm_kernel<Q4_K, SWIGLU> (int8 matrix cores, RMSNorm + SwiGLU fused)",
-    "down": "mvx_kernel<Q6_K / Q4_K, RESID> (down + residual)",
+    "down": "mvx_kernel<Q6_K in the unit layout / Q4_K, RESID> (down + residual)",
     "lm_head": "mvm_kernel<Q6_K, STORE> (int8 matrix cores, final RMSNorm fused)",
 }
 

@@ -31,6 +31,10 @@ enum { MV_STORE = 0, MV_RESID = 1, MV_SWIGLU = 2 };
  * Cache row r = h*head_dim + d lands at ((h*max_seq + pos)*head_dim + d). */
 enum { SEG_PLAIN = 0, SEG_ROPE = 1, SEG_ROPE_KV = 2, SEG_KV = 3 };
 
+/* Q6_K in the vector-ALU matvec's unit layout: an internal weight type,
+ * never seen at the C ABI */
+#define GQ_Q6_KX 65
+
 struct MvSeg {
   const uint8_t *w;
   float *y;
@@ -58,6 +62,10 @@ struct MvArgs {
    * (gq_launch_mm_tile), segments in order (MV_SWIGLU: gate and up in one
    * tensor); NULL: that kernel is not used */
   const uint8_t *mm;
+  /* a Q6_K segment 0 in the vector-ALU kernel's unit layout
+   * (gq_launch_q6k_units), used for one-segment store and residual launches
+   * instead of seg[0].w; NULL: the reference layout */
+  const uint8_t *dx;
 };
 
 /* silu(g) * u as the reference computes it: silu(g) = g * (1 / (1 + expf(-g)))
@@ -146,6 +154,11 @@ void gq_matvec_set_cus(int n_cu);
  * same rows of w1.  Bytes: gq_mm_tile_bytes. */
 size_t gq_mm_tile_bytes(int dtype, int rows, int cols, bool swiglu);
 int gq_launch_mm_tile(void *dst, int dtype, const void *w0, const void *w1, int rows, int cols, hipStream_t s);
+/* Q6_K weights (rows x cols, cols a multiple of 512) re-laid out for the
+ * vector-ALU matvec: each 32-column unit's quants, high bits, scales and d
+ * at naturally aligned offsets, the same bytes (gq_q6k_units_bytes). */
+size_t gq_q6k_units_bytes(int rows, int cols);
+int gq_launch_q6k_units(void *dst, const void *src, int rows, int cols, hipStream_t s);
 /* whether the matrix-core kernel is selected for every launch it fits
  * (gq_hip_set_matvec_path(2)): the op-level entry points then tile their
  * weights per call */

@@ -81,7 +81,9 @@ struct Ux<GQ_Q4_K> {
   static __device__ __forceinline__ int col(int u) { return 256 * (u >> 3) + 64 * ((u >> 1) & 3) + 16 * (u & 1); }
   /* blk: this lane's block (a per-lane 64-bit address: measured faster
    * than a scalar row base with 32-bit lane offsets) */
-  static __device__ __forceinline__ Raw load(const uint8_t *blk, int j) {
+  static __device__ __forceinline__ Raw load(const uint8_t *row, int u, int) {
+    const uint8_t *blk = row + boff(u);
+    const int j = u & 7;
     Raw r;
     r.q = gld<uint4>(blk + 16 + 16 * j);
     r.h = gld<uint32_t>(blk + 4 * (j & 3));
@@ -145,7 +147,9 @@ struct Ux<GQ_Q6_K> {
   };
   static __device__ __forceinline__ uint32_t boff(int u) { return (uint32_t)BB * (uint32_t)(u >> 3); }
   static __device__ __forceinline__ int col(int u) { return 256 * (u >> 3) + 128 * ((u >> 2) & 1) + 16 * (u & 3); }
-  static __device__ __forceinline__ Raw load(const uint8_t *blk, int j) {
+  static __device__ __forceinline__ Raw load(const uint8_t *row, int u, int) {
+    const uint8_t *blk = row + boff(u);
+    const int j = u & 7;
     Raw r;
     const int h = j >> 2, v = j & 3;
     /* ql at 64h+16v and qh at 128+32h+16(v&1): both at the block's 2-byte
@@ -210,7 +214,8 @@ struct Ux<GQ_Q8_0> {
   };
   static __device__ __forceinline__ uint32_t boff(int u) { return (uint32_t)BB * (uint32_t)u; }
   static __device__ __forceinline__ int col(int u) { return 32 * u; }
-  static __device__ __forceinline__ Raw load(const uint8_t *blk, int) {
+  static __device__ __forceinline__ Raw load(const uint8_t *row, int u, int) {
+    const uint8_t *blk = row + boff(u);
     Raw r;
     /* quants from blk + 2: the aligned start is the block or 2 bytes in */
     const uintptr_t a = (uintptr_t)(blk + 2) & ~(uintptr_t)3;
@@ -239,6 +244,88 @@ struct Ux<GQ_Q8_0> {
     return gq_h2f(r.d) * __builtin_fmaf(-128.f, sxl + sxh, s);
   }
 };
+
+/* Q6_K re-laid out per row for this kernel (gq_launch_q6k_units, made once
+ * at model bind; the same 210 bytes per block, every field naturally
+ * aligned): unit u (block u/8, half h, group v as for Q6_K) has its 16
+ * bytes of ql_h[16v ..] at 24u, then two dwords of its 2-bit fields: byte k
+ * of quant dword m's fields (bits 0-1 and 4-5 of (qh_h[16(v&1) + 4m + k] >>
+ * 2(v/2)), the pair Q6_K uses for that quant's low and high nibble) sits in
+ * byte k of dword m/2 shifted left by 2(m&1); its two scales (sc_h[v],
+ * sc_h[v+4]) are the int8 pair at 192*nb + 2u, and its block's d the fp16
+ * at 208*nb + 2(u/8).  A lane holds 8 dwords per row (12 for the reference
+ * layout, whose 2-byte block phase costs an extra dword per field and the
+ * funnel shifts), so 8-row groups fit 128 VGPRs.  The products and their
+ * order are Q6_K's: results are bit-identical to it. */
+template <>
+struct Ux<GQ_Q6_KX> {
+  static constexpr int BB = 210, XHI = 64;
+  struct Raw {
+    uint4 q;
+    uint2 h;
+    uint32_t s, d;
+  };
+  static __device__ __forceinline__ uint32_t boff(int u) { return 24u * (uint32_t)u; }
+  static __device__ __forceinline__ int col(int u) { return Ux<GQ_Q6_K>::col(u); }
+  static __device__ __forceinline__ Raw load(const uint8_t *row, int u, int nb) {
+    Raw r;
+    r.q = gld<uint4>(row + boff(u));
+    r.h = gld<uint2>(row + boff(u) + 16);
+    r.s = gld<unsigned short>(row + 192 * nb + 2 * u);
+    r.d = gld<unsigned short>(row + 208 * nb + 2 * (u >> 3));
+    return r;
+  }
+  static __device__ __forceinline__ float dot(const Raw &r, int, const float4 (&xl)[4], const float4 (&xh)[4],
+                                              float sxl, float sxh, uint32_t) {
+    const uint32_t ql[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+    const uint32_t hf[4] = {r.h.x, r.h.x >> 2, r.h.y, r.h.y >> 2};
+    const int s0 = __builtin_amdgcn_sbfe((int)r.s, 0, 8), s1 = __builtin_amdgcn_sbfe((int)r.s, 8, 8);
+    float dl = 0.f, dh = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t lo = (ql[i] & 0x0F0F0F0Fu) | ((hf[i] << 4) & 0x30303030u); /* 6-bit q, 0..63 */
+      const uint32_t hi = ((ql[i] >> 4) & 0x0F0F0F0Fu) | (hf[i] & 0x30303030u);
+      dl = __builtin_fmaf((float)(lo & 0xffu), xl[i].x, dl);
+      dl = __builtin_fmaf((float)((lo >> 8) & 0xffu), xl[i].y, dl);
+      dl = __builtin_fmaf((float)((lo >> 16) & 0xffu), xl[i].z, dl);
+      dl = __builtin_fmaf((float)(lo >> 24), xl[i].w, dl);
+      dh = __builtin_fmaf((float)(hi & 0xffu), xh[i].x, dh);
+      dh = __builtin_fmaf((float)((hi >> 8) & 0xffu), xh[i].y, dh);
+      dh = __builtin_fmaf((float)((hi >> 16) & 0xffu), xh[i].z, dh);
+      dh = __builtin_fmaf((float)(hi >> 24), xh[i].w, dh);
+    }
+    const float d = gq_h2f(r.d);
+    const float acc = (d * (float)s0) * __builtin_fmaf(-32.f, sxl, dl);
+    return __builtin_fmaf(d * (float)s1, __builtin_fmaf(-32.f, sxh, dh), acc);
+  }
+};
+
+/* One thread per (row, unit): the Q6_K row in the reference layout (src) to
+ * the unit layout above (dst, same size). */
+__global__ __launch_bounds__(256) void q6k_units_kernel(const uint8_t *src, uint8_t *dst, int rows, int nb) {
+  const int upr = 8 * nb;
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (long long)rows * upr) return;
+  const int row = (int)(t / upr), u = (int)(t - (long long)row * upr);
+  const int b = u >> 3, j = u & 7, h = j >> 2, v = j & 3;
+  const uint8_t *blk = src + ((size_t)row * nb + b) * 210;
+  uint8_t *drow = dst + (size_t)row * nb * 210, *du = drow + 24 * u;
+  for (int i = 0; i < 16; i++) du[i] = blk[64 * h + 16 * v + i];
+  const int qs = 2 * (v >> 1);
+  uint32_t P[2] = {0u, 0u};
+  for (int i = 0; i < 16; i++) {
+    const uint32_t f = ((uint32_t)blk[128 + 32 * h + 16 * (v & 1) + i] >> qs) & 0x33u;
+    const int m = i >> 2, k = i & 3;
+    P[m >> 1] |= f << (8 * k + 2 * (m & 1));
+  }
+  for (int i = 0; i < 8; i++) du[16 + i] = (uint8_t)(P[i >> 2] >> (8 * (i & 3)));
+  drow[192 * nb + 2 * u] = blk[192 + 8 * h + v];
+  drow[192 * nb + 2 * u + 1] = blk[192 + 8 * h + v + 4];
+  if (j == 0) {
+    drow[208 * nb + 2 * b] = blk[208];
+    drow[208 * nb + 2 * b + 1] = blk[209];
+  }
+}
 
 struct MxPlan {
   int L;        /* lanes per row group, a multiple of 8 */
@@ -295,6 +382,7 @@ __device__ __forceinline__ void mvx_body(const MvArgs &a, const MxPlan &p, int b
                  "+s"(msq), "+s"(L), "+s"(upr), "+s"(nt), "+s"(rowbytes), "+s"(G), "+s"(total), "+s"(sw0),
                  "+s"(sw1), "+s"(sw2), "+s"(sy0), "+s"(sy1), "+s"(sy2), "+s"(sr0), "+s"(sn0), "+s"(sn1),
                  "+s"(nseg), "+s"(sk0), "+s"(sk1), "+s"(sk2));
+  const int nbq = cols >> 8; /* 256-column blocks per row (the Q6_K unit layout) */
   /* UNI: row groups are whole waves (L % 64 == 0), so the group, its rows
    * and their addresses are wave-uniform (scalar registers) */
   const int g = UNI ? __builtin_amdgcn_readfirstlane(tid / L) : tid / L;
@@ -388,7 +476,7 @@ __device__ __forceinline__ void mvx_body(const MvArgs &a, const MxPlan &p, int b
       typename T::Raw raw[R];
       if (act) {
 #pragma unroll
-        for (int k = 0; k < R; k++) raw[k] = T::load(rp[k] + T::boff(u), u & 7);
+        for (int k = 0; k < R; k++) raw[k] = T::load(rp[k], u, nbq);
       }
       /* the device position and its RoPE row, behind the weights (kept in a
        * register until the reduction puts it in LDS) */
@@ -507,7 +595,8 @@ __global__ __launch_bounds__(MAXNT) void mvx_pair_kernel(MvArgs a0, MxPlan p0, M
 
 /* 0: this kernel for every launch; 1 (default): the matrix-core kernel for
  * gate/up + SwiGLU and the LM head, where the weights have tiled copies;
- * 2: the matrix-core kernel wherever it fits */
+ * 2: the matrix-core kernel wherever it fits; 3: as 1, with every Q6_K
+ * launch on the reference layout (no unit-layout copies) */
 int g_path = 1;
 
 int rows_out(const MvArgs &a, int mode) {
@@ -533,7 +622,7 @@ void plan(int dt, int mode, const MvArgs &a, int total, MxPlan &p, int &r, int &
   const int nt = p.G * p.L;
   maxnt = nt <= 256 ? 256 : nt <= 512 ? 512 : 1024;
   if (maxnt == 1024)
-    r = dt == GQ_Q4_K ? 4 : 2; /* 1024 threads leave 128 VGPRs: 4 rows of Q6_K or Q8_0 spill */
+    r = dt == GQ_Q4_K || dt == GQ_Q6_KX ? 4 : 2; /* 1024 threads leave 128 VGPRs: 4 rows of Q6_K or Q8_0 spill */
   else if (dt == GQ_Q8_0)
     r = 4;
   else if (dt == GQ_Q6_K && total >= 4096)
@@ -547,8 +636,8 @@ void plan(int dt, int mode, const MvArgs &a, int total, MxPlan &p, int &r, int &
       return true;
     };
     if (!fits(r)) {
-      if (maxnt == 1024 && dt != GQ_Q4_K) r = fits(2) ? 2 : 0;
-      else r = fits(4) ? 4 : fits(6) && maxnt != 1024 && dt != GQ_Q8_0 ? 6 : 0;
+      if (maxnt == 1024 && dt != GQ_Q4_K && dt != GQ_Q6_KX) r = fits(2) ? 2 : 0;
+      else r = fits(4) ? 4 : fits(6) && maxnt != 1024 && dt != GQ_Q8_0 && dt != GQ_Q6_KX ? 6 : 0;
     }
   }
   p.total = total;
@@ -557,7 +646,7 @@ void plan(int dt, int mode, const MvArgs &a, int total, MxPlan &p, int &r, int &
   p.nwg = (ngroups + p.G - 1) / p.G;
   int qk = 256, bb = 0;
   if (dt == GQ_Q4_K) bb = 144;
-  else if (dt == GQ_Q6_K) bb = 210;
+  else if (dt == GQ_Q6_K || dt == GQ_Q6_KX) bb = 210;
   else bb = 34, qk = 32;
   p.rowbytes = (a.cols / qk) * bb;
 }
@@ -585,7 +674,8 @@ int launch_fl(const MvArgs &a, const MxPlan &p, hipStream_t s) {
 template <int DT, int MODE, int R>
 int launch_r(const MvArgs &a, const MxPlan &p, int segw, int maxnt, hipStream_t s) {
   if (maxnt == 1024) {
-    if constexpr ((R == 4 && DT == GQ_Q4_K) || (R == 2 && DT != GQ_Q4_K)) {
+    constexpr bool four = DT == GQ_Q4_K || DT == GQ_Q6_KX;
+    if constexpr ((R == 4 && four) || (R == 2 && !four)) {
       if (p.nt > 1)
         return segw == 16 ? launch_fl<DT, MODE, R, 16, 1024, kMT>(a, p, s) : launch_fl<DT, MODE, R, 8, 1024, kMT>(a, p, s);
       return segw == 16 ? launch_fl<DT, MODE, R, 16, 1024, 0>(a, p, s) : launch_fl<DT, MODE, R, 8, 1024, 0>(a, p, s);
@@ -617,7 +707,8 @@ int launch_mvx(const MvArgs &a, int total, hipStream_t s) {
     return r == 2 ? launch_r<DT, MODE, 2>(a, p, segw, maxnt, s) : launch_r<DT, MODE, 4>(a, p, segw, maxnt, s);
   } else {
     if (r == 8) return launch_r<DT, MODE, 8>(a, p, segw, maxnt, s);
-    if (r == 6) return launch_r<DT, MODE, 6>(a, p, segw, maxnt, s);
+    if constexpr (DT != GQ_Q6_KX)
+      if (r == 6) return launch_r<DT, MODE, 6>(a, p, segw, maxnt, s);
     if constexpr (DT == GQ_Q6_K)
       if (r == 2) return launch_r<DT, MODE, 2>(a, p, segw, maxnt, s);
     return launch_r<DT, MODE, 4>(a, p, segw, maxnt, s);
@@ -667,9 +758,19 @@ int launch_dt(int mode, const MvArgs &a, int total, hipStream_t s) {
 
 } // namespace
 
+size_t gq_q6k_units_bytes(int rows, int cols) { return (size_t)rows * (size_t)(cols / 256) * 210; }
+
+int gq_launch_q6k_units(void *dst, const void *src, int rows, int cols, hipStream_t s) {
+  if (!dst || !src || rows <= 0 || cols <= 0 || cols % 512) return -1; /* an even count of blocks per row */
+  const long long n = (long long)rows * (cols / 32);
+  hipLaunchKernelGGL(q6k_units_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (const uint8_t *)src,
+                     (uint8_t *)dst, rows, cols / 256);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
 extern "C" int gq_hip_set_matvec_path(int path) {
   const int prev = g_path;
-  if (path >= 0 && path <= 2) g_path = path;
+  if (path >= 0 && path <= 3) g_path = path;
   return prev;
 }
 
@@ -684,10 +785,16 @@ int gq_launch_matvec(int dtype, int mode, const MvArgs &a, hipStream_t s) {
    * exists: gate/up + SwiGLU (8B decode: 14.9 us against 16-17 on the
    * vector ALUs) and the LM head (>= 16384 rows) by default */
   const bool mm = a.mm && (dtype == GQ_Q4_K || dtype == GQ_Q6_K) &&
-                  (g_path == 2 || (g_path == 1 && (mode == MV_SWIGLU || (mode == MV_STORE && total >= 16384))));
+                  (g_path == 2 || ((g_path == 1 || g_path == 3) && (mode == MV_SWIGLU || (mode == MV_STORE && total >= 16384))));
   if (mm) {
     const int rc = gq_launch_mm(dtype, mode, a, s);
     if (rc <= 0) return rc;
+  }
+  /* Q6_K residual launches with a unit-layout copy (the down projection) */
+  if (dtype == GQ_Q6_K && a.dx && g_path != 3 && a.nseg == 1 && mode == MV_RESID && (a.cols / 256) % 2 == 0) {
+    MvArgs b = a;
+    b.seg[0].w = a.dx;
+    return launch_mvx<GQ_Q6_KX, MV_RESID>(b, total, s);
   }
   switch (dtype) {
   case GQ_Q4_K: return launch_dt<GQ_Q4_K>(mode, a, total, s);

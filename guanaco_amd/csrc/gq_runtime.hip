@@ -77,6 +77,7 @@ struct gq_ctx {
    * NULL where a weight does not take that layout */
   struct MmLayer {
     const uint8_t *gu = nullptr;
+    const uint8_t *dx = nullptr; /* Q6_K down in the vector-ALU unit layout (gq_launch_q6k_units) */
   };
   std::vector<MmLayer> mm;
   const uint8_t *mm_lm = nullptr;
@@ -771,7 +772,7 @@ static void mm_free(gq_ctx *c) {
     if (p) gq_hip_free(c, (void *)p);
     p = nullptr;
   };
-  for (auto &L : c->mm) rel(L.gu);
+  for (auto &L : c->mm) rel(L.gu), rel(L.dx);
   c->mm.clear();
   rel(c->mm_lm);
 }
@@ -820,6 +821,13 @@ extern "C" int gq_hip_model_bind(gq_ctx *c, const gq_model *m) {
     const gq_layer &L = c->layers[l];
     const gq_weight *gu[2] = {&L.w_gate, &L.w_up};
     if (L.w_gate.dtype == L.w_up.dtype) c->mm[l].gu = mm_build(c, gu, 2, true);
+    /* the down projection's Q6_K rows re-laid out so 8-row groups fit the
+     * vector-ALU kernel's registers (one round of workgroups) */
+    if (L.w_down.dtype == GQ_Q6_K && L.w_down.cols % 512 == 0) {
+      uint8_t *d = (uint8_t *)dev_alloc(c, gq_q6k_units_bytes(L.w_down.rows, L.w_down.cols));
+      if (d && gq_launch_q6k_units(d, L.w_down.data, L.w_down.rows, L.w_down.cols, c->stream) == 0) c->mm[l].dx = d;
+      else if (d) gq_hip_free(c, d);
+    }
   }
   {
     const gq_weight *lm[1] = {&m->lm_head};
@@ -982,6 +990,7 @@ static int op_down(gq_ctx *c, int l, float *hidden) {
   MvArgs a{};
   a.seg[0] = MvSeg{(const uint8_t *)L.w_down.data, hidden, hidden, L.w_down.rows};
   a.nseg = 1, a.cols = L.w_down.cols, a.x = c->ws.act;
+  a.dx = (size_t)l < c->mm.size() ? c->mm[l].dx : nullptr;
   const int rc = gq_launch_matvec(L.w_down.dtype, MV_RESID, a, c->stream);
   if (rc) return rc;
   mark(c, PC_DOWN, mv_bytes(L.w_down, 1));

@@ -111,7 +111,7 @@ def _load():
 lib, EXPORTS = _load()
 NCLASS = 7
 CLASS_NAMES = ("qkv", "attention", "o_proj", "gate_up", "down", "lm_head", "other")
-MATVEC_PATHS = ("valu", "auto", "mfma")
+MATVEC_PATHS = ("valu", "auto", "mfma", "auto_q6k_ref")
 
 
 class matvec_path:
@@ -120,7 +120,9 @@ class matvec_path:
     the vector-ALU kernel for the rest; "valu" the vector-ALU kernel for
     every launch; "mfma" the int8 matrix-core kernel wherever it fits
     (Q4_K/Q6_K; the op-level entry points tile their weights per call),
-    else the vector-ALU kernel."""
+    else the vector-ALU kernel; "auto_q6k_ref" as "auto" with the Q6_K down
+    projection read from the reference layout instead of the unit-layout
+    copy made at model bind."""
 
     def __init__(self, name):
         self.lds = MATVEC_PATHS.index(name)

@@ -234,7 +234,9 @@ float gq_hip_time_matvec(gq_ctx *ctx, int dtype, const void *const *w_devs, int 
  * vector-ALU kernel for every other launch; 0 the vector-ALU kernel for
  * every launch; 2 the matrix-core kernel wherever it fits (the op-level
  * entry points then tile their weights per call), else the vector-ALU
- * kernel.  Returns the previous setting.  No reference counterpart: a switch
+ * kernel; 3 as 1, with the Q6_K down projection read from the reference
+ * layout instead of the unit-layout copy gq_hip_model_bind makes for the
+ * vector-ALU kernel.  Returns the previous setting.  No reference counterpart: a switch
  * for the parity tests (each kernel against the oracle) and for timing. */
 int gq_hip_set_matvec_path(int path);
 /* Device time of n launches of the attention kernels for one layer. */

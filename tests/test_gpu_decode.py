@@ -52,6 +52,31 @@ def _forward_per_layer_and_tokens(ctx, orc, spec, pre, hm, dm):
     print("worst per-layer rel L2", worst)
 
 
+@pytest.mark.parametrize("name", ["tiny-test", "wide-ff-test"])
+def test_q6k_unit_layout_bit_identical(name):
+    """The Q6_K down projection read from the vector-ALU unit layout (the
+    copy gq_hip_model_bind makes; 4-row groups in the 1024-thread launches
+    of wide-ff's 28672-column rows) gives the reference layout's results bit
+    for bit: the same products in the same order."""
+    import guanaco_amd.hip as H
+    from util import bits
+    spec = S.PRESETS[name]
+    c = H.Context(0)
+    try:
+        ms, pre = 64, 24
+        dm = H.DeviceModel(c, spec, ms, prefill=pre)
+        out = {}
+        for path in ("auto", "auto_q6k_ref"):
+            with H.matvec_path(path):
+                c.kv_prefill_synth(11, 12, pre)
+                out[path] = [dm.forward(7 + i, pre + i, want_hidden=True) for i in range(3)]
+        for a, b in zip(out["auto"], out["auto_q6k_ref"]):
+            assert a[0] == b[0]
+            assert np.array_equal(bits(a[1]), bits(b[1])) and np.array_equal(bits(a[2]), bits(b[2]))
+    finally:
+        c.close()
+
+
 def test_graph_loop_matches_eager_and_oracle(ctx, orc, tiny):
     spec, ms, pre, hm, dm = tiny
     from guanaco_amd.synth import tensor_seed
