@@ -77,6 +77,25 @@ def test_q6k_unit_layout_bit_identical(name):
         c.close()
 
 
+def test_forward_q6k_down_odd_blocks(orc):
+    """A Q6_K down projection whose rows hold an odd count of 256-column
+    blocks (ff 768) gets no unit-layout copy (its rows would start at a
+    2-byte phase) and reads the reference layout: per-layer hidden states and
+    tokens against the oracle as for the other models."""
+    import guanaco_amd.hip as H
+    from oracle import HostModel
+    spec = S.ModelSpec("odd-ff-test", n_layers=2, hidden=512, ff=768, n_heads=8, n_kv_heads=2, vocab=1000,
+                       layer_dtypes=dict(wd=S.Q6_K))
+    c = H.Context(0)
+    try:
+        ms, pre = 64, 24
+        hm = HostModel(orc, spec, ms)
+        dm = H.DeviceModel(c, spec, ms, prefill=pre)
+        _forward_per_layer_and_tokens(c, orc, spec, pre, hm, dm)
+    finally:
+        c.close()
+
+
 def test_graph_loop_matches_eager_and_oracle(ctx, orc, tiny):
     spec, ms, pre, hm, dm = tiny
     from guanaco_amd.synth import tensor_seed
