@@ -34,6 +34,8 @@ enum { SEG_PLAIN = 0, SEG_ROPE = 1, SEG_ROPE_KV = 2, SEG_KV = 3 };
 /* Q6_K in the vector-ALU matvec's unit layout: an internal weight type,
  * never seen at the C ABI */
 #define GQ_Q6_KX 65
+/* Q6_K in the prefill GEMM's step layout (gq_launch_q6k_steps): internal too */
+#define GQ_Q6_KP 66
 
 struct MvSeg {
   const uint8_t *w;
@@ -163,6 +165,8 @@ int gq_launch_q6k_units(void *dst, const void *src, int rows, int cols, hipStrea
  * (gq_hip_set_matvec_path(2)): the op-level entry points then tile their
  * weights per call */
 bool gq_matvec_mm_forced();
+/* matvec path 3: every Q6_K launch on the reference layout (no re-laid copies) */
+bool gq_matvec_q6k_ref();
 
 /* ---- attention -------------------------------------------------------- */
 struct AttnArgs {
@@ -255,6 +259,12 @@ struct PgArgs {
   int nseg, T, K;
 };
 int gq_launch_pgemm(int mode, const PgArgs &a, hipStream_t s);
+/* Q6_K weights (rows x cols, cols a multiple of 2048) re-laid out for the
+ * prefill GEMM: each 64-weight step's quant bytes together, then the scales
+ * and d, the same bytes (gq_q6k_steps_bytes); segments then take dtype
+ * GQ_Q6_KP. */
+size_t gq_q6k_steps_bytes(int rows, int cols);
+int gq_launch_q6k_steps(void *dst, const void *src, int rows, int cols, hipStream_t s);
 int gq_launch_to_bf16(const float *x, __bf16 *y, size_t n, hipStream_t s);
 /* RMSNorm of `rows` consecutive rows of dim floats, one workgroup per row;
  * out16 != NULL writes bf16 there instead of fp32 to out */

@@ -775,6 +775,7 @@ extern "C" int gq_hip_set_matvec_path(int path) {
 }
 
 bool gq_matvec_mm_forced() { return g_path == 2; }
+bool gq_matvec_q6k_ref() { return g_path == 3; }
 
 int gq_launch_matvec(int dtype, int mode, const MvArgs &a, hipStream_t s) {
   if (dtype != GQ_Q4_K && dtype != GQ_Q6_K && dtype != GQ_Q8_0) return -1;

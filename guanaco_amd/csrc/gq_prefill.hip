@@ -223,6 +223,116 @@ struct PW<GQ_Q6_K> {
   }
 };
 
+
+/* Q6_K in the prefill step layout (gq_launch_q6k_steps, made once at model
+ * bind for rows whose 210-byte blocks fall on 16-byte boundaries, K % 2048
+ * == 0): per row, the 48 quant bytes of each 64-weight step s at 48 s (32
+ * bytes whose byte j holds the 4-bit parts of step weights j (low nibble)
+ * and j + 32 (high nibble), then 16 bytes whose byte j holds the 2-bit parts
+ * of weights j, j + 16, j + 32, j + 48 at bits 0, 2, 4, 6), the blocks'
+ * 16 scale bytes as they are at 192 nb, their d at 208 nb: the same 210
+ * bytes per block.  A wave stages its 32 rows' step in two 16-byte DMA
+ * instructions plus one dword instruction (scales and d) instead of the
+ * reference layout's fifteen dword instructions, and reads every quant
+ * byte once.  Weights and their order are the reference layout's, so the
+ * GEMM's results are bit-identical to it. */
+template <>
+struct PW<GQ_Q6_KP> {
+  static constexpr int BB = 210;
+  static constexpr int kWaveLds = 2048 + 256; /* quants (96 16-byte pieces), then 32 scale + 32 d dwords */
+  static constexpr int kDma = 3;
+  struct Plan {
+    uint32_t off[3];
+    bool on[2];
+    bool dlane; /* lanes 32..63 of the dword instruction fetch the d pair */
+  };
+  __device__ static void plan(Plan &p, int lane, uint32_t rowbytes) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int pc = 64 * i + lane, row = pc / 3, part = pc - 3 * row;
+      p.on[i] = pc < 96;
+      p.off[i] = (uint32_t)row * rowbytes + 16u * (uint32_t)part;
+    }
+    const uint32_t nb = rowbytes / 210u;
+    p.dlane = lane >= 32;
+    p.off[2] = (uint32_t)(lane & 31) * rowbytes + (p.dlane ? 208u : 192u) * nb;
+  }
+  __device__ static void issue(const Plan &p, const uint8_t *w, int s, uint32_t lds) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const uint32_t d = __builtin_amdgcn_readfirstlane(lds + 1024u * i);
+      if (p.on[i]) dma16(w + p.off[i] + (size_t)48 * s, d);
+    }
+    dma4(w + p.off[2] + (p.dlane ? 4u * (uint32_t)(s >> 3) : 4u * (uint32_t)s),
+         __builtin_amdgcn_readfirstlane(lds + 2048u));
+  }
+  struct Raw {
+    uint2 q0, q1, hb;
+    uint32_t sc, dd;
+  };
+  __device__ static void read(Raw &w, const GQ_LDS uint8_t *ws, int lane, int) {
+    const uint32_t r = (uint32_t)(lane & 31), h = (uint32_t)(lane >> 5);
+    w.q0 = lld<uint2>(ws, 48u * r + 8u * h);
+    w.q1 = lld<uint2>(ws, 48u * r + 16u + 8u * h);
+    w.hb = lld<uint2>(ws, 48u * r + 32u + 8u * h);
+    w.sc = lld<uint32_t>(ws, 2048u + 4u * r);
+    w.dd = lld<uint32_t>(ws, 2176u + 4u * r);
+  }
+  /* w = (d sc) q - 32 (d sc) as PW<GQ_Q6_K>::dequant (the same roundings) */
+  __device__ static void dequant(const Raw &rw, int s, gq_bf16x8 b[4]) {
+    const float d = gq_h2f(rw.dd >> (16u * (uint32_t)((s >> 2) & 1)));
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+      const float a = d * (float)(int8_t)((rw.sc >> (8 * kk)) & 0xffu);
+      const float m = 32.0f * a;
+      const uint2 q = (kk & 1) ? rw.q1 : rw.q0;
+      const uint32_t sh = kk >= 2 ? 4u : 0u;
+      const uint32_t pw[2] = {q.x, q.y}, hw[2] = {rw.hb.x, rw.hb.y};
+      uint32_t o[4];
+#pragma unroll
+      for (int k = 0; k < 2; k++) {
+        const uint32_t u = ((pw[k] >> sh) & 0x0f0f0f0fu) | (((hw[k] >> (2 * kk)) & 0x03030303u) << 4);
+        const float v0 = __builtin_fmaf(a, (float)(u & 0xffu), -m);
+        const float v1 = __builtin_fmaf(a, (float)((u >> 8) & 0xffu), -m);
+        const float v2 = __builtin_fmaf(a, (float)((u >> 16) & 0xffu), -m);
+        const float v3 = __builtin_fmaf(a, (float)(u >> 24), -m);
+        o[2 * k] = pack_bf16x2(v0, v1);
+        o[2 * k + 1] = pack_bf16x2(v2, v3);
+      }
+      b[kk] = __builtin_bit_cast(gq_bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
+    }
+  }
+};
+
+/* One thread per (row, step): a Q6_K row in the reference layout (src) to the
+ * step layout above (dst, same size). */
+__global__ __launch_bounds__(256) void q6k_steps_kernel(const uint8_t *src, uint8_t *dst, int rows, int nb) {
+  const int sp = 4 * nb;
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (long long)rows * sp) return;
+  const int row = (int)(t / sp), s = (int)(t - (long long)row * sp);
+  const int b = s >> 2, cc = s & 3, n = cc >> 1, par = cc & 1;
+  const uint8_t *blk = src + ((size_t)row * nb + b) * 210;
+  uint8_t *drow = dst + (size_t)row * nb * 210, *dq = drow + 48 * s;
+  /* step weight tt < 64 is block weight 128 n + 32 g + l, g = 2 par + tt / 32,
+   * l = tt % 32 (quant_matvec_q6_k.c:70-90) */
+  auto q4 = [&](int tt) -> uint32_t {
+    const int g = 2 * par + (tt >> 5), l = tt & 31;
+    return ((uint32_t)blk[64 * n + 32 * (g & 1) + l] >> (4 * (g >> 1))) & 15u;
+  };
+  auto q2 = [&](int tt) -> uint32_t {
+    const int g = 2 * par + (tt >> 5), l = tt & 31;
+    return ((uint32_t)blk[128 + 32 * n + l] >> (2 * g)) & 3u;
+  };
+  for (int j = 0; j < 32; j++) dq[j] = (uint8_t)(q4(j) | (q4(j + 32) << 4));
+  for (int j = 0; j < 16; j++) dq[32 + j] = (uint8_t)(q2(j) | (q2(j + 16) << 2) | (q2(j + 32) << 4) | (q2(j + 48) << 6));
+  for (int k = 0; k < 4; k++) drow[192 * nb + 4 * s + k] = blk[192 + 4 * cc + k];
+  if (cc == 0) {
+    drow[208 * nb + 2 * b] = blk[208];
+    drow[208 * nb + 2 * b + 1] = blk[209];
+  }
+}
+
 /* KS = 1 or 2 K-splits per workgroup: with KS = 2, eight waves, the second
  * four running the upper half of K for the same tile; their sums are added
  * through LDS at the end.  Two waves per SIMD hide each other's LDS, DMA and
@@ -249,6 +359,7 @@ constexpr bool fits() {
   return ring<DT, KS, TT>() >= 3 && (ring<DT, KS, TT>() - 2) * (TT + PW<DT>::kDma) < 64;
 }
 static_assert(fits<GQ_Q4_K, 1, 2>() && fits<GQ_Q4_K, 2, 2>() && fits<GQ_Q6_K, 1, 2>() && fits<GQ_Q6_K, 2, 2>() &&
+                  fits<GQ_Q6_KP, 1, 2>() && fits<GQ_Q6_KP, 2, 2>() &&
                   fits<GQ_Q4_K, 1, 4>() && fits<GQ_Q4_K, 2, 4>(),
               "ring shapes");
 
@@ -387,9 +498,11 @@ __global__ __launch_bounds__(kPThreads * KS) void pgemm_kernel(PgArgs a) {
   const uint32_t rowbytes = (uint32_t)(a.K / 256) * (dt == GQ_Q4_K ? 144u : 210u);
   const uint8_t *w = S.w + (size_t)r0 * rowbytes;
   gq_f32x16 acc[TT];
-  if constexpr (fits<GQ_Q6_K, KS, TT>()) {
+  if constexpr (fits<GQ_Q6_K, KS, TT>() && fits<GQ_Q6_KP, KS, TT>()) {
     if (dt == GQ_Q4_K)
       tile_loop<GQ_Q4_K, KS, TT>(a, w, rowbytes, t0, smem, acc);
+    else if (dt == GQ_Q6_KP)
+      tile_loop<GQ_Q6_KP, KS, TT>(a, w, rowbytes, t0, smem, acc);
     else
       tile_loop<GQ_Q6_K, KS, TT>(a, w, rowbytes, t0, smem, acc);
   } else { /* the launcher sends Q6_K to shapes that fit */
@@ -492,9 +605,10 @@ int launch_shape(const PgArgs &a, int row_tiles, size_t lds, hipStream_t s) {
 
 template <int MODE>
 int launch_mode(const PgArgs &a, int row_tiles, hipStream_t s) {
-  bool q4 = false, q6 = false;
-  for (int i = 0; i < a.nseg; i++) q4 |= a.seg[i].dtype == GQ_Q4_K, q6 |= a.seg[i].dtype == GQ_Q6_K;
-  const int tt = !q6 && row_tiles * ((a.T + 127) / 128) >= n_cus() ? 4 : 2;
+  bool q4 = false, q6 = false, q6p = false;
+  for (int i = 0; i < a.nseg; i++)
+    q4 |= a.seg[i].dtype == GQ_Q4_K, q6 |= a.seg[i].dtype == GQ_Q6_K, q6p |= a.seg[i].dtype == GQ_Q6_KP;
+  const int tt = !q6 && !q6p && row_tiles * ((a.T + 127) / 128) >= n_cus() ? 4 : 2;
   const int wgs = row_tiles * ((a.T + 32 * tt - 1) / (32 * tt));
   int ks = wgs <= n_cus() ? 2 : 1;
   if ((a.K / kBK) % 2) ks = 1;
@@ -503,10 +617,12 @@ int launch_mode(const PgArgs &a, int row_tiles, hipStream_t s) {
     return ks == 2 ? launch_shape<MODE, 2, 4>(a, row_tiles, lds, s) : launch_shape<MODE, 1, 4>(a, row_tiles, lds, s);
   }
   if (ks == 2) {
-    const size_t lds = std::max(q6 ? ring_bytes<GQ_Q6_K, 2, 2>() : 0, q4 ? ring_bytes<GQ_Q4_K, 2, 2>() : 0);
+    const size_t lds = std::max({q6 ? ring_bytes<GQ_Q6_K, 2, 2>() : 0, q6p ? ring_bytes<GQ_Q6_KP, 2, 2>() : 0,
+                                 q4 ? ring_bytes<GQ_Q4_K, 2, 2>() : 0});
     return launch_shape<MODE, 2, 2>(a, row_tiles, lds, s);
   }
-  const size_t lds = std::max(q6 ? ring_bytes<GQ_Q6_K, 1, 2>() : 0, q4 ? ring_bytes<GQ_Q4_K, 1, 2>() : 0);
+  const size_t lds = std::max({q6 ? ring_bytes<GQ_Q6_K, 1, 2>() : 0, q6p ? ring_bytes<GQ_Q6_KP, 1, 2>() : 0,
+                               q4 ? ring_bytes<GQ_Q4_K, 1, 2>() : 0});
   return launch_shape<MODE, 1, 2>(a, row_tiles, lds, s);
 }
 
@@ -518,8 +634,8 @@ int gq_launch_pgemm(int mode, const PgArgs &a, hipStream_t s) {
   for (int i = 0; i < a.nseg; i++) {
     const PgSeg &g = a.seg[i];
     if (!g.w || g.rows <= 0) return -1;
-    if (g.dtype != GQ_Q4_K && g.dtype != GQ_Q6_K) return -1;
-    if (g.dtype == GQ_Q6_K && a.K % 512) return -2;
+    if (g.dtype != GQ_Q4_K && g.dtype != GQ_Q6_K && g.dtype != GQ_Q6_KP) return -1;
+    if ((g.dtype == GQ_Q6_K && a.K % 512) || (g.dtype == GQ_Q6_KP && a.K % 2048)) return -2;
     if (mode == MV_SWIGLU) {
       if (g.rows % (kBN / 2) || g.dtype != a.seg[0].dtype || g.rows != a.seg[0].rows) return -1;
     } else {
@@ -542,6 +658,16 @@ int gq_launch_pgemm(int mode, const PgArgs &a, hipStream_t s) {
   if (mode == MV_RESID) return launch_mode<MV_RESID>(a, tiles, s);
   if (mode == MV_STORE) return launch_mode<MV_STORE>(a, tiles, s);
   return -1;
+}
+
+size_t gq_q6k_steps_bytes(int rows, int cols) { return (size_t)rows * (size_t)(cols / 256) * 210; }
+
+int gq_launch_q6k_steps(void *dst, const void *src, int rows, int cols, hipStream_t s) {
+  if (!dst || !src || rows <= 0 || cols <= 0 || cols % 2048) return -1; /* 16-byte aligned rows */
+  const long long n = (long long)rows * (cols / 64);
+  hipLaunchKernelGGL(q6k_steps_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (const uint8_t *)src,
+                     (uint8_t *)dst, rows, cols / 256);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
 int gq_launch_to_bf16(const float *x, __bf16 *y, size_t n, hipStream_t s) {

@@ -78,6 +78,9 @@ struct gq_ctx {
   struct MmLayer {
     const uint8_t *gu = nullptr;
     const uint8_t *dx = nullptr; /* Q6_K down in the vector-ALU unit layout (gq_launch_q6k_units) */
+    /* Q6_K projections in the prefill GEMM's step layout (gq_launch_q6k_steps):
+     * wq, wk, wv, wo, gate, up, down */
+    const uint8_t *ps[7] = {};
   };
   std::vector<MmLayer> mm;
   const uint8_t *mm_lm = nullptr;
@@ -373,7 +376,7 @@ static int launch_one_mv(gq_ctx *c, int dtype, const void *w, int rows, int cols
 }
 
 /* The op-level entry points take weights in the reference layout; with the
- * matrix-core kernel selected explicitly (path 5) they tile a copy for the
+ * matrix-core kernel selected explicitly (path 2) they tile a copy for the
  * call (freed by the caller with gq_hip_free after the stream is done). */
 static const uint8_t *op_tile(gq_ctx *c, int dtype, const void *w, int rows, int cols) {
   if (!gq_matvec_mm_forced() || (dtype != GQ_Q4_K && dtype != GQ_Q6_K)) return nullptr;
@@ -772,7 +775,10 @@ static void mm_free(gq_ctx *c) {
     if (p) gq_hip_free(c, (void *)p);
     p = nullptr;
   };
-  for (auto &L : c->mm) rel(L.gu), rel(L.dx);
+  for (auto &L : c->mm) {
+    rel(L.gu), rel(L.dx);
+    for (auto &p : L.ps) rel(p);
+  }
   c->mm.clear();
   rel(c->mm_lm);
 }
@@ -826,6 +832,16 @@ extern "C" int gq_hip_model_bind(gq_ctx *c, const gq_model *m) {
     if (L.w_down.dtype == GQ_Q6_K && L.w_down.cols % 512 == 0) {
       uint8_t *d = (uint8_t *)dev_alloc(c, gq_q6k_units_bytes(L.w_down.rows, L.w_down.cols));
       if (d && gq_launch_q6k_units(d, L.w_down.data, L.w_down.rows, L.w_down.cols, c->stream) == 0) c->mm[l].dx = d;
+      else if (d) gq_hip_free(c, d);
+    }
+    /* Q6_K projections the prefill GEMM takes, re-laid out so a step's quant
+     * bytes are one 16-byte-aligned range (rows on 16-byte boundaries) */
+    const gq_weight *pw[7] = {&L.wq, &L.wk, &L.wv, &L.wo, &L.w_gate, &L.w_up, &L.w_down};
+    for (int i = 0; i < 7; i++) {
+      const gq_weight &g = *pw[i];
+      if (g.dtype != GQ_Q6_K || g.cols % 2048 || g.rows % 128) continue;
+      uint8_t *d = (uint8_t *)dev_alloc(c, gq_q6k_steps_bytes(g.rows, g.cols));
+      if (d && gq_launch_q6k_steps(d, g.data, g.rows, g.cols, c->stream) == 0) c->mm[l].ps[i] = d;
       else if (d) gq_hip_free(c, d);
     }
   }
@@ -1224,7 +1240,12 @@ static bool pf_model_ok(const gq_ctx *c) {
   return true;
 }
 
-static PgSeg pg_seg(const gq_weight &w, float *y) { return PgSeg{(const uint8_t *)w.data, y, w.rows, w.dtype}; }
+/* weight i (wq, wk, wv, wo, gate, up, down) of layer l as a GEMM segment:
+ * its step-layout copy where model bind made one */
+static PgSeg pg_seg(const gq_ctx *c, int l, int i, const gq_weight &w, float *y) {
+  const uint8_t *ps = (size_t)l < c->mm.size() && !gq_matvec_q6k_ref() ? c->mm[l].ps[i] : nullptr;
+  return ps ? PgSeg{ps, y, w.rows, GQ_Q6_KP} : PgSeg{(const uint8_t *)w.data, y, w.rows, w.dtype};
+}
 
 /* RoPE + append of T tokens at pos..pos+T-1 (q: T x n_heads*hd in place,
  * k/v: T x n_kv*hd), then causal attention of the T tokens into out (fp32)
@@ -1255,11 +1276,12 @@ static int pf_layer(gq_ctx *c, int l, int pos, int T) {
   PgArgs qkv{}, o{}, gu{}, dn{};
   qkv.T = o.T = gu.T = dn.T = T;
   qkv.x = w.xn, qkv.K = m.hidden, qkv.nseg = 3;
-  qkv.seg[0] = pg_seg(L.wq, w.q), qkv.seg[1] = pg_seg(L.wk, w.k), qkv.seg[2] = pg_seg(L.wv, w.v);
-  o.x = w.att, o.K = m.hidden, o.nseg = 1, o.seg[0] = pg_seg(L.wo, w.x);
+  qkv.seg[0] = pg_seg(c, l, 0, L.wq, w.q), qkv.seg[1] = pg_seg(c, l, 1, L.wk, w.k);
+  qkv.seg[2] = pg_seg(c, l, 2, L.wv, w.v);
+  o.x = w.att, o.K = m.hidden, o.nseg = 1, o.seg[0] = pg_seg(c, l, 3, L.wo, w.x);
   gu.x = w.xn, gu.K = m.hidden, gu.nseg = 2, gu.act = w.act;
-  gu.seg[0] = pg_seg(L.w_gate, nullptr), gu.seg[1] = pg_seg(L.w_up, nullptr);
-  dn.x = w.act, dn.K = m.ff, dn.nseg = 1, dn.seg[0] = pg_seg(L.w_down, w.x);
+  gu.seg[0] = pg_seg(c, l, 4, L.w_gate, nullptr), gu.seg[1] = pg_seg(c, l, 5, L.w_up, nullptr);
+  dn.x = w.act, dn.K = m.ff, dn.nseg = 1, dn.seg[0] = pg_seg(c, l, 6, L.w_down, w.x);
   if ((rc = gq_launch_rmsnorm_rows(w.x, L.rms_att, nullptr, m.hidden, T, m.rms_eps, c->stream, w.xn)) ||
       (rc = gq_launch_pgemm(MV_STORE, qkv, c->stream)) ||
       (rc = pf_attention(c, l, pos, T, m.n_heads, w.q, w.k, w.v, nullptr, w.att)) ||
@@ -1662,6 +1684,23 @@ extern "C" int gq_hip_chat_turn(gq_ctx *c, const int32_t *tokens, int n_tokens, 
   return n;
 }
 
+/* Q6_K weights the prefill GEMM can read in its step layout (cols % 2048):
+ * a copy for the call, as a bound model keeps from gq_hip_model_bind;
+ * matvec path 3 keeps the reference layout.  Freed by the caller. */
+static const uint8_t *op_steps(gq_ctx *c, int dtype, const void *w, int rows, int cols) {
+  if (dtype != GQ_Q6_K || cols % 2048 || gq_matvec_q6k_ref()) return nullptr;
+  uint8_t *d = (uint8_t *)dev_alloc(c, gq_q6k_steps_bytes(rows, cols));
+  if (d && gq_launch_q6k_steps(d, w, rows, cols, c->stream)) {
+    gq_hip_free(c, d);
+    return nullptr;
+  }
+  return d;
+}
+
+static PgSeg op_seg(const uint8_t *ps, const void *w, float *y, int n, int dtype) {
+  return ps ? PgSeg{ps, y, n, GQ_Q6_KP} : PgSeg{(const uint8_t *)w, y, n, dtype};
+}
+
 /* fp32 x -> the bf16 copy the GEMM reads */
 static const __bf16 *pf_x16(gq_ctx *c, const float *x, size_t n) {
   PrefillWs &w = c->pf;
@@ -1678,11 +1717,40 @@ extern "C" int gq_hip_prefill_gemm_dev(gq_ctx *c, int dtype, int mode, const voi
   if (n % 128) return fail(c, -1, "prefill GEMM: rows must be a multiple of 128");
   PgArgs a{};
   if (!(a.x = pf_x16(c, x, (size_t)t * k))) return fail(c, -4, "prefill GEMM: x conversion");
-  a.T = t, a.K = k, a.nseg = 1, a.seg[0] = PgSeg{(const uint8_t *)w, y, n, dtype};
+  const uint8_t *ps = op_steps(c, dtype, w, n, k);
+  a.T = t, a.K = k, a.nseg = 1, a.seg[0] = op_seg(ps, w, y, n, dtype);
   if (mode == 1 && r != y)
     HIPCHK(c, hipMemcpyAsync(y, r, sizeof(float) * (size_t)t * n, hipMemcpyDeviceToDevice, c->stream));
   const int rc = gq_launch_pgemm(mode == 1 ? MV_RESID : MV_STORE, a, c->stream);
+  if (ps) gq_hip_free(c, (void *)ps);
   return rc ? fail(c, rc, "prefill GEMM launch") : 0;
+}
+
+extern "C" float gq_hip_time_prefill_gemm(gq_ctx *c, int dtype, const void *w, int n, int k, const float *x, int t,
+                                         float *y, int n_iter) {
+  if (!c || !w || !x || !y || t <= 0 || n <= 0 || k <= 0 || n_iter <= 0) return fail(c, -1, "time GEMM: bad argument"), -1.f;
+  if (dtype != GQ_Q4_K && dtype != GQ_Q6_K) return fail(c, -1, "time GEMM: Q4_K or Q6_K weights only"), -1.f;
+  if (k % 256 || (dtype == GQ_Q6_K && k % 512) || n % 128) return fail(c, -2, "time GEMM: shape"), -1.f;
+  PgArgs a{};
+  if (!(a.x = pf_x16(c, x, (size_t)t * k))) return fail(c, -4, "time GEMM: x conversion"), -1.f;
+  const uint8_t *ps = op_steps(c, dtype, w, n, k);
+  a.T = t, a.K = k, a.nseg = 1, a.seg[0] = op_seg(ps, w, y, n, dtype);
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  int rc = hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess ? 0 : -4;
+  if (!rc) rc = gq_launch_pgemm(MV_STORE, a, c->stream); /* untimed first launch */
+  if (!rc) (void)hipEventRecord(e0, c->stream);
+  for (int i = 0; i < n_iter && !rc; i++) rc = gq_launch_pgemm(MV_STORE, a, c->stream);
+  float ms = 0.f;
+  if (!rc) {
+    (void)hipEventRecord(e1, c->stream);
+    (void)hipEventSynchronize(e1);
+    (void)hipEventElapsedTime(&ms, e0, e1);
+  }
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  if (ps) gq_hip_free(c, (void *)ps);
+  if (rc) return fail(c, rc, "time GEMM launch"), -1.f;
+  return ms / n_iter;
 }
 
 extern "C" int gq_hip_prefill_gate_up_dev(gq_ctx *c, int dtype, const void *w_gate, const void *w_up, int n, int k,
@@ -1694,10 +1762,13 @@ extern "C" int gq_hip_prefill_gate_up_dev(gq_ctx *c, int dtype, const void *w_ga
   if (n % 64) return fail(c, -1, "prefill gate/up: rows must be a multiple of 64");
   PgArgs a{};
   if (!(a.x = pf_x16(c, x, (size_t)t * k))) return fail(c, -4, "prefill gate/up: x conversion");
+  const uint8_t *pg = op_steps(c, dtype, w_gate, n, k), *pu = pg ? op_steps(c, dtype, w_up, n, k) : nullptr;
+  if (pg && !pu) gq_hip_free(c, (void *)pg), pg = nullptr;
   a.T = t, a.K = k, a.nseg = 2, a.act = (__bf16 *)act;
-  a.seg[0] = PgSeg{(const uint8_t *)w_gate, nullptr, n, dtype};
-  a.seg[1] = PgSeg{(const uint8_t *)w_up, nullptr, n, dtype};
+  a.seg[0] = op_seg(pg, w_gate, nullptr, n, dtype);
+  a.seg[1] = op_seg(pu, w_up, nullptr, n, dtype);
   const int rc = gq_launch_pgemm(MV_SWIGLU, a, c->stream);
+  if (pg) gq_hip_free(c, (void *)pg), gq_hip_free(c, (void *)pu);
   return rc ? fail(c, rc, "prefill gate/up launch") : 0;
 }
 

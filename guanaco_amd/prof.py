@@ -165,15 +165,12 @@ def config5(ctx, T=512, iters=20):
             x = ctx.synth_normal(T * K, 5)
             y = ctx.alloc(4 * T * N)
 
-            def go():
-                ctx.check(H.lib.gq_hip_prefill_gemm_dev(ctx.h, dt, 0, w.ptr, N, K, x.ptr, T, y.ptr, None), "gemm")
-            go()
-            ctx.sync()
-            t0 = time.perf_counter()
-            for _ in range(iters):
-                go()
-            ctx.sync()
-            dt_s = (time.perf_counter() - t0) / iters
+            # device time of the GEMM launches alone (x's bf16 copy and the
+            # Q6_K step-layout copy made before the timed region)
+            ms = H.lib.gq_hip_time_prefill_gemm(ctx.h, dt, w.ptr, N, K, x.ptr, T, y.ptr, iters)
+            if ms < 0:
+                ctx.raise_last("time_prefill_gemm")
+            dt_s = ms * 1e-3
             flop = 2.0 * T * N * K
             emit(config=5, what=f"prefill GEMM {name} {what}: {T} tokens x {N}x{K}", us_per_launch=round(dt_s * 1e6, 2),
                  gflop=round(flop / 1e9, 2), TFLOP_per_s=round(flop / dt_s / 1e12, 1),

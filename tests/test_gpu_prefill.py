@@ -156,7 +156,7 @@ def silu_mul_f32(g, u):
 
 
 @pytest.mark.parametrize("dtype,T,N,K", [(S.Q4_K, 512, 1024, 4096), (S.Q4_K, 70, 192, 512),
-                                         (S.Q6_K, 100, 256, 1024)])
+                                         (S.Q6_K, 100, 256, 1024), (S.Q6_K, 100, 256, 4096)])
 def test_prefill_gate_up_swiglu(ctx, orc, dtype, T, N, K):
     """gate and up in one launch with SiLU(gate) * up in the epilogue
     (kernels_cpu.c:312-389), bf16 out: against the exact-input reference
@@ -279,6 +279,61 @@ def test_prefill_model_vs_oracle(ctx, orc, pre, T, ms):
     t_cpu2, lc2, _ = hm.forward(kv, t_cpu, pre + T)
     assert rel_l2(lg2, lc2) < PF_TOL and t_gpu == t_cpu2
     print(f"prefill T={T} pre={pre}: logits rel {rel_l2(lg, lc):.2e}, device {ms_dev:.3f} ms")
+
+
+@pytest.mark.parametrize("T,N,K,mode", [(96, 256, 4096, 0), (77, 384, 2048, 1), (512, 4096, 14336, 1)])
+def test_prefill_q6k_step_layout_bit_identical(ctx, orc, T, N, K, mode):
+    """Q6_K weights whose rows fall on 16-byte boundaries (K % 2048 == 0) go
+    through the GEMM in the step layout (a copy made per call here, at model
+    bind for a bound model): the same bf16 weights in the same K order as the
+    reference layout, so the outputs are bit-identical to those of matvec
+    path 3, which reads the reference layout."""
+    import guanaco_amd.hip as H
+    seed = 0x5E9 ^ (T << 16) ^ (N << 4) ^ K
+    w = orc.synth_quant(S.Q6_K, seed, N, K)
+    x = orc.synth_normal(seed + 1, T * K).reshape(T, K)
+    r = orc.synth_normal(seed + 2, T * N).reshape(T, N)
+    wd, xd = ctx.upload_weight(w), ctx.upload(x)
+    out = {}
+    for path in ("auto", "auto_q6k_ref"):
+        yd = ctx.upload(r) if mode == 1 else ctx.alloc(4 * T * N)
+        with H.matvec_path(path):
+            assert H.lib.gq_hip_prefill_gemm_dev(ctx.h, S.Q6_K, mode, wd, N, K, xd.ptr, T, yd.ptr,
+                                                 yd.ptr if mode == 1 else None) == 0
+        out[path] = yd.download(count=T * N)
+        yd.free()
+    assert np.abs(out["auto"]).sum() > 0
+    assert np.array_equal(bits(out["auto"]), bits(out["auto_q6k_ref"]))
+    H.lib.gq_hip_free(ctx.h, wd)
+    xd.free()
+
+
+def test_prefill_q6k_step_layout_model(orc):
+    """A model whose Q6_K projections (v, o, down) have K % 2048 == 0 prefills
+    from the step-layout copies made at model bind: logits and the last hidden
+    state bit-identical to the reference layout (matvec path 3), and the
+    prompt against the oracle as for the other models."""
+    import guanaco_amd.hip as H
+    from oracle import HostModel
+    spec = S.ModelSpec("q6k-steps-test", n_layers=2, hidden=2048, ff=4096, n_heads=16, n_kv_heads=4, vocab=1000,
+                       layer_dtypes=dict(wv=S.Q6_K, wo=S.Q6_K, wd=S.Q6_K))
+    c = H.Context(0)
+    try:
+        hm = HostModel(orc, spec, 64)
+        dm = H.DeviceModel(c, spec, 64)
+        toks = np.random.default_rng(7).integers(0, spec.vocab, 40).astype(np.int32)
+        res = {}
+        for path in ("auto", "auto_q6k_ref"):
+            with H.matvec_path(path):
+                res[path] = dm.prefill(toks, 0, want_hidden=True)
+        (nxt, lg, hg, _), (nxt2, lg2, hg2, _) = res["auto"], res["auto_q6k_ref"]
+        assert nxt == nxt2 and np.array_equal(bits(lg), bits(lg2)) and np.array_equal(bits(hg), bits(hg2))
+        kv = hm.new_kv()
+        for t in range(len(toks)):
+            t_cpu, lc, _ = hm.forward(kv, int(toks[t]), t)
+        assert rel_l2(lg, lc) < PF_TOL and nxt == t_cpu
+    finally:
+        c.close()
 
 
 def test_prefill_after_rebinding_larger_models(orc):
