@@ -315,17 +315,20 @@ typedef __bf16 gq_bf2a __attribute__((ext_vector_type(2)));
  *                 4 j + i), B = V rows; output tile d holds dims ND c + d,
  *                 so a lane reads ND consecutive floats of each V row and
  *                 holds ND consecutive output dims of rows 4 j + i.
- * Two waves per workgroup take alternate key blocks and combine their
- * (max, sum, O) through LDS at the end, so the longest causal rows finish in
- * half the time.  Same mathematics as the reference (engine.c:476-501:
+ * Four waves per workgroup take every fourth key block each and combine
+ * their (max, sum, O) through LDS at the end, so the longest causal rows
+ * finish in a quarter of the time.  One register buffer per wave: the next
+ * block's K loads once the scores have read K, its V once P V has read V,
+ * which keeps the kernel at 208 VGPRs, two waves per SIMD (two buffers
+ * needed 312, one wave per SIMD, and ran 1.25-1.4x slower).  Same mathematics as the reference (engine.c:476-501:
  * scores * 1/sqrt(hd), -inf past the query position, softmax, P V) in fp32
  * throughout; only the summation order differs. */
 template <int HD, int G>
-__global__ __launch_bounds__(128) void flash_prefill_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) void flash_prefill_kernel(AttnArgs a) {
   constexpr int TPT = 16 / G; /* tokens per tile */
   constexpr int NS = HD / 4;  /* QK^T MFMA steps */
   constexpr int ND = HD / 16; /* output tiles over the head dimension */
-  __shared__ float xm[64], xl[64], xo[ND * 4][64];
+  __shared__ float xm[3][64], xl[3][64], xo[3][ND * 4][64];
   const int lane = threadIdx.x & 63, c = lane & 15, j = lane >> 4;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   /* heavy (late) tiles first */
@@ -354,15 +357,17 @@ __global__ __launch_bounds__(128) void flash_prefill_kernel(AttnArgs a) {
   const int nblk = pmax / 16 + 1;
   /* K row key0 + c, dims NS j ..; V rows key0 + 4 j + i, dims ND c ..
    * (rows past pmax are never weighted: zeroed so stale cache contents
-   * cannot leak in as 0 * inf).  Block b + 1 loads while block b computes. */
+   * cannot leak in as 0 * inf). */
   float kv[NS], vv[4][ND];
-  auto load = [&](int key0, float (&kq)[NS], float (&vq)[4][ND]) {
+  auto loadk = [&](int key0, float (&kq)[NS]) {
     const float *kp = K + (size_t)min(key0 + c, a.max_seq - 1) * HD + NS * j;
 #pragma unroll
     for (int s4 = 0; s4 < NS / 4; s4++) {
       const float4 v = gld<float4>(kp + 4 * s4);
       kq[4 * s4] = v.x, kq[4 * s4 + 1] = v.y, kq[4 * s4 + 2] = v.z, kq[4 * s4 + 3] = v.w;
     }
+  };
+  auto loadv = [&](int key0, float (&vq)[4][ND]) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int key = key0 + 4 * j + i;
@@ -377,7 +382,7 @@ __global__ __launch_bounds__(128) void flash_prefill_kernel(AttnArgs a) {
   };
   /* one key block: S^T (four independent MFMA chains), mask, online
    * softmax, rescale, O += P V */
-  auto step = [&](int key0, const float (&kq)[NS], const float (&vq)[4][ND]) {
+  auto stepS = [&](int key0, const float (&kq)[NS], float (&p)[4]) {
     gq_f32x4 sp[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) sp[u] = gq_f32x4{0.f, 0.f, 0.f, 0.f};
@@ -396,7 +401,7 @@ __global__ __launch_bounds__(128) void flash_prefill_kernel(AttnArgs a) {
     const float mn = fmaxf(m, mb);
     const float ms = mn == -INFINITY ? 0.f : mn;
     const float alpha = __expf(m - ms);
-    float p[4], lb = 0.f;
+    float lb = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       p[i] = __expf(sv[i] - ms);
@@ -413,42 +418,45 @@ __global__ __launch_bounds__(128) void flash_prefill_kernel(AttnArgs a) {
 #pragma unroll
       for (int d = 0; d < ND; d++) o[d][i] *= al;
     }
+  };
+  auto stepPV = [&](const float (&p)[4], const float (&vq)[4][ND]) {
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
       for (int d = 0; d < ND; d++) o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[i], vq[i][d], o[d], 0, 0, 0);
   };
-  /* wave wv takes blocks wv, wv + 2, ...; two register buffers, the next
-   * block of the wave loading while the current one computes */
-  float k2[NS], v2[4][ND];
-  if (wv < nblk) load(16 * wv, kv, vv);
+  /* wave wv takes blocks wv, wv + 4, ...; the wave's next block loads into
+   * the registers as the current one frees them */
+  if (wv < nblk) loadk(16 * wv, kv), loadv(16 * wv, vv);
   for (int b = wv; b < nblk; b += 4) {
-    if (b + 2 < nblk) load(16 * (b + 2), k2, v2);
-    step(16 * b, kv, vv);
-    if (b + 2 >= nblk) break;
-    if (b + 4 < nblk) load(16 * (b + 4), kv, vv);
-    step(16 * (b + 2), k2, v2);
+    float p[4];
+    stepS(16 * b, kv, p);
+    if (b + 4 < nblk) loadk(16 * (b + 4), kv);
+    stepPV(p, vv);
+    if (b + 4 < nblk) loadv(16 * (b + 4), vv);
   }
-  /* combine: wave 1 hands (m, l, O) to wave 0 (wave 0 holds block 0, so its
-   * m is finite; wave 1's is -inf when it had no block and then weighs 0) */
-  if (wv == 1) {
-    xm[lane] = m, xl[lane] = l;
+  /* combine: waves 1-3 hand (m, l, O) to wave 0 (wave 0 holds block 0, so
+   * its m is finite; a wave that had no block has m = -inf and weighs 0) */
+  if (wv > 0) {
+    xm[wv - 1][lane] = m, xl[wv - 1][lane] = l;
 #pragma unroll
     for (int d = 0; d < ND; d++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) xo[4 * d + i][lane] = o[d][i];
+      for (int i = 0; i < 4; i++) xo[wv - 1][4 * d + i][lane] = o[d][i];
   }
   __syncthreads();
-  if (wv == 1) return;
-  {
-    const float m1 = xm[lane], mt = fmaxf(m, m1);
+  if (wv > 0) return;
+#pragma unroll
+  for (int w = 0; w < 3; w++) {
+    const float m1 = xm[w][lane], mt = fmaxf(m, m1);
     const float s0 = __expf(m - mt), s1 = __expf(m1 - mt);
-    l = l * s0 + xl[lane] * s1;
+    l = l * s0 + xl[w][lane] * s1;
+    m = mt;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const float a0 = __shfl(s0, 4 * j + i, 64), a1 = __shfl(s1, 4 * j + i, 64);
 #pragma unroll
-      for (int d = 0; d < ND; d++) o[d][i] = o[d][i] * a0 + xo[4 * d + i][lane] * a1;
+      for (int d = 0; d < ND; d++) o[d][i] = o[d][i] * a0 + xo[w][4 * d + i][lane] * a1;
     }
   }
   /* out[row] = O[row] / l[row]; row 4 j + i -> token t0 + row / G, head
@@ -478,7 +486,7 @@ __global__ __launch_bounds__(128) void flash_prefill_kernel(AttnArgs a) {
 
 template <int HD, int G>
 int launch_flash(const AttnArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL((flash_prefill_kernel<HD, G>), dim3((a.ntok + 16 / G - 1) / (16 / G), a.n_kv), dim3(128), 0, s,
+  hipLaunchKernelGGL((flash_prefill_kernel<HD, G>), dim3((a.ntok + 16 / G - 1) / (16 / G), a.n_kv), dim3(256), 0, s,
                      a);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
