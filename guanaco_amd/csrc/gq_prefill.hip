@@ -345,10 +345,13 @@ constexpr int stage_bytes() {
 
 /* Steps in the LDS ring: as deep as LDS (160 KB) and the 6-bit vmcnt allow
  * (each wave keeps (ring - 2) steps of DMA instructions in flight while it
- * waits), at least 3 (the pipeline reads two slots) */
+ * waits), at least 3 (the pipeline reads two slots).  The four-wave shape
+ * with 128-token tiles (KS 1, TT 4: 24 KB stages) takes 3 slots, 72 KB, so
+ * two workgroups share a CU (two waves per SIMD): gate/up at 512 tokens ran
+ * 265 -> 200 us against 4 slots and one workgroup per CU. */
 template <int DT, int KS, int TT>
 constexpr int ring() {
-  return std::min(4, (160 * 1024) / stage_bytes<DT, KS, TT>());
+  return std::min(KS == 1 && TT == 4 ? 3 : 4, (160 * 1024) / stage_bytes<DT, KS, TT>());
 }
 template <int DT, int KS, int TT>
 constexpr int ring_bytes() {
