@@ -106,6 +106,7 @@ def _gemm_case(ctx, orc, dtype, T, N, K, mode):
     (S.Q4_K, 14336, 4096, 0),   # gate / up
     (S.Q4_K, 4096, 14336, 1),   # down + residual
     (S.Q6_K, 4096, 14336, 1),   # the Q6_K down of the Q4_K_M mix
+    (S.Q6_K, 14336, 4096, 0),   # Q6_K gate / up: 128-token tiles from the step layout
 ])
 def test_prefill_gemm_config5_shapes(ctx, orc, dtype, N, K, mode):
     """Config 5's full 512-token GEMMs on the 8B projection shapes; every
