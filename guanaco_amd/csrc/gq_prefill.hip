@@ -45,6 +45,8 @@ typedef float gq_f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kPThreads = 256;
 constexpr int kBN = 128, kBK = 64;
+/* K parts of a launch split over the grid (PgArgs.part) */
+constexpr int kKParts = kPgKParts;
 /* TT 32-token MFMA tiles per wave (the token tile is 32 TT); X bytes per
  * step of one K-split */
 template <int TT>
@@ -378,7 +380,9 @@ __device__ __forceinline__ void tile_loop(const PgArgs &a, const uint8_t *w, uin
   constexpr int kRing = ring<DT, KS, TT>();
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kh = wave >> 2, rw = wave & 3;
-  const int ns = a.K / kBK / KS, s0 = kh * ns; /* this split's steps: s0 .. s0 + ns - 1 */
+  /* this wave's steps s0 .. s0 + ns - 1: K part blockIdx.z of a.kparts,
+   * then split kh of KS within the workgroup */
+  const int nsp = a.K / kBK / a.kparts, ns = nsp / KS, s0 = (int)blockIdx.z * nsp + kh * ns;
   typename PW<DT>::Plan pl;
   PW<DT>::plan(pl, lane, rowbytes);
   const uint32_t sbase = (uint32_t)(uintptr_t)smem;
@@ -544,6 +548,10 @@ __global__ __launch_bounds__(kPThreads * KS) void pgemm_kernel(PgArgs a) {
           const int t = t0 + tile_token(i, e, lane);
           if (t < a.T) {
             float v = acc[i][e];
+            if (a.kparts > 1) { /* this K part's sums, added up by pg_parts_kernel */
+              gst<float>(a.part + ((size_t)blockIdx.z * a.T + t) * S.rows + n, v);
+              continue;
+            }
             float *y = S.y + (size_t)t * S.rows + n;
             if (MODE == MV_RESID) v = gld<float>(y) + v;
             gst<float>(y, v);
@@ -578,6 +586,22 @@ __global__ __launch_bounds__(kPThreads * KS) void pgemm_kernel(PgArgs a) {
   }
 }
 
+/* y = (y +) ((part 0 + part 1) + ...) elementwise, n4 float4s per part */
+__global__ void pg_parts_kernel(float *y, const float *part, size_t n4, int kparts, int resid) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n4) return;
+  float4 s = gld<float4>(part + 4 * i);
+  for (int k = 1; k < kparts; k++) {
+    const float4 u = gld<float4>(part + ((size_t)k * n4 + i) * 4);
+    s.x += u.x, s.y += u.y, s.z += u.z, s.w += u.w;
+  }
+  if (resid) {
+    const float4 r = gld<float4>(y + 4 * i);
+    s = make_float4(r.x + s.x, r.y + s.y, r.z + s.z, r.w + s.w);
+  }
+  gst<float4>(y + 4 * i, s);
+}
+
 __global__ void to_bf16_kernel(const float *x, __bf16 *y, size_t n) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) y[i] = (__bf16)x[i];
@@ -586,9 +610,11 @@ __global__ void to_bf16_kernel(const float *x, __bf16 *y, size_t n) {
 /* Launch shape: token tiles of 128 (TT = 4: each dequantized weight feeds
  * four MFMAs) for launches whose grid still gives every CU a workgroup
  * (gate/up at 512 tokens) and whose weights are Q4_K or Q6_K in the step
- * layout (Q6_K 14336 x 4096 at 512 tokens: 160 -> 95 us), else of 64; then 2 K-splits when the
- * grid has at most one workgroup per CU (a second wave per SIMD comes from
- * the split), 1 when it has more. */
+ * layout (Q6_K 14336 x 4096 at 512 tokens: 160 -> 95 us).  One-segment
+ * launches with fewer such tiles than CUs split K over the grid instead
+ * (PgArgs.part).  Otherwise tiles of 64, with 2 K-splits inside the
+ * workgroup when the grid has at most one workgroup per CU (a second wave
+ * per SIMD comes from the split), 1 when it has more. */
 int n_cus() {
   static const int cus = [] {
     int dev = 0, n = 0;
@@ -607,17 +633,44 @@ int launch_shape(const PgArgs &a, int row_tiles, size_t lds, hipStream_t s) {
                               160 * 1024);
     attr_done = true;
   }
-  hipLaunchKernelGGL((pgemm_kernel<MODE, KS, TT>), dim3(row_tiles, (a.T + 32 * TT - 1) / (32 * TT)),
+  hipLaunchKernelGGL((pgemm_kernel<MODE, KS, TT>), dim3(row_tiles, (a.T + 32 * TT - 1) / (32 * TT), a.kparts),
                      dim3(kPThreads * KS), lds, s, a);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
 template <int MODE>
-int launch_mode(const PgArgs &a, int row_tiles, hipStream_t s) {
+int launch_mode(const PgArgs &a0, int row_tiles, hipStream_t s) {
+  PgArgs a = a0;
+  a.kparts = 1;
   bool q4 = false, q6 = false, q6p = false;
   for (int i = 0; i < a.nseg; i++)
     q4 |= a.seg[i].dtype == GQ_Q4_K, q6 |= a.seg[i].dtype == GQ_Q6_K, q6p |= a.seg[i].dtype == GQ_Q6_KP;
-  const int tt = !q6 && row_tiles * ((a.T + 127) / 128) >= n_cus() ? 4 : 2;
+  const int tiles4 = row_tiles * ((a.T + 127) / 128);
+  if (MODE != MV_SWIGLU && a.nseg == 1 && a.part && tiles4 < n_cus() && (a.K / kBK) % kKParts == 0 &&
+      (size_t)kKParts * a.T * a.seg[0].rows <= a.part_cap && (size_t)a.T * a.seg[0].rows % 4 == 0) {
+    /* too few 128-token tiles to give every CU work: K in kKParts parts
+     * over the grid (four-wave workgroups, two per CU), then their sum.  At
+     * 512 tokens: down 120 -> 91 us (Q4_K) and 145 -> 101 us (Q6_K step
+     * layout), k/v 33 -> 25 us, the o projection in the model forward
+     * ~8 us faster, whole forward 15.1 -> 13.6 ms.  Q6_K in the reference
+     * layout keeps 64-token tiles (its stages are larger); the tile width
+     * does not change the order of any sum, so both layouts still agree
+     * bit for bit. */
+    a.kparts = kKParts;
+    int rc;
+    if (q6) {
+      rc = launch_shape<MODE, 1, 2>(a, row_tiles, std::max(ring_bytes<GQ_Q6_K, 1, 2>(), ring_bytes<GQ_Q4_K, 1, 2>()), s);
+    } else {
+      const size_t lds = std::max(q6p ? ring_bytes<GQ_Q6_KP, 1, 4>() : 0, ring_bytes<GQ_Q4_K, 1, 4>());
+      rc = launch_shape<MODE, 1, 4>(a, row_tiles, lds, s);
+    }
+    if (rc) return rc;
+    const size_t n4 = (size_t)a.T * a.seg[0].rows / 4;
+    hipLaunchKernelGGL(pg_parts_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, a.seg[0].y, a.part, n4,
+                       kKParts, MODE == MV_RESID ? 1 : 0);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+  }
+  const int tt = !q6 && tiles4 >= n_cus() ? 4 : 2;
   const int wgs = row_tiles * ((a.T + 32 * tt - 1) / (32 * tt));
   int ks = wgs <= n_cus() ? 2 : 1;
   if ((a.K / kBK) % 2) ks = 1;

@@ -46,6 +46,8 @@ struct PrefillWs {
   __bf16 *xb = nullptr; /* op-level entry: bf16 copy of its fp32 x */
   int *tok = nullptr;
   size_t xb_cap = 0;
+  float *part = nullptr; /* the GEMM's K-part sums (PgArgs.part) */
+  size_t part_cap = 0;
 };
 
 /* tokens per prefill chunk */
@@ -1268,6 +1270,13 @@ static int pf_attention(gq_ctx *c, int layer, int pos, int T, int n_heads, float
 /* one layer over the chunk (engine.c:352-554 with T tokens): 7 launches of
  * the GEMM (q/k/v together, gate/up together with SwiGLU), RMSNorms writing
  * bf16, RoPE + append + attention writing bf16 */
+/* the K-part workspace for a one-segment launch of rows x T */
+static void pf_parts(gq_ctx *c, PgArgs &a) {
+  PrefillWs &w = c->pf;
+  const size_t n = (size_t)kPgKParts * a.T * a.seg[0].rows;
+  if (pf_ensure(c, w.part, w.part_cap, n) == 0) a.part = w.part, a.part_cap = w.part_cap;
+}
+
 static int pf_layer(gq_ctx *c, int l, int pos, int T) {
   const gq_model &m = c->m;
   const gq_layer &L = c->layers[l];
@@ -1282,6 +1291,7 @@ static int pf_layer(gq_ctx *c, int l, int pos, int T) {
   gu.x = w.xn, gu.K = m.hidden, gu.nseg = 2, gu.act = w.act;
   gu.seg[0] = pg_seg(c, l, 4, L.w_gate, nullptr), gu.seg[1] = pg_seg(c, l, 5, L.w_up, nullptr);
   dn.x = w.act, dn.K = m.ff, dn.nseg = 1, dn.seg[0] = pg_seg(c, l, 6, L.w_down, w.x);
+  pf_parts(c, o), pf_parts(c, dn);
   if ((rc = gq_launch_rmsnorm_rows(w.x, L.rms_att, nullptr, m.hidden, T, m.rms_eps, c->stream, w.xn)) ||
       (rc = gq_launch_pgemm(MV_STORE, qkv, c->stream)) ||
       (rc = pf_attention(c, l, pos, T, m.n_heads, w.q, w.k, w.v, nullptr, w.att)) ||
@@ -1719,6 +1729,7 @@ extern "C" int gq_hip_prefill_gemm_dev(gq_ctx *c, int dtype, int mode, const voi
   if (!(a.x = pf_x16(c, x, (size_t)t * k))) return fail(c, -4, "prefill GEMM: x conversion");
   const uint8_t *ps = op_steps(c, dtype, w, n, k);
   a.T = t, a.K = k, a.nseg = 1, a.seg[0] = op_seg(ps, w, y, n, dtype);
+  pf_parts(c, a);
   if (mode == 1 && r != y)
     HIPCHK(c, hipMemcpyAsync(y, r, sizeof(float) * (size_t)t * n, hipMemcpyDeviceToDevice, c->stream));
   const int rc = gq_launch_pgemm(mode == 1 ? MV_RESID : MV_STORE, a, c->stream);
@@ -1735,6 +1746,7 @@ extern "C" float gq_hip_time_prefill_gemm(gq_ctx *c, int dtype, const void *w, i
   if (!(a.x = pf_x16(c, x, (size_t)t * k))) return fail(c, -4, "time GEMM: x conversion"), -1.f;
   const uint8_t *ps = op_steps(c, dtype, w, n, k);
   a.T = t, a.K = k, a.nseg = 1, a.seg[0] = op_seg(ps, w, y, n, dtype);
+  pf_parts(c, a);
   hipEvent_t e0 = nullptr, e1 = nullptr;
   int rc = hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess ? 0 : -4;
   if (!rc) rc = gq_launch_pgemm(MV_STORE, a, c->stream); /* untimed first launch */
