@@ -257,16 +257,18 @@ struct PgArgs {
   __bf16 *act;
   PgSeg seg[3];
   int nseg, T, K;
-  /* optional workspace of part_cap floats: a one-segment STORE or RESID
-   * launch whose grid is too small for 128-token tiles then splits K over
-   * workgroups, each part writing its sums there, and a second kernel adds
-   * the parts (and the residual) in a fixed order */
+  /* optional workspace of part_cap floats: a STORE or RESID launch whose
+   * grid is too small for 128-token tiles then splits K over workgroups,
+   * each part writing its sums there (T x all segments' rows per part), and
+   * a second kernel adds the parts (and the residual) in a fixed order and
+   * scatters them to the segments' outputs */
   float *part;
   size_t part_cap;
-  int kparts; /* set by the launcher */
+  int kparts, rows_total; /* set by the launcher */
 };
 int gq_launch_pgemm(int mode, const PgArgs &a, hipStream_t s);
-/* K parts of a split launch: PgArgs.part needs kPgKParts * T * rows floats */
+/* at most this many K parts in a split launch: PgArgs.part needs
+ * kPgKParts * T * (all segments' rows) floats */
 constexpr int kPgKParts = 4;
 /* Q6_K weights (rows x cols, cols a multiple of 2048) re-laid out for the
  * prefill GEMM: each 64-weight step's quant bytes together, then the scales

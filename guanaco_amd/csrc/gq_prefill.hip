@@ -494,9 +494,9 @@ __global__ __launch_bounds__(kPThreads * KS) void pgemm_kernel(PgArgs a) {
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kh = wave >> 2, rw = wave & 3;
   const int t0 = blockIdx.y * 32 * TT;
-  int sg = 0, tb = blockIdx.x;
+  int sg = 0, tb = blockIdx.x, roff = 0; /* roff: the segment's first row among all segments' */
   if (MODE != MV_SWIGLU)
-    while (sg + 1 < a.nseg && tb >= a.seg[sg].rows / kBN) tb -= a.seg[sg].rows / kBN, sg++;
+    while (sg + 1 < a.nseg && tb >= a.seg[sg].rows / kBN) tb -= a.seg[sg].rows / kBN, roff += a.seg[sg].rows, sg++;
   /* this wave's weights: rows r0 .. r0 + 31 of segment ws */
   int ws = sg, r0 = tb * kBN + 32 * rw;
   if (MODE == MV_SWIGLU) ws = rw >> 1, r0 = tb * (kBN / 2) + 32 * (rw & 1);
@@ -549,7 +549,7 @@ __global__ __launch_bounds__(kPThreads * KS) void pgemm_kernel(PgArgs a) {
           if (t < a.T) {
             float v = acc[i][e];
             if (a.kparts > 1) { /* this K part's sums, added up by pg_parts_kernel */
-              gst<float>(a.part + ((size_t)blockIdx.z * a.T + t) * S.rows + n, v);
+              gst<float>(a.part + ((size_t)blockIdx.z * a.T + t) * a.rows_total + roff + n, v);
               continue;
             }
             float *y = S.y + (size_t)t * S.rows + n;
@@ -586,20 +586,32 @@ __global__ __launch_bounds__(kPThreads * KS) void pgemm_kernel(PgArgs a) {
   }
 }
 
-/* y = (y +) ((part 0 + part 1) + ...) elementwise, n4 float4s per part */
-__global__ void pg_parts_kernel(float *y, const float *part, size_t n4, int kparts, int resid) {
+/* y = (y +) ((part 0 + part 1) + ...) elementwise over T x rows_total
+ * (n4 float4s per part), scattered back to the segments' outputs */
+__global__ void pg_parts_kernel(PgArgs a, size_t n4, int resid) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n4) return;
-  float4 s = gld<float4>(part + 4 * i);
-  for (int k = 1; k < kparts; k++) {
-    const float4 u = gld<float4>(part + ((size_t)k * n4 + i) * 4);
+  const size_t e = 4 * i;
+  const int t = (int)(e / (size_t)a.rows_total);
+  int r = (int)(e - (size_t)t * a.rows_total);
+  const int n0 = a.seg[0].rows, n1 = a.seg[1].rows;
+  float *yb = a.seg[0].y;
+  int rows = n0;
+  if (a.nseg > 1 && r >= n0) {
+    r -= n0, yb = a.seg[1].y, rows = n1;
+    if (a.nseg > 2 && r >= n1) r -= n1, yb = a.seg[2].y, rows = a.seg[2].rows;
+  }
+  float *y = yb + (size_t)t * rows + r;
+  float4 s = gld<float4>(a.part + e);
+  for (int k = 1; k < a.kparts; k++) {
+    const float4 u = gld<float4>(a.part + (size_t)k * 4 * n4 + e);
     s.x += u.x, s.y += u.y, s.z += u.z, s.w += u.w;
   }
   if (resid) {
-    const float4 r = gld<float4>(y + 4 * i);
-    s = make_float4(r.x + s.x, r.y + s.y, r.z + s.z, r.w + s.w);
+    const float4 q = gld<float4>(y);
+    s = make_float4(q.x + s.x, q.y + s.y, q.z + s.z, q.w + s.w);
   }
-  gst<float4>(y + 4 * i, s);
+  gst<float4>(y, s);
 }
 
 __global__ void to_bf16_kernel(const float *x, __bf16 *y, size_t n) {
@@ -646,17 +658,23 @@ int launch_mode(const PgArgs &a0, int row_tiles, hipStream_t s) {
   for (int i = 0; i < a.nseg; i++)
     q4 |= a.seg[i].dtype == GQ_Q4_K, q6 |= a.seg[i].dtype == GQ_Q6_K, q6p |= a.seg[i].dtype == GQ_Q6_KP;
   const int tiles4 = row_tiles * ((a.T + 127) / 128);
-  if (MODE != MV_SWIGLU && a.nseg == 1 && a.part && tiles4 < n_cus() && (a.K / kBK) % kKParts == 0 &&
-      (size_t)kKParts * a.T * a.seg[0].rows <= a.part_cap && (size_t)a.T * a.seg[0].rows % 4 == 0) {
-    /* too few 128-token tiles to give every CU work: K in kKParts parts
-     * over the grid (four-wave workgroups, two per CU), then their sum.  At
-     * 512 tokens: down 120 -> 91 us (Q4_K) and 145 -> 101 us (Q6_K step
-     * layout), k/v 33 -> 25 us, the o projection in the model forward
-     * ~8 us faster, whole forward 15.1 -> 13.6 ms.  Q6_K in the reference
+  a.rows_total = 0;
+  for (int i = 0; i < a.nseg; i++) a.rows_total += a.seg[i].rows;
+  /* as few parts as give 1.5 workgroups per CU: 2 for the fused q/k/v
+   * launch at 512 tokens (forward 13.83 -> 13.62 ms against 4 parts'
+   * 13.95), 4 for o, down and k/v alone */
+  const int KP = 2 * tiles4 * 2 >= 3 * n_cus() ? 2 : kKParts;
+  if (MODE != MV_SWIGLU && a.part && tiles4 < n_cus() && (a.K / kBK) % KP == 0 &&
+      (size_t)KP * a.T * a.rows_total <= a.part_cap) {
+    /* too few 128-token tiles to give every CU work: K in KP parts over
+     * the grid (four-wave workgroups), then their sum.  At 512 tokens: down
+     * 120 -> 91 us (Q4_K) and 145 -> 101 us (Q6_K step layout), k/v
+     * 33 -> 25 us, the o projection in the model forward ~4 us faster,
+     * whole forward 15.1 -> 13.6 ms.  Q6_K in the reference
      * layout keeps 64-token tiles (its stages are larger); the tile width
      * does not change the order of any sum, so both layouts still agree
      * bit for bit. */
-    a.kparts = kKParts;
+    a.kparts = KP;
     int rc;
     if (q6) {
       rc = launch_shape<MODE, 1, 2>(a, row_tiles, std::max(ring_bytes<GQ_Q6_K, 1, 2>(), ring_bytes<GQ_Q4_K, 1, 2>()), s);
@@ -665,9 +683,9 @@ int launch_mode(const PgArgs &a0, int row_tiles, hipStream_t s) {
       rc = launch_shape<MODE, 1, 4>(a, row_tiles, lds, s);
     }
     if (rc) return rc;
-    const size_t n4 = (size_t)a.T * a.seg[0].rows / 4;
-    hipLaunchKernelGGL(pg_parts_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, a.seg[0].y, a.part, n4,
-                       kKParts, MODE == MV_RESID ? 1 : 0);
+    const size_t n4 = (size_t)a.T * a.rows_total / 4;
+    hipLaunchKernelGGL(pg_parts_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, a, n4,
+                       MODE == MV_RESID ? 1 : 0);
     return hipGetLastError() == hipSuccess ? 0 : -4;
   }
   const int tt = !q6 && tiles4 >= n_cus() ? 4 : 2;

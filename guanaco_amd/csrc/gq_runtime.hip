@@ -1270,10 +1270,12 @@ static int pf_attention(gq_ctx *c, int layer, int pos, int T, int n_heads, float
 /* one layer over the chunk (engine.c:352-554 with T tokens): 7 launches of
  * the GEMM (q/k/v together, gate/up together with SwiGLU), RMSNorms writing
  * bf16, RoPE + append + attention writing bf16 */
-/* the K-part workspace for a one-segment launch of rows x T */
+/* the K-part workspace for a launch of T x (its segments' rows) */
 static void pf_parts(gq_ctx *c, PgArgs &a) {
   PrefillWs &w = c->pf;
-  const size_t n = (size_t)kPgKParts * a.T * a.seg[0].rows;
+  size_t rows = 0;
+  for (int i = 0; i < a.nseg; i++) rows += a.seg[i].rows;
+  const size_t n = (size_t)kPgKParts * a.T * rows;
   if (pf_ensure(c, w.part, w.part_cap, n) == 0) a.part = w.part, a.part_cap = w.part_cap;
 }
 
@@ -1291,7 +1293,7 @@ static int pf_layer(gq_ctx *c, int l, int pos, int T) {
   gu.x = w.xn, gu.K = m.hidden, gu.nseg = 2, gu.act = w.act;
   gu.seg[0] = pg_seg(c, l, 4, L.w_gate, nullptr), gu.seg[1] = pg_seg(c, l, 5, L.w_up, nullptr);
   dn.x = w.act, dn.K = m.ff, dn.nseg = 1, dn.seg[0] = pg_seg(c, l, 6, L.w_down, w.x);
-  pf_parts(c, o), pf_parts(c, dn);
+  pf_parts(c, qkv), pf_parts(c, o), pf_parts(c, dn);
   if ((rc = gq_launch_rmsnorm_rows(w.x, L.rms_att, nullptr, m.hidden, T, m.rms_eps, c->stream, w.xn)) ||
       (rc = gq_launch_pgemm(MV_STORE, qkv, c->stream)) ||
       (rc = pf_attention(c, l, pos, T, m.n_heads, w.q, w.k, w.v, nullptr, w.att)) ||
