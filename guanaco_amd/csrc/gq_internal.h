@@ -265,6 +265,10 @@ struct PgArgs {
   float *part;
   size_t part_cap;
   int kparts, rows_total; /* set by the launcher */
+  /* a one-segment RESID launch with kparts_out set leaves the parts' sum
+   * (and the residual add) to its caller when it splits, writing the number
+   * of parts there (1: not split, y is final) */
+  int *kparts_out;
 };
 int gq_launch_pgemm(int mode, const PgArgs &a, hipStream_t s);
 /* at most this many K parts in a split launch: PgArgs.part needs
@@ -278,9 +282,13 @@ size_t gq_q6k_steps_bytes(int rows, int cols);
 int gq_launch_q6k_steps(void *dst, const void *src, int rows, int cols, hipStream_t s);
 int gq_launch_to_bf16(const float *x, __bf16 *y, size_t n, hipStream_t s);
 /* RMSNorm of `rows` consecutive rows of dim floats, one workgroup per row;
- * out16 != NULL writes bf16 there instead of fp32 to out */
+ * out16 != NULL writes bf16 there instead of fp32 to out.  parts != NULL
+ * (kparts of rows x dim each, a K-split GEMM's sums left to this launch by
+ * PgArgs.kparts_out): each row is first x plus the sum of its parts, which
+ * is also stored to xnew (may be x). */
 int gq_launch_rmsnorm_rows(const float *x, const float *w, float *out, int dim, int rows, float eps,
-                           hipStream_t s, __bf16 *out16 = nullptr);
+                           hipStream_t s, __bf16 *out16 = nullptr, const float *parts = nullptr, int kparts = 0,
+                           float *xnew = nullptr);
 /* embedding rows of tokens[0..n) (device array) into out (n x hidden) */
 int gq_launch_embed_rows(int dtype, const void *table, int hidden, const int *tokens_dev, int n, float *out,
                          hipStream_t s);

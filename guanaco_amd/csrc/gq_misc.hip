@@ -20,15 +20,21 @@ constexpr int kThreads = 256;
  * aligned; other shapes take the scalar two-pass loop. */
 constexpr int kNormVec = 16;
 
+/* parts != NULL: the row is first x + ((part 0 + part 1) + ...), the sum of
+ * a K-split GEMM's parts added to the residual as pg_parts_kernel does
+ * (part p of the row at parts + p * pstride), and is stored to xnew */
 __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *x, const float *w, float *out,
-                                                          int dim, float eps, __bf16 *out16) {
+                                                          int dim, float eps, __bf16 *out16, const float *parts,
+                                                          int kparts, size_t pstride, float *xnew) {
   __shared__ float red[kThreads / GQ_WAVE];
   const int tid = threadIdx.x;
   x += (size_t)blockIdx.x * dim;
   out += (size_t)blockIdx.x * dim;
   if (out16) out16 += (size_t)blockIdx.x * dim;
+  if (parts) parts += (size_t)blockIdx.x * dim, xnew += (size_t)blockIdx.x * dim;
   const bool vec = (dim & 3) == 0 && dim <= kNormVec * 4 * kThreads && (((uintptr_t)x | (uintptr_t)out) & 15) == 0 &&
-                   (!w || ((uintptr_t)w & 15) == 0) && (!out16 || ((uintptr_t)out16 & 7) == 0);
+                   (!w || ((uintptr_t)w & 15) == 0) && (!out16 || ((uintptr_t)out16 & 7) == 0) &&
+                   (!parts || (((uintptr_t)parts | (uintptr_t)xnew | pstride) & 3) == 0);
   float4 xv[kNormVec];
   float ss = 0.f;
   if (vec) {
@@ -37,12 +43,31 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *x, const
       const int e = 4 * (tid + k * kThreads);
       if (e < dim) {
         xv[k] = gld<float4>(x + e);
+        if (parts) {
+          float4 s = gld<float4>(parts + e);
+          for (int p = 1; p < kparts; p++) {
+            const float4 u = gld<float4>(parts + p * pstride + e);
+            s.x += u.x, s.y += u.y, s.z += u.z, s.w += u.w;
+          }
+          xv[k] = make_float4(xv[k].x + s.x, xv[k].y + s.y, xv[k].z + s.z, xv[k].w + s.w);
+          gst<float4>(xnew + e, xv[k]);
+        }
         ss = __builtin_fmaf(xv[k].x, xv[k].x, ss), ss = __builtin_fmaf(xv[k].y, xv[k].y, ss);
         ss = __builtin_fmaf(xv[k].z, xv[k].z, ss), ss = __builtin_fmaf(xv[k].w, xv[k].w, ss);
       }
     }
   } else {
-    for (int i = tid; i < dim; i += kThreads) ss = __builtin_fmaf(x[i], x[i], ss);
+    for (int i = tid; i < dim; i += kThreads) {
+      float xi = x[i];
+      if (parts) {
+        float s = parts[i];
+        for (int p = 1; p < kparts; p++) s += parts[p * pstride + i];
+        xi = xi + s;
+        xnew[i] = xi;
+      }
+      ss = __builtin_fmaf(xi, xi, ss);
+    }
+    if (parts) x = xnew; /* this thread's own elements, read back below */
   }
   ss = gq_wave_sum(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
@@ -234,9 +259,10 @@ int gq_launch_rmsnorm(const float *x, const float *w, float *out, int dim, float
 }
 
 int gq_launch_rmsnorm_rows(const float *x, const float *w, float *out, int dim, int rows, float eps,
-                           hipStream_t s, __bf16 *out16) {
-  if (rows <= 0 || dim <= 0) return -1;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, s, x, w, out, dim, eps, out16);
+                           hipStream_t s, __bf16 *out16, const float *parts, int kparts, float *xnew) {
+  if (rows <= 0 || dim <= 0 || (parts && (kparts < 1 || !xnew))) return -1;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, s, x, w, out, dim, eps, out16,
+                     parts, kparts, (size_t)rows * dim, xnew);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 

@@ -654,6 +654,7 @@ template <int MODE>
 int launch_mode(const PgArgs &a0, int row_tiles, hipStream_t s) {
   PgArgs a = a0;
   a.kparts = 1;
+  if (a.kparts_out) *a.kparts_out = 1;
   bool q4 = false, q6 = false, q6p = false;
   for (int i = 0; i < a.nseg; i++)
     q4 |= a.seg[i].dtype == GQ_Q4_K, q6 |= a.seg[i].dtype == GQ_Q6_K, q6p |= a.seg[i].dtype == GQ_Q6_KP;
@@ -683,6 +684,10 @@ int launch_mode(const PgArgs &a0, int row_tiles, hipStream_t s) {
       rc = launch_shape<MODE, 1, 4>(a, row_tiles, lds, s);
     }
     if (rc) return rc;
+    if (MODE == MV_RESID && a.nseg == 1 && a.kparts_out) { /* the caller sums the parts */
+      *a.kparts_out = KP;
+      return 0;
+    }
     const size_t n4 = (size_t)a.T * a.rows_total / 4;
     hipLaunchKernelGGL(pg_parts_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, a, n4,
                        MODE == MV_RESID ? 1 : 0);

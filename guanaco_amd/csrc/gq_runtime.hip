@@ -1279,7 +1279,11 @@ static void pf_parts(gq_ctx *c, PgArgs &a) {
   if (pf_ensure(c, w.part, w.part_cap, n) == 0) a.part = w.part, a.part_cap = w.part_cap;
 }
 
-static int pf_layer(gq_ctx *c, int l, int pos, int T) {
+/* pending: K parts of the previous layer's down launch still to be added
+ * into the residual x (1: none); this layer's first RMSNorm adds them, and
+ * this layer leaves its own down's parts the same way unless it is the
+ * last */
+static int pf_layer(gq_ctx *c, int l, int pos, int T, int &pending) {
   const gq_model &m = c->m;
   const gq_layer &L = c->layers[l];
   PrefillWs &w = c->pf;
@@ -1294,13 +1298,21 @@ static int pf_layer(gq_ctx *c, int l, int pos, int T) {
   gu.seg[0] = pg_seg(c, l, 4, L.w_gate, nullptr), gu.seg[1] = pg_seg(c, l, 5, L.w_up, nullptr);
   dn.x = w.act, dn.K = m.ff, dn.nseg = 1, dn.seg[0] = pg_seg(c, l, 6, L.w_down, w.x);
   pf_parts(c, qkv), pf_parts(c, o), pf_parts(c, dn);
-  if ((rc = gq_launch_rmsnorm_rows(w.x, L.rms_att, nullptr, m.hidden, T, m.rms_eps, c->stream, w.xn)) ||
-      (rc = gq_launch_pgemm(MV_STORE, qkv, c->stream)) ||
+  /* the o and down launches leave their K parts' sum to the next RMSNorm
+   * (the last layer's down sums its own: the LM head reads x) */
+  int ko = 1, kd = 1;
+  o.kparts_out = &ko;
+  if (l + 1 < m.n_layers) dn.kparts_out = &kd;
+  auto norm = [&](const float *nw, int k) {
+    return gq_launch_rmsnorm_rows(w.x, nw, nullptr, m.hidden, T, m.rms_eps, c->stream, w.xn,
+                                  k > 1 ? w.part : nullptr, k, w.x);
+  };
+  if ((rc = norm(L.rms_att, pending)) || (rc = gq_launch_pgemm(MV_STORE, qkv, c->stream)) ||
       (rc = pf_attention(c, l, pos, T, m.n_heads, w.q, w.k, w.v, nullptr, w.att)) ||
-      (rc = gq_launch_pgemm(MV_RESID, o, c->stream)) ||
-      (rc = gq_launch_rmsnorm_rows(w.x, L.rms_ffn, nullptr, m.hidden, T, m.rms_eps, c->stream, w.xn)) ||
+      (rc = gq_launch_pgemm(MV_RESID, o, c->stream)) || (rc = norm(L.rms_ffn, ko)) ||
       (rc = gq_launch_pgemm(MV_SWIGLU, gu, c->stream)) || (rc = gq_launch_pgemm(MV_RESID, dn, c->stream)))
     return rc;
+  pending = kd;
   return 0;
 }
 
@@ -1332,8 +1344,9 @@ extern "C" int gq_hip_prefill(gq_ctx *c, const int32_t *tokens, int n_tokens, in
       HIPCHK(c, hipMemcpyAsync(w.tok, tokens + t0, sizeof(int) * T, hipMemcpyHostToDevice, c->stream));
       if ((rc = gq_launch_embed_rows(m.embed.dtype, m.embed.data, m.hidden, w.tok, T, w.x, c->stream)))
         return fail(c, rc, "prefill: embed");
+      int pending = 1;
       for (int l = 0; l < m.n_layers; l++)
-        if ((rc = pf_layer(c, l, pos + t0, T))) return fail(c, rc, "prefill: layer %d launch failed", l);
+        if ((rc = pf_layer(c, l, pos + t0, T, pending))) return fail(c, rc, "prefill: layer %d launch failed", l);
     }
     /* last token: final RMSNorm + LM head + argmax as in a decode step */
     HIPCHK(c, hipMemcpyAsync(ws.hidden, w.x + (size_t)(T - 1) * m.hidden, sizeof(float) * m.hidden,
