@@ -48,13 +48,28 @@ __global__ __launch_bounds__(kThreads) void rope_append_kernel(RopeArgs a) {
   float *q = a.q + (size_t)tz * a.q_stride;
   const float *kin = a.k + (size_t)tz * a.k_stride, *vin = a.v + (size_t)tz * a.v_stride;
   const int nq = a.n_heads * half, nk = a.n_kv * half;
+  /* element o of this token's q | k | v from the GEMM's parts, summed in
+   * pg_parts_kernel's order */
+  const int qd = a.n_heads * a.hd, kvd = a.n_kv * a.hd;
+  auto part = [&](int o) {
+    const float *r = a.parts + (size_t)tz * a.prow + o;
+    float v = r[0];
+    for (int k = 1; k < a.kparts; k++) v += r[(size_t)k * a.pstride];
+    return v;
+  };
   for (int t = threadIdx.x; t < nq + nk; t += kThreads) {
     const bool isq = t < nq;
     const int u = isq ? t : t - nq;
     const int h = u / half, i = u - h * half;
     const float2 c = cs[i];
-    const float *src = isq ? q + (size_t)h * a.hd : kin + (size_t)h * a.hd;
-    const float x0 = src[2 * i], x1 = src[2 * i + 1];
+    float x0, x1;
+    if (a.parts) {
+      const int o = (isq ? 0 : qd) + h * a.hd + 2 * i;
+      x0 = part(o), x1 = part(o + 1);
+    } else {
+      const float *src = isq ? q + (size_t)h * a.hd : kin + (size_t)h * a.hd;
+      x0 = src[2 * i], x1 = src[2 * i + 1];
+    }
     const float y0 = x0 * c.x - x1 * c.y;
     const float y1 = x0 * c.y + x1 * c.x;
     if (isq) {
@@ -66,9 +81,9 @@ __global__ __launch_bounds__(kThreads) void rope_append_kernel(RopeArgs a) {
       dst[2 * i + 1] = y1;
     }
   }
-  for (int t = threadIdx.x; t < a.n_kv * a.hd; t += kThreads) {
+  for (int t = threadIdx.x; t < kvd; t += kThreads) {
     const int h = t / a.hd, d = t - h * a.hd;
-    a.vc[((size_t)h * a.max_seq + p) * a.hd + d] = vin[t];
+    a.vc[((size_t)h * a.max_seq + p) * a.hd + d] = a.parts ? part(qd + kvd + t) : vin[t];
   }
 }
 
@@ -508,7 +523,7 @@ int gq_launch_flash_prefill(const AttnArgs &a, hipStream_t s) {
 }
 
 int gq_launch_rope_append(const RopeArgs &a, hipStream_t s) {
-  if ((a.hd & 1) || a.n_kv <= 0 || a.ntok < 0) return -1;
+  if ((a.hd & 1) || a.n_kv <= 0 || a.ntok < 0 || (a.parts && a.kparts < 1)) return -1;
   hipLaunchKernelGGL(rope_append_kernel, dim3(std::max(a.ntok, 1)), dim3(kThreads), 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }

@@ -207,6 +207,12 @@ struct RopeArgs {
   /* ntok tokens at pos .. pos + ntok - 1 (0 or 1: one); per-token strides in
    * floats of q, k, v */
   int ntok, q_stride, k_stride, v_stride;
+  /* parts != NULL: q, k and v of token t are the sums of a K-split GEMM's
+   * kparts parts (PgArgs.kparts_out), q | k | v of token t at parts +
+   * t * prow, part p at + p * pstride; the rotated q still goes to q */
+  const float *parts;
+  int kparts, prow;
+  size_t pstride;
 };
 int gq_launch_rope_append(const RopeArgs &a, hipStream_t s);
 
@@ -265,9 +271,9 @@ struct PgArgs {
   float *part;
   size_t part_cap;
   int kparts, rows_total; /* set by the launcher */
-  /* a one-segment RESID launch with kparts_out set leaves the parts' sum
-   * (and the residual add) to its caller when it splits, writing the number
-   * of parts there (1: not split, y is final) */
+  /* a launch with kparts_out set leaves the parts' sum (and for RESID the
+   * residual add) to its caller when it splits, writing the number of parts
+   * there (1: not split, y is final) */
   int *kparts_out;
 };
 int gq_launch_pgemm(int mode, const PgArgs &a, hipStream_t s);

@@ -684,7 +684,7 @@ int launch_mode(const PgArgs &a0, int row_tiles, hipStream_t s) {
       rc = launch_shape<MODE, 1, 4>(a, row_tiles, lds, s);
     }
     if (rc) return rc;
-    if (MODE == MV_RESID && a.nseg == 1 && a.kparts_out) { /* the caller sums the parts */
+    if (a.kparts_out) { /* the caller sums the parts */
       *a.kparts_out = KP;
       return 0;
     }

@@ -1253,10 +1253,12 @@ static PgSeg pg_seg(const gq_ctx *c, int l, int i, const gq_weight &w, float *y)
  * k/v: T x n_kv*hd), then causal attention of the T tokens into out (fp32)
  * or out16 (bf16), T x n_heads*hd */
 static int pf_attention(gq_ctx *c, int layer, int pos, int T, int n_heads, float *q, const float *k, const float *v,
-                        float *out, __bf16 *out16) {
+                        float *out, __bf16 *out16, int kparts = 1) {
   const int hd = c->kv_hd, kvd = c->kv_heads * hd, qd = n_heads * hd;
   RopeArgs ra{q, k, v, gq_hip_kv_k(c, layer), gq_hip_kv_v(c, layer), c->rope, nullptr, pos,
               n_heads, c->kv_heads, hd, c->kv_max_seq, T, qd, kvd, kvd};
+  if (kparts > 1) /* q, k, v are still the q/k/v GEMM's K parts */
+    ra.parts = c->pf.part, ra.kparts = kparts, ra.prow = qd + 2 * kvd, ra.pstride = (size_t)T * (qd + 2 * kvd);
   int rc = gq_launch_rope_append(ra, c->stream);
   if (rc) return rc;
   AttnArgs aa{};
@@ -1298,9 +1300,11 @@ static int pf_layer(gq_ctx *c, int l, int pos, int T, int &pending) {
   gu.seg[0] = pg_seg(c, l, 4, L.w_gate, nullptr), gu.seg[1] = pg_seg(c, l, 5, L.w_up, nullptr);
   dn.x = w.act, dn.K = m.ff, dn.nseg = 1, dn.seg[0] = pg_seg(c, l, 6, L.w_down, w.x);
   pf_parts(c, qkv), pf_parts(c, o), pf_parts(c, dn);
-  /* the o and down launches leave their K parts' sum to the next RMSNorm
-   * (the last layer's down sums its own: the LM head reads x) */
-  int ko = 1, kd = 1;
+  /* the q/k/v launch leaves its K parts' sum to the RoPE + append kernel,
+   * o and down theirs to the next RMSNorm (the last layer's down sums its
+   * own: the LM head reads x) */
+  int kq = 1, ko = 1, kd = 1;
+  qkv.kparts_out = &kq;
   o.kparts_out = &ko;
   if (l + 1 < m.n_layers) dn.kparts_out = &kd;
   auto norm = [&](const float *nw, int k) {
@@ -1308,7 +1312,7 @@ static int pf_layer(gq_ctx *c, int l, int pos, int T, int &pending) {
                                   k > 1 ? w.part : nullptr, k, w.x);
   };
   if ((rc = norm(L.rms_att, pending)) || (rc = gq_launch_pgemm(MV_STORE, qkv, c->stream)) ||
-      (rc = pf_attention(c, l, pos, T, m.n_heads, w.q, w.k, w.v, nullptr, w.att)) ||
+      (rc = pf_attention(c, l, pos, T, m.n_heads, w.q, w.k, w.v, nullptr, w.att, kq)) ||
       (rc = gq_launch_pgemm(MV_RESID, o, c->stream)) || (rc = norm(L.rms_ffn, ko)) ||
       (rc = gq_launch_pgemm(MV_SWIGLU, gu, c->stream)) || (rc = gq_launch_pgemm(MV_RESID, dn, c->stream)))
     return rc;
