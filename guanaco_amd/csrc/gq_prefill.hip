@@ -548,7 +548,7 @@ __global__ __launch_bounds__(kPThreads * KS) void pgemm_kernel(PgArgs a) {
           const int t = t0 + tile_token(i, e, lane);
           if (t < a.T) {
             float v = acc[i][e];
-            if (a.kparts > 1) { /* this K part's sums, added up by pg_parts_kernel */
+            if (a.kparts > 1) { /* this K part's sums, added up by pg_parts_kernel or the caller */
               gst<float>(a.part + ((size_t)blockIdx.z * a.T + t) * a.rows_total + roff + n, v);
               continue;
             }
@@ -622,9 +622,9 @@ __global__ void to_bf16_kernel(const float *x, __bf16 *y, size_t n) {
 /* Launch shape: token tiles of 128 (TT = 4: each dequantized weight feeds
  * four MFMAs) for launches whose grid still gives every CU a workgroup
  * (gate/up at 512 tokens) and whose weights are Q4_K or Q6_K in the step
- * layout (Q6_K 14336 x 4096 at 512 tokens: 160 -> 95 us).  One-segment
- * launches with fewer such tiles than CUs split K over the grid instead
- * (PgArgs.part).  Otherwise tiles of 64, with 2 K-splits inside the
+ * layout (Q6_K 14336 x 4096 at 512 tokens: 160 -> 95 us).  Other STORE
+ * and RESID launches with fewer such tiles than CUs split K over the grid
+ * instead (PgArgs.part).  Otherwise tiles of 64, with 2 K-splits inside the
  * workgroup when the grid has at most one workgroup per CU (a second wave
  * per SIMD comes from the split), 1 when it has more. */
 int n_cus() {
@@ -671,10 +671,10 @@ int launch_mode(const PgArgs &a0, int row_tiles, hipStream_t s) {
      * the grid (four-wave workgroups), then their sum.  At 512 tokens: down
      * 120 -> 91 us (Q4_K) and 145 -> 101 us (Q6_K step layout), k/v
      * 33 -> 25 us, the o projection in the model forward ~4 us faster,
-     * whole forward 15.1 -> 13.6 ms.  Q6_K in the reference
-     * layout keeps 64-token tiles (its stages are larger); the tile width
-     * does not change the order of any sum, so both layouts still agree
-     * bit for bit. */
+     * whole forward 15.1 -> 13.6 ms.  Q6_K in the reference layout keeps
+     * 64-token tiles (its stages are larger); the tile width does not
+     * change the order of any sum, so both layouts still agree bit for
+     * bit. */
     a.kparts = KP;
     int rc;
     if (q6) {
