@@ -473,6 +473,12 @@ __device__ __forceinline__ void mvx_body(const MvArgs &a, const MxPlan &p, int b
           xh[i] = make_float4(xh[i].x * wh[i].x, xh[i].y * wh[i].y, xh[i].z * wh[i].z, xh[i].w * wh[i].w);
         }
       }
+      /* every wave's x requests ahead of any wave's weight requests: a
+       * CU's memory pipeline serves its waves' requests in about the order
+       * they were issued, and without this barrier a late wave's x queued
+       * behind the early waves' rows (down: x in at 1.2-5.8 us, so most
+       * rows' arithmetic waited for x; q/k/v 9.1 -> 8.9 us) */
+      if (!MT) __builtin_amdgcn_s_barrier();
       typename T::Raw raw[R];
       if (act) {
 #pragma unroll
