@@ -51,10 +51,27 @@ __global__ __launch_bounds__(kThreads) void rope_append_kernel(RopeArgs a) {
   /* element o of this token's q | k | v from the GEMM's parts, summed in
    * pg_parts_kernel's order */
   const int qd = a.n_heads * a.hd, kvd = a.n_kv * a.hd;
-  auto part = [&](int o) {
-    const float *r = a.parts + (size_t)tz * a.prow + o;
-    float v = r[0];
-    for (int k = 1; k < a.kparts; k++) v += r[(size_t)k * a.pstride];
+  const float *prow = a.parts ? a.parts + (size_t)tz * a.prow : nullptr;
+  /* element pairs (2i, 2i + 1) move as one 8-byte access when every address
+   * of this token allows it (always, from the runtime's own buffers: hd and
+   * the strides are even); op-level callers' 4-byte-aligned buffers take
+   * two scalar accesses.  The values and their order are the same. */
+  const bool v2 = ((uintptr_t)q & 7) == 0 && (((uintptr_t)a.kc | (uintptr_t)a.vc) & 7) == 0 &&
+                  (prow ? ((uintptr_t)prow & 7) == 0 && (a.pstride & 1) == 0
+                        : (((uintptr_t)kin | (uintptr_t)vin) & 7) == 0);
+  auto ld2 = [&](const float *s) {
+    return v2 ? gld<float2>(s) : make_float2(s[0], s[1]);
+  };
+  auto st2 = [&](float *d, float2 y) {
+    if (v2) gst<float2>(d, y);
+    else d[0] = y.x, d[1] = y.y;
+  };
+  auto part2 = [&](int o) {
+    float2 v = ld2(prow + o);
+    for (int k = 1; k < a.kparts; k++) {
+      const float2 u = ld2(prow + (size_t)k * a.pstride + o);
+      v.x += u.x, v.y += u.y;
+    }
     return v;
   };
   for (int t = threadIdx.x; t < nq + nk; t += kThreads) {
@@ -62,28 +79,14 @@ __global__ __launch_bounds__(kThreads) void rope_append_kernel(RopeArgs a) {
     const int u = isq ? t : t - nq;
     const int h = u / half, i = u - h * half;
     const float2 c = cs[i];
-    float x0, x1;
-    if (a.parts) {
-      const int o = (isq ? 0 : qd) + h * a.hd + 2 * i;
-      x0 = part(o), x1 = part(o + 1);
-    } else {
-      const float *src = isq ? q + (size_t)h * a.hd : kin + (size_t)h * a.hd;
-      x0 = src[2 * i], x1 = src[2 * i + 1];
-    }
-    const float y0 = x0 * c.x - x1 * c.y;
-    const float y1 = x0 * c.y + x1 * c.x;
-    if (isq) {
-      q[(size_t)h * a.hd + 2 * i] = y0;
-      q[(size_t)h * a.hd + 2 * i + 1] = y1;
-    } else {
-      float *dst = a.kc + ((size_t)h * a.max_seq + p) * a.hd;
-      dst[2 * i] = y0;
-      dst[2 * i + 1] = y1;
-    }
+    const float2 x = prow ? part2((isq ? 0 : qd) + h * a.hd + 2 * i)
+                          : ld2((isq ? (const float *)q : kin) + (size_t)h * a.hd + 2 * i);
+    const float2 y = make_float2(x.x * c.x - x.y * c.y, x.x * c.y + x.y * c.x);
+    st2(isq ? q + (size_t)h * a.hd + 2 * i : a.kc + ((size_t)h * a.max_seq + p) * a.hd + 2 * i, y);
   }
-  for (int t = threadIdx.x; t < kvd; t += kThreads) {
+  for (int t = 2 * threadIdx.x; t < kvd; t += 2 * kThreads) {
     const int h = t / a.hd, d = t - h * a.hd;
-    a.vc[((size_t)h * a.max_seq + p) * a.hd + d] = a.parts ? part(qd + kvd + t) : vin[t];
+    st2(a.vc + ((size_t)h * a.max_seq + p) * a.hd + d, prow ? part2(qd + kvd + t) : ld2(vin + t));
   }
 }
 

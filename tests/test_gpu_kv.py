@@ -109,23 +109,27 @@ def test_lctx_rejects_mismatch(ctx, tmp_path):
     # TinyLlama's rope theta (config 2) at its shape, and at the 8B shape
     (32, 4, 64, 639, 10000.0), (32, 4, 64, 2047, 10000.0), (32, 8, 128, 4095, 10000.0),
 ])
-def test_rope_append_bitexact(ctx, orc, nh, nkv, hd, pos, theta):
+@pytest.mark.parametrize("off", [0, 1])
+def test_rope_append_bitexact(ctx, orc, nh, nkv, hd, pos, theta, off):
     """Fused RoPE + append: rotated q and the cached K row equal the
     reference's rope() + kv_cache_append bit for bit (table from the same fp32
-    expressions, no contraction)."""
+    expressions, no contraction).  off = 1 passes q, k and v one float past
+    an 8-byte boundary: the kernel's scalar path for such buffers."""
     ms = pos + 1
     ctx.kv_init(1, nkv, hd, ms, theta)
     rng = np.random.default_rng(pos)
     q = rng.standard_normal(nh * hd).astype(np.float32) * np.float32(30)
     k = rng.standard_normal(nkv * hd).astype(np.float32) * np.float32(30)
     v = rng.standard_normal(nkv * hd).astype(np.float32)
-    qb, kb, vb = ctx.upload(q), ctx.upload(k), ctx.upload(v)
-    assert ctx.rope_append_dev(0, pos, nh, qb, kb, vb) == 0
+    pad = np.zeros(off, np.float32)
+    qb, kb, vb = (ctx.upload(np.concatenate([pad, a])) for a in (q, k, v))
+    at = [type("At", (), {"ptr": b.ptr + 4 * off})() for b in (qb, kb, vb)]
+    assert ctx.rope_append_dev(0, pos, nh, *at) == 0
     q2, k2 = orc.rope(q, k, nh, nkv, hd, pos, theta)
-    assert np.array_equal(bits(qb.download()), bits(q2))
+    assert np.array_equal(bits(qb.download()[off:]), bits(q2))
     dk, dv = ctx.kv_read_layer(0)
     dk = dk.reshape(nkv, ms, hd)
     dv = dv.reshape(nkv, ms, hd)
     assert np.array_equal(bits(dk[:, pos]), bits(k2.reshape(nkv, hd)))
     assert np.array_equal(bits(dv[:, pos]), bits(v.reshape(nkv, hd)))
-    assert ctx.rope_append_dev(0, ms, nh, qb, kb, vb) == -5
+    assert ctx.rope_append_dev(0, ms, nh, *at) == -5
