@@ -224,8 +224,11 @@ int gq_launch_embed(int dtype, const void *table, int hidden, const int *token_d
 /* argmax of x[n] (ties -> lowest index) -> *out_index; when step_dev != NULL
  * also stores the index at tokens[*step_dev], then ++*step_dev and
  * ++*pos_dev (the decode-loop bookkeeping of one graph replay). */
+/* emb_out != NULL: the winner's embedding row (emb_dtype, emb_table,
+ * hidden) is also written to emb_out, by the same launch */
 int gq_launch_argmax(const float *x, int n, float *scratch, int nblk, int *out_index,
-                     int *tokens, int *step_dev, int *pos_dev, hipStream_t s);
+                     int *tokens, int *step_dev, int *pos_dev, hipStream_t s, int emb_dtype = 0,
+                     const void *emb_table = nullptr, int hidden = 0, float *emb_out = nullptr);
 int gq_argmax_blocks(int n);
 
 /* On-device sampling (gq_sample.hip).  top-k handles k <= kMaxTopK. */

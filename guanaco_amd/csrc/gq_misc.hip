@@ -107,43 +107,43 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *x, const
   }
 }
 
-/* Embedding row of `token` (engine.c:214-283): F32 copy, Q8_0 q*scale,
- * Q4_K (d*sc)*q - dmin*m with separate roundings.  With tokens != NULL,
- * row blockIdx.y holds tokens[blockIdx.y] (out + blockIdx.y * hidden);
- * blockIdx.x covers 256-element slices of the row. */
+/* Element e of embedding row `tok` (engine.c:214-283): F32 copy, Q8_0
+ * q*scale, Q4_K (d*sc)*q - dmin*m with separate roundings. */
+__device__ __forceinline__ float embed_value(int dtype, const uint8_t *table, int hidden, int tok, int e) {
+#pragma clang fp contract(off)
+  if (dtype == GQ_F32) return ((const float *)table)[(size_t)tok * hidden + e];
+  if (dtype == GQ_Q8_0) {
+    const uint8_t *blk = table + ((size_t)tok * (hidden / 32) + e / 32) * 34;
+    return (float)(int8_t)blk[2 + (e & 31)] * gq_h2f(blk[0] | (blk[1] << 8));
+  }
+  const uint8_t *blk = table + ((size_t)tok * (hidden / 256) + e / 256) * 144;
+  const int u = e & 255, cc = u >> 6, o = u & 63;
+  const int j = 2 * cc + (o >= 32);
+  const uint8_t *s = blk + 4;
+  int sc, m;
+  if (j < 4) {
+    sc = s[j] & 63, m = s[j + 4] & 63;
+  } else {
+    sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
+    m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+  }
+  const uint8_t qb = blk[16 + 32 * cc + (o & 31)];
+  const int q = o < 32 ? (qb & 15) : (qb >> 4);
+  const float d = gq_h2f(blk[0] | (blk[1] << 8)), dm = gq_h2f(blk[2] | (blk[3] << 8));
+  const float d1 = d * (float)sc, m1 = dm * (float)m;
+  return d1 * (float)q - m1;
+}
+
+/* Embedding row of `token`.  With tokens != NULL, row blockIdx.y holds
+ * tokens[blockIdx.y] (out + blockIdx.y * hidden); blockIdx.x covers
+ * 256-element slices of the row. */
 __global__ __launch_bounds__(kThreads) void embed_kernel(int dtype, const uint8_t *table, int hidden,
                                                         const int *token_dev, int token, const int *tokens,
                                                         float *out) {
-#pragma clang fp contract(off)
   const int tok = tokens ? tokens[blockIdx.y] : token_dev ? *token_dev : token;
   out += (size_t)blockIdx.y * hidden;
-  for (int e = blockIdx.x * kThreads + threadIdx.x; e < hidden; e += gridDim.x * kThreads) {
-    float v;
-    if (dtype == GQ_F32) {
-      v = ((const float *)table)[(size_t)tok * hidden + e];
-    } else if (dtype == GQ_Q8_0) {
-      const uint8_t *blk = table + ((size_t)tok * (hidden / 32) + e / 32) * 34;
-      v = (float)(int8_t)blk[2 + (e & 31)] * gq_h2f(blk[0] | (blk[1] << 8));
-    } else {
-      const uint8_t *blk = table + ((size_t)tok * (hidden / 256) + e / 256) * 144;
-      const int u = e & 255, cc = u >> 6, o = u & 63;
-      const int j = 2 * cc + (o >= 32);
-      const uint8_t *s = blk + 4;
-      int sc, m;
-      if (j < 4) {
-        sc = s[j] & 63, m = s[j + 4] & 63;
-      } else {
-        sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
-        m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
-      }
-      const uint8_t qb = blk[16 + 32 * cc + (o & 31)];
-      const int q = o < 32 ? (qb & 15) : (qb >> 4);
-      const float d = gq_h2f(blk[0] | (blk[1] << 8)), dm = gq_h2f(blk[2] | (blk[3] << 8));
-      const float d1 = d * (float)sc, m1 = dm * (float)m;
-      v = d1 * (float)q - m1;
-    }
-    out[e] = v;
-  }
+  for (int e = blockIdx.x * kThreads + threadIdx.x; e < hidden; e += gridDim.x * kThreads)
+    out[e] = embed_value(dtype, table, hidden, tok, e);
 }
 
 /* (value, index) reduction, ties to the lower index (tokenizer.c:175-185). */
@@ -182,15 +182,22 @@ __global__ __launch_bounds__(kThreads) void argmax_stage1(const float *x, int n,
   }
 }
 
+/* The winner of stage 1's block results.  With eout != NULL it also writes
+ * the winner's embedding row (the next decode step's input) to eout: each
+ * workgroup of the grid reduces the same block results to the same winner
+ * and writes its 256-element slices of the row, and workgroup 0 alone
+ * writes the token, the step and the position (one launch fewer than a
+ * separate embedding after the argmax). */
 __global__ __launch_bounds__(kThreads) void argmax_stage2(const float *scratch, int nblk, int *out,
-                                                         int *tokens, int *step_dev, int *pos_dev) {
+                                                         int *tokens, int *step_dev, int *pos_dev, int edt,
+                                                         const uint8_t *etab, int hidden, float *eout) {
   float v = -INFINITY;
   int i = 0x7fffffff;
   for (int b = threadIdx.x; b < nblk; b += kThreads)
     better(v, i, scratch[2 * b], __float_as_int(scratch[2 * b + 1]));
   block_argmax(v, i);
-  if (threadIdx.x == 0) {
-    if (i == 0x7fffffff) i = 0; /* all NaN: the reference keeps index 0 */
+  if (i == 0x7fffffff) i = 0; /* all NaN: the reference keeps index 0 */
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
     *out = i;
     if (step_dev) {
       tokens[*step_dev] = i;
@@ -198,6 +205,9 @@ __global__ __launch_bounds__(kThreads) void argmax_stage2(const float *scratch, 
       *pos_dev += 1;
     }
   }
+  if (eout)
+    for (int e = blockIdx.x * kThreads + threadIdx.x; e < hidden; e += gridDim.x * kThreads)
+      eout[e] = embed_value(edt, etab, hidden, i, e);
 }
 
 __global__ void silu_mul_kernel(float *gate, const float *up, int n) {
@@ -285,11 +295,16 @@ int gq_launch_embed_rows(int dtype, const void *table, int hidden, const int *to
 int gq_argmax_blocks(int n) { return (n + kArgmaxPerBlock - 1) / kArgmaxPerBlock; }
 
 int gq_launch_argmax(const float *x, int n, float *scratch, int nblk, int *out_index, int *tokens,
-                     int *step_dev, int *pos_dev, hipStream_t s) {
+                     int *step_dev, int *pos_dev, hipStream_t s, int emb_dtype, const void *emb_table, int hidden,
+                     float *emb_out) {
   if (n <= 0 || nblk != gq_argmax_blocks(n)) return -1;
+  if (emb_out && ((emb_dtype != GQ_F32 && emb_dtype != GQ_Q8_0 && emb_dtype != GQ_Q4_K) || !emb_table ||
+                  hidden <= 0))
+    return -1;
   hipLaunchKernelGGL(argmax_stage1, dim3(nblk), dim3(kThreads), 0, s, x, n, scratch);
-  hipLaunchKernelGGL(argmax_stage2, dim3(1), dim3(kThreads), 0, s, scratch, nblk, out_index, tokens,
-                     step_dev, pos_dev);
+  hipLaunchKernelGGL(argmax_stage2, dim3(emb_out ? (hidden + kThreads - 1) / kThreads : 1), dim3(kThreads), 0, s,
+                     scratch, nblk, out_index, tokens, step_dev, pos_dev, emb_dtype, (const uint8_t *)emb_table,
+                     hidden, emb_out);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 

@@ -1038,16 +1038,20 @@ static int run_layer(gq_ctx *c, int l, int pos, const int *pos_dev, float *hidde
 }
 
 /* embedding -> layers -> final RMSNorm + LM head -> argmax.  Eager form
- * (token/pos host values) or graph form (device token/pos/step). */
+ * (token/pos host values) or graph form (device token/pos/step).  The graph
+ * form starts from the embedding already in w.hidden and leaves the next
+ * token's there: its argmax launch writes it, and gq_hip_decode_loop embeds
+ * the first token before the first step. */
 static int run_step(gq_ctx *c, int token, int pos, bool device_state, float *hidden_per_layer) {
   const gq_model &m = c->m;
   Workspace &w = c->ws;
   int rc;
-  const int *tok_dev = device_state ? w.d_token : nullptr;
   const int *pos_dev = device_state ? w.d_pos : nullptr;
-  if ((rc = gq_launch_embed(m.embed.dtype, m.embed.data, m.hidden, tok_dev, token, w.hidden, c->stream)))
-    return rc;
-  mark(c, PC_OTHER, 4.0 * m.hidden);
+  if (!device_state) {
+    if ((rc = gq_launch_embed(m.embed.dtype, m.embed.data, m.hidden, nullptr, token, w.hidden, c->stream)))
+      return rc;
+    mark(c, PC_OTHER, 4.0 * m.hidden);
+  }
   for (int l = 0; l < m.n_layers; l++) {
     if ((rc = run_layer(c, l, pos, pos_dev, w.hidden))) return rc;
     if (hidden_per_layer)
@@ -1057,7 +1061,8 @@ static int run_step(gq_ctx *c, int token, int pos, bool device_state, float *hid
   if ((rc = op_lm_head(c, w.hidden))) return rc;
   if ((rc = gq_launch_argmax(w.logits, m.vocab, w.amax, w.amax_blocks, w.d_token,
                              device_state ? w.d_tokens : nullptr, device_state ? w.d_step : nullptr,
-                             device_state ? w.d_pos : nullptr, c->stream)))
+                             device_state ? w.d_pos : nullptr, c->stream, m.embed.dtype, m.embed.data, m.hidden,
+                             device_state ? w.hidden : nullptr)))
     return rc;
   mark(c, PC_OTHER, 4.0 * m.vocab);
   return 0;
@@ -1158,6 +1163,9 @@ extern "C" int gq_hip_decode_loop(gq_ctx *c, int token, int pos, int n_steps, in
   HIPCHK(c, hipEventCreate(&e0));
   HIPCHK(c, hipEventCreate(&e1));
   HIPCHK(c, hipEventRecord(e0, c->stream));
+  /* the first step's input; each step's argmax embeds the next token */
+  if ((rc = gq_launch_embed(c->m.embed.dtype, c->m.embed.data, c->m.hidden, w.d_token, token, w.hidden, c->stream)))
+    return fail(c, rc, "embed launch failed");
   for (int i = 0; i < n_steps; i++) {
     if (use_graph) {
       HIPCHK(c, hipGraphLaunch(c->gexec, c->stream));
