@@ -8,8 +8,10 @@
  * rope_append: one workgroup rotates every Q head and the new K row with the
  * (cos, sin) table row of `pos` (precomputed on the host with the reference's
  * fp32 expressions, kernels_cpu.c:409-413; rotation products and differences
- * rounded separately, :415-429) and writes K and V at pos % max_seq
- * (kv_cache.c:101-125).  Appended rows are bit copies of the reference's.
+ * rounded separately, :415-429) and writes K and V at row pos of the slab
+ * (kv_cache.c:101-125 with pos < max_seq; the device cache does not wrap,
+ * the host rejects pos >= max_seq with -5 and the kernel returns for such a
+ * position).  Appended rows are bit copies of the reference's.
  *
  * attention: flash-decoding split over the sequence.  Workgroup (g, c)
  * streams chunk c of KV head g once for all G = n_heads/n_kv query heads

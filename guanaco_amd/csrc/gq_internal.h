@@ -236,8 +236,8 @@ constexpr int kMaxTopK = 1024;
 struct SampleWs {
   float *keys = nullptr;           /* sorted logits (top-p) or probabilities (temperature) */
   int *ids_in = nullptr, *ids = nullptr;
-  void *cub = nullptr;             /* radix-sort temporary storage */
-  size_t cub_bytes = 0;
+  void *sort_tmp = nullptr;        /* radix-sort temporary storage */
+  size_t sort_bytes = 0;
   int cap = 0;                     /* vocabulary the buffers hold */
 };
 /* radix-sort temporary bytes for a vocabulary */

@@ -174,7 +174,15 @@ __global__ __launch_bounds__(kThreads) void argmax_stage1(const float *x, int n,
   const int end = min(n, base + kArgmaxPerBlock);
   float v = -INFINITY;
   int i = 0x7fffffff;
-  for (int e = base + threadIdx.x; e < end; e += kThreads) better(v, i, x[e], e);
+  for (int e = base + threadIdx.x; e < end; e += kThreads) {
+    float xe = x[e];
+    /* sample_greedy starts from logits[0] and only a strictly greater value
+     * replaces it, so a NaN there is never replaced: index 0 wins.  As +inf
+     * it does, since ties go to the lowest index.  A NaN elsewhere never
+     * compares greater and is skipped, as better() skips it. */
+    if (e == 0 && xe != xe) xe = INFINITY;
+    better(v, i, xe, e);
+  }
   block_argmax(v, i);
   if (threadIdx.x == 0) {
     scratch[2 * blockIdx.x] = v;
@@ -235,9 +243,10 @@ __global__ void synth_quant_kernel(uint8_t *out, int dtype, size_t nbytes, int b
     const size_t i = i4 + k;
     const uint64_t b = i / (size_t)bb;
     const uint32_t o = (uint32_t)(i - b * bb);
-    const uint8_t v = dtype == GQ_Q4_K ? gq_q4k_byte(seed, b, o)
-                      : dtype == GQ_Q6_K ? gq_q6k_byte(seed, b, o)
-                                         : gq_q8_0_byte(seed, b, o);
+    const uint8_t v = dtype == GQ_Q4_K                             ? gq_q4k_byte(seed, b, o)
+                      : dtype == (GQ_Q4_K | GQ_SYNTH_Q4K_ZERO_MEAN) ? gq_q4k_zm_byte(seed, b, o)
+                      : dtype == GQ_Q6_K                             ? gq_q6k_byte(seed, b, o)
+                                                                     : gq_q8_0_byte(seed, b, o);
     word |= (uint32_t)v << (8 * k);
   }
   if (i4 + 4 <= nbytes) {
@@ -325,7 +334,7 @@ int gq_launch_copy(void *dst, const void *src, size_t bytes, int n_cu, hipStream
 
 int gq_launch_synth_quant(void *dev, int dtype, int rows, int cols, uint64_t seed, hipStream_t s) {
   int qk, bb;
-  if (dtype == GQ_Q4_K) qk = 256, bb = 144;
+  if (dtype == GQ_Q4_K || dtype == (GQ_Q4_K | GQ_SYNTH_Q4K_ZERO_MEAN)) qk = 256, bb = 144;
   else if (dtype == GQ_Q6_K) qk = 256, bb = 210;
   else if (dtype == GQ_Q8_0) qk = 32, bb = 34;
   else return -1;

@@ -31,7 +31,7 @@
  * The arithmetic is the reference's formula refactored so each weight costs
  * one convert and one FMA: Q4_K d*sc*sum(q*x) - dmin*m*sum(x) with nibbles
  * converted two at a time by v_cvt_pk_f32_fp8 (gq_nib2f, exact), Q6_K
- * d*sc*(sum(q*x) - 32*sum(x)), Q8_0 d*(sum((q+128)*x) - 128*sum(x)).  Row
+ * d*sc*(sum(q*x) - 32*sum(x)), Q8_0 d*sum(q*x) with q sign-extended.  Row
  * sums reduce by DPP over 8- or 16-lane segments, then in LDS, in a fixed
  * order: outputs are deterministic.
  */
@@ -228,20 +228,22 @@ struct Ux<GQ_Q8_0> {
   /* sh: the block's byte phase (0 or 2); its quants start 2 bytes later */
   static __device__ __forceinline__ float dot(const Raw &r, int, const float4 (&xl)[4], const float4 (&xh)[4],
                                               float sxl, float sxh, uint32_t sh) {
+    (void)sxl, (void)sxh;
     const uint32_t qsh = (sh + 2u) & 3u;
     const uint32_t w[9] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w, r.t};
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      /* int8 q + 128 as an unsigned byte */
-      const uint32_t q = __builtin_amdgcn_alignbyte(w[i + 1], w[i], qsh) ^ 0x80808080u;
+      /* the int8 quants sign-extended, so the sum is of q*x itself, as the
+       * reference's (quant_matvec_q8_0.c:60-75): no large offset to cancel */
+      const uint32_t q = __builtin_amdgcn_alignbyte(w[i + 1], w[i], qsh);
       const float4 &x = i < 4 ? xl[i] : xh[i - 4];
-      s = __builtin_fmaf((float)(q & 0xffu), x.x, s);
-      s = __builtin_fmaf((float)((q >> 8) & 0xffu), x.y, s);
-      s = __builtin_fmaf((float)((q >> 16) & 0xffu), x.z, s);
-      s = __builtin_fmaf((float)(q >> 24), x.w, s);
+      s = __builtin_fmaf((float)(int8_t)q, x.x, s);
+      s = __builtin_fmaf((float)(int8_t)(q >> 8), x.y, s);
+      s = __builtin_fmaf((float)(int8_t)(q >> 16), x.z, s);
+      s = __builtin_fmaf((float)(int8_t)(q >> 24), x.w, s);
     }
-    return gq_h2f(r.d) * __builtin_fmaf(-128.f, sxl + sxh, s);
+    return gq_h2f(r.d) * s;
   }
 };
 

@@ -70,10 +70,17 @@ struct gq_ctx {
   float theta = 0.f;
   float *kslab = nullptr, *vslab = nullptr;
   float2 *rope = nullptr;
-  /* model */
-  bool bound = false;
+  /* model: `bound` once gq_hip_model_bind succeeded; layer_on[l] for the
+   * layers it holds (the rest stay on the host); `whole` when every layer,
+   * the embedding and the LM head are on the device, which the whole-model
+   * entry points need */
+  bool bound = false, whole = false;
   gq_model m{};
   std::vector<gq_layer> layers;
+  std::vector<char> layer_on;
+  /* prompts through gq_hip_prefill: 0 the matrix-core GEMM in chunks, 1 token
+   * by token through the fp32 decode step (gq_hip_set_prefill_mode) */
+  int prefill_mode = 0;
   /* tile-interleaved copies of the bound model's gate+up pairs and LM head
    * for the matrix-core matvec (gq_launch_mm_tile), owned by the context;
    * NULL where a weight does not take that layout */
@@ -97,6 +104,11 @@ struct gq_ctx {
   /* graph */
   hipGraph_t graph = nullptr;
   hipGraphExec_t gexec = nullptr;
+  /* the device state a graph replay left behind (graph_step): w.hidden holds
+   * the embedding of g_token, to be decoded at g_pos */
+  bool g_valid = false;
+  int g_token = -1, g_pos = -1;
+  int *st_pinned = nullptr; /* pinned (token, pos, step) for graph_step */
   /* measurement hooks for eager steps */
   bool prof = false;
   std::vector<hipEvent_t> ev;
@@ -121,6 +133,24 @@ static int fail(gq_ctx *c, int code, const char *fmt, ...) {
     hipError_t e_ = (call);                                                                     \
     if (e_ != hipSuccess) return fail((c), -4, "%s: %s", #call, hipGetErrorString(e_));         \
   } while (0)
+
+/* A start/stop pair of timing events, destroyed on every exit path. */
+struct EventPair {
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  hipError_t create() {
+    const hipError_t e = hipEventCreate(&e0);
+    return e != hipSuccess ? e : hipEventCreate(&e1);
+  }
+  float ms() const {
+    float t = 0.f;
+    (void)hipEventElapsedTime(&t, e0, e1);
+    return t;
+  }
+  ~EventPair() {
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+  }
+};
 
 static size_t block_bytes(int dtype, int *qk) {
   switch (dtype) {
@@ -195,6 +225,7 @@ static void free_graph(gq_ctx *c) {
   if (c->graph) (void)hipGraphDestroy(c->graph);
   c->gexec = nullptr;
   c->graph = nullptr;
+  c->g_valid = false;
 }
 
 extern "C" void gq_hip_destroy(gq_ctx *c) {
@@ -202,6 +233,7 @@ extern "C" void gq_hip_destroy(gq_ctx *c) {
   (void)hipSetDevice(c->dev);
   (void)hipStreamSynchronize(c->stream);
   free_graph(c);
+  if (c->st_pinned) (void)hipHostFree(c->st_pinned);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
   for (void *p : c->allocs) (void)hipFree(p);
   for (int i = 0; i < 2; i++) {
@@ -463,7 +495,7 @@ static void kv_release(gq_ctx *c) {
   c->kslab = c->vslab = nullptr;
   c->rope = nullptr;
   c->kv_layers = c->kv_heads = c->kv_hd = c->kv_max_seq = 0;
-  c->bound = false;
+  c->bound = c->whole = false;
 }
 
 extern "C" int gq_hip_kv_init(gq_ctx *c, int n_layers, int n_kv_heads, int head_dim, int max_seq,
@@ -473,7 +505,7 @@ extern "C" int gq_hip_kv_init(gq_ctx *c, int n_layers, int n_kv_heads, int head_
   (void)hipSetDevice(c->dev);
   kv_release(c);
   free_graph(c);
-  c->bound = false;
+  c->bound = c->whole = false;
   const size_t bytes = sizeof(float) * (size_t)n_kv_heads * max_seq * head_dim * n_layers;
   const size_t half = (size_t)head_dim / 2;
   c->kslab = (float *)dev_alloc(c, bytes);
@@ -711,20 +743,15 @@ extern "C" int gq_hip_lctx_restore_image(gq_ctx *c, const void *image, size_t si
   const size_t off = sizeof h + sizeof(int32_t) * (size_t)h.n_tokens;
   if (size < off + 2 * slab) return fail(c, -1, "lctx_restore: short image");
   /* the image's K and V regions are laid out exactly like the device slabs */
-  hipEvent_t e0, e1;
-  HIPCHK(c, hipEventCreate(&e0));
-  HIPCHK(c, hipEventCreate(&e1));
-  HIPCHK(c, hipEventRecord(e0, c->stream));
+  EventPair ev;
+  HIPCHK(c, ev.create());
+  HIPCHK(c, hipEventRecord(ev.e0, c->stream));
   HIPCHK(c, hipMemcpyAsync(c->kslab, (const char *)image + off, slab, hipMemcpyHostToDevice, c->stream));
   HIPCHK(c, hipMemcpyAsync(c->vslab, (const char *)image + off + slab, slab, hipMemcpyHostToDevice,
                            c->stream));
-  HIPCHK(c, hipEventRecord(e1, c->stream));
-  HIPCHK(c, hipEventSynchronize(e1));
-  float t = 0.f;
-  (void)hipEventElapsedTime(&t, e0, e1);
-  (void)hipEventDestroy(e0);
-  (void)hipEventDestroy(e1);
-  if (ms) *ms = t;
+  HIPCHK(c, hipEventRecord(ev.e1, c->stream));
+  HIPCHK(c, hipEventSynchronize(ev.e1));
+  if (ms) *ms = ev.ms();
   if (current_pos) *current_pos = h.current_pos;
   return 0;
 }
@@ -801,31 +828,47 @@ extern "C" int gq_hip_model_bind(gq_ctx *c, const gq_model *m) {
   if ((m->hidden & 255) || (m->ff & 255))
     return fail(c, -1, "model_bind: hidden and ff must be multiples of 256");
   const int H = m->hidden, F = m->ff, kvd = m->n_kv_heads * m->head_dim;
+  /* A layer whose seven projections and norm weights are all NULL stays on
+   * the host (the --n-gpu-layers split, or a projection the device kernels
+   * do not take); so may the LM head and the embedding (an F32 LM head, for
+   * one).  Anything in between is an error. */
+  std::vector<char> on(m->n_layers, 0);
   for (int l = 0; l < m->n_layers; l++) {
     const gq_layer &L = m->layers[l];
+    const void *ps[9] = {L.wq.data, L.wk.data, L.wv.data, L.wo.data, L.w_gate.data, L.w_up.data, L.w_down.data,
+                         L.rms_att, L.rms_ffn};
+    int n_set = 0;
+    for (const void *p : ps) n_set += p != nullptr;
+    if (n_set == 0) continue;
     int rc = check_weight(c, L.wq, H, H, "wq") || check_weight(c, L.wk, kvd, H, "wk") ||
              check_weight(c, L.wv, kvd, H, "wv") || check_weight(c, L.wo, H, H, "wo") ||
              check_weight(c, L.w_gate, F, H, "w_gate") || check_weight(c, L.w_up, F, H, "w_up") ||
              check_weight(c, L.w_down, H, F, "w_down");
-    if (rc) return -1;
+    if (rc) return fail(c, -1, "layer %d: %s", l, c->err);
     if (!L.rms_att || !L.rms_ffn) return fail(c, -1, "layer %d: norm weights", l);
+    on[l] = 1;
   }
-  if (check_weight(c, m->lm_head, m->vocab, H, "lm_head")) return -1;
-  if (!m->embed.data || m->embed.rows != m->vocab || m->embed.cols != H ||
-      (m->embed.dtype != GQ_F32 && m->embed.dtype != GQ_Q8_0 && m->embed.dtype != GQ_Q4_K))
+  const bool has_lm = m->lm_head.data != nullptr, has_embed = m->embed.data != nullptr;
+  if (has_lm && check_weight(c, m->lm_head, m->vocab, H, "lm_head")) return -1;
+  if (has_embed && (m->embed.rows != m->vocab || m->embed.cols != H ||
+                    (m->embed.dtype != GQ_F32 && m->embed.dtype != GQ_Q8_0 && m->embed.dtype != GQ_Q4_K)))
     return fail(c, -1, "embed: F32, Q8_0 or Q4_K (vocab x hidden)");
-  if (!m->rms_final) return fail(c, -1, "rms_final");
+  if (has_lm && !m->rms_final) return fail(c, -1, "rms_final");
   free_graph(c);
   pf_release(c); /* sized for the previous model */
   c->m = *m;
   c->layers.assign(m->layers, m->layers + m->n_layers);
   c->m.layers = c->layers.data();
+  c->layer_on = on;
+  c->whole = has_lm && has_embed && m->rms_final;
+  for (char o : on) c->whole = c->whole && o;
   /* tile-interleaved copies for the matrix-core matvec, for the launches
    * the decode step runs on it (gate/up + SwiGLU, the LM head); ordered on
    * the stream after whatever wrote the weights */
   mm_free(c);
   c->mm.resize(m->n_layers);
   for (int l = 0; l < m->n_layers; l++) {
+    if (!on[l]) continue;
     const gq_layer &L = c->layers[l];
     const gq_weight *gu[2] = {&L.w_gate, &L.w_up};
     if (L.w_gate.dtype == L.w_up.dtype) c->mm[l].gu = mm_build(c, gu, 2, true);
@@ -847,7 +890,7 @@ extern "C" int gq_hip_model_bind(gq_ctx *c, const gq_model *m) {
       else if (d) gq_hip_free(c, d);
     }
   }
-  {
+  if (has_lm) {
     const gq_weight *lm[1] = {&m->lm_head};
     c->mm_lm = mm_build(c, lm, 1, false);
   }
@@ -1047,6 +1090,7 @@ static int run_step(gq_ctx *c, int token, int pos, bool device_state, float *hid
   Workspace &w = c->ws;
   int rc;
   const int *pos_dev = device_state ? w.d_pos : nullptr;
+  if (!device_state) c->g_valid = false; /* w.hidden and d_token take this step's values */
   if (!device_state) {
     if ((rc = gq_launch_embed(m.embed.dtype, m.embed.data, m.hidden, nullptr, token, w.hidden, c->stream)))
       return rc;
@@ -1068,18 +1112,31 @@ static int run_step(gq_ctx *c, int token, int pos, bool device_state, float *hid
   return 0;
 }
 
+/* Positions pos .. pos+n-1 of a whole-model entry point (every layer, the
+ * embedding and the LM head on the device). */
 static int check_pos(gq_ctx *c, int pos, int n) {
   if (!c->bound) return fail(c, -1, "no model bound");
+  if (!c->whole)
+    return fail(c, -1, "the bound model is not wholly on the device (host layers, LM head or embedding)");
   if (pos < 0 || pos + n > c->kv_max_seq)
     return fail(c, -5, "positions %d..%d outside the KV cache (max_seq %d)", pos, pos + n - 1, c->kv_max_seq);
   return 0;
 }
 
+/* One bound layer at one position (the per-layer hook). */
+static int check_layer_pos(gq_ctx *c, int layer, int pos) {
+  if (!c->bound) return fail(c, -1, "no model bound");
+  if (layer < 0 || layer >= c->m.n_layers) return fail(c, -1, "bad layer %d", layer);
+  if (!c->layer_on[layer]) return fail(c, -1, "layer %d is not on the device", layer);
+  if (pos < 0 || pos >= c->kv_max_seq)
+    return fail(c, -5, "position %d outside the KV cache (max_seq %d)", pos, c->kv_max_seq);
+  return 0;
+}
+
 extern "C" int gq_hip_decode_layer_dev(gq_ctx *c, int layer, int pos, float *hidden) {
   if (!c || !hidden) return -1;
-  int rc = check_pos(c, pos, 1);
+  int rc = check_layer_pos(c, layer, pos);
   if (rc) return rc;
-  if (layer < 0 || layer >= c->m.n_layers) return fail(c, -1, "bad layer");
   rc = run_layer(c, layer, pos, nullptr, hidden);
   return rc ? fail(c, rc, "decode_layer launch failed") : 0;
 }
@@ -1087,10 +1144,10 @@ extern "C" int gq_hip_decode_layer_dev(gq_ctx *c, int layer, int pos, float *hid
 extern "C" int gq_hip_transformer_layer(gq_ctx *c, int layer, int pos, float *h_hidden, float *h_k,
                                         float *h_v, int head_stride) {
   if (!c || !h_hidden) return -1;
-  int rc = check_pos(c, pos, 1);
+  int rc = check_layer_pos(c, layer, pos);
   if (rc) return rc;
-  if (layer < 0 || layer >= c->m.n_layers) return fail(c, -1, "bad layer");
   const int H = c->m.hidden;
+  c->g_valid = false;
   HIPCHK(c, hipMemcpyAsync(c->ws.hidden, h_hidden, sizeof(float) * H, hipMemcpyHostToDevice, c->stream));
   if ((rc = run_layer(c, layer, pos, nullptr, c->ws.hidden))) return fail(c, rc, "layer launch failed");
   HIPCHK(c, hipMemcpyAsync(h_hidden, c->ws.hidden, sizeof(float) * H, hipMemcpyDeviceToHost, c->stream));
@@ -1106,11 +1163,57 @@ extern "C" int gq_hip_transformer_layer(gq_ctx *c, int layer, int pos, float *h_
   return 0;
 }
 
+static int ensure_tokens(gq_ctx *c, int n);
+static int ensure_graph(gq_ctx *c);
+
+/* One decode step of a host-driven loop (the generate and chat loops call
+ * forward_token / forward_sample once per token) as a replay of the
+ * captured step graph.  The graph expects the token's embedding in w.hidden
+ * and token, position and step on the device, and leaves the argmax
+ * token's embedding and the next position there.  When the caller's
+ * (token, pos) is what the previous replay left (a greedy loop), only the
+ * step counter is reset; otherwise the token is embedded first. */
+static int graph_step(gq_ctx *c, int token, int pos) {
+  Workspace &w = c->ws;
+  int rc;
+  if ((rc = ensure_tokens(c, 1)) || (rc = ensure_graph(c))) return rc;
+  if (!c->st_pinned && hipHostMalloc((void **)&c->st_pinned, 4 * sizeof(int)) != hipSuccess) {
+    c->st_pinned = nullptr;
+    return fail(c, -4, "pinned step state");
+  }
+  const bool same = c->g_valid && c->g_token == token && c->g_pos == pos;
+  c->st_pinned[0] = token, c->st_pinned[1] = pos, c->st_pinned[2] = 0;
+  HIPCHK(c, hipMemcpyAsync(w.d_token, c->st_pinned, 3 * sizeof(int), hipMemcpyHostToDevice, c->stream));
+  if (!same && (rc = gq_launch_embed(c->m.embed.dtype, c->m.embed.data, c->m.hidden, w.d_token, token, w.hidden,
+                                     c->stream)))
+    return fail(c, rc, "embed launch failed");
+  c->g_valid = false;
+  HIPCHK(c, hipGraphLaunch(c->gexec, c->stream));
+  return 0;
+}
+
+/* After graph_step: the argmax token to the host; the device state is then
+ * (next, pos + 1). */
+static int graph_step_token(gq_ctx *c, int pos, float *logits) {
+  HIPCHK(c, hipMemcpyAsync(c->st_pinned + 3, c->ws.d_token, sizeof(int), hipMemcpyDeviceToHost, c->stream));
+  if (logits)
+    HIPCHK(c, hipMemcpyAsync(logits, c->ws.logits, sizeof(float) * c->m.vocab, hipMemcpyDeviceToHost,
+                             c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  const int next = c->st_pinned[3];
+  c->g_valid = true, c->g_token = next, c->g_pos = pos + 1;
+  return next;
+}
+
 extern "C" int gq_hip_forward_token(gq_ctx *c, int token, int pos, float *logits, float *hidden_per_layer) {
   if (!c) return -1;
   int rc = check_pos(c, pos, 1);
   if (rc) return rc;
   if (token < 0 || token >= c->m.vocab) return fail(c, -1, "token %d out of range", token);
+  if (!hidden_per_layer) { /* no per-layer copies: the captured step */
+    if ((rc = graph_step(c, token, pos))) return rc;
+    return graph_step_token(c, pos, logits);
+  }
   if ((rc = run_step(c, token, pos, false, hidden_per_layer))) return fail(c, rc, "step launch failed");
   int next = -1;
   HIPCHK(c, hipMemcpyAsync(&next, c->ws.d_token, sizeof(int), hipMemcpyDeviceToHost, c->stream));
@@ -1132,6 +1235,27 @@ static int ensure_tokens(gq_ctx *c, int n) {
   return 0;
 }
 
+/* The decode step captured once into a HIP graph (run_step's device-state
+ * form: token, position and step read on the device). */
+static int ensure_graph(gq_ctx *c) {
+  if (c->gexec) return 0;
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  HIPCHK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+  const int rc = run_step(c, 0, 0, true, nullptr);
+  hipGraph_t g = nullptr;
+  const hipError_t e = hipStreamEndCapture(c->stream, &g);
+  if (rc || e != hipSuccess) {
+    if (g) (void)hipGraphDestroy(g);
+    return fail(c, rc ? rc : -4, "graph capture failed");
+  }
+  c->graph = g;
+  if (hipGraphInstantiate(&c->gexec, g, nullptr, nullptr, 0) != hipSuccess) {
+    free_graph(c);
+    return fail(c, -4, "graph instantiate failed");
+  }
+  return 0;
+}
+
 extern "C" int gq_hip_decode_loop(gq_ctx *c, int token, int pos, int n_steps, int use_graph,
                                   int32_t *tokens_out, float *ms) {
   if (!c || n_steps <= 0 || !tokens_out) return fail(c, -1, "decode_loop: bad argument");
@@ -1143,26 +1267,11 @@ extern "C" int gq_hip_decode_loop(gq_ctx *c, int token, int pos, int n_steps, in
   int st[3] = {token, pos, 0};
   HIPCHK(c, hipMemcpyAsync(w.d_token, st, sizeof st, hipMemcpyHostToDevice, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));
-  if (use_graph && !c->gexec) {
-    HIPCHK(c, hipStreamSynchronize(c->stream));
-    HIPCHK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
-    rc = run_step(c, token, pos, true, nullptr);
-    hipGraph_t g = nullptr;
-    hipError_t e = hipStreamEndCapture(c->stream, &g);
-    if (rc || e != hipSuccess) {
-      if (g) (void)hipGraphDestroy(g);
-      return fail(c, rc ? rc : -4, "graph capture failed");
-    }
-    c->graph = g;
-    if (hipGraphInstantiate(&c->gexec, g, nullptr, nullptr, 0) != hipSuccess) {
-      free_graph(c);
-      return fail(c, -4, "graph instantiate failed");
-    }
-  }
-  hipEvent_t e0, e1;
-  HIPCHK(c, hipEventCreate(&e0));
-  HIPCHK(c, hipEventCreate(&e1));
-  HIPCHK(c, hipEventRecord(e0, c->stream));
+  if (use_graph && (rc = ensure_graph(c))) return rc;
+  c->g_valid = false;
+  EventPair ev;
+  HIPCHK(c, ev.create());
+  HIPCHK(c, hipEventRecord(ev.e0, c->stream));
   /* the first step's input; each step's argmax embeds the next token */
   if ((rc = gq_launch_embed(c->m.embed.dtype, c->m.embed.data, c->m.hidden, w.d_token, token, w.hidden, c->stream)))
     return fail(c, rc, "embed launch failed");
@@ -1173,14 +1282,10 @@ extern "C" int gq_hip_decode_loop(gq_ctx *c, int token, int pos, int n_steps, in
       return fail(c, rc, "step launch failed");
     }
   }
-  HIPCHK(c, hipEventRecord(e1, c->stream));
+  HIPCHK(c, hipEventRecord(ev.e1, c->stream));
   HIPCHK(c, hipMemcpyAsync(tokens_out, w.d_tokens, sizeof(int32_t) * n_steps, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));
-  float t = 0.f;
-  (void)hipEventElapsedTime(&t, e0, e1);
-  (void)hipEventDestroy(e0);
-  (void)hipEventDestroy(e1);
-  if (ms) *ms = t;
+  if (ms) *ms = ev.ms();
   return 0;
 }
 
@@ -1243,6 +1348,7 @@ static bool pf_gemm_ok(const gq_weight &w) {
 }
 
 static bool pf_model_ok(const gq_ctx *c) {
+  if (c->prefill_mode != 0) return false;
   for (const gq_layer &L : c->layers)
     if (!pf_gemm_ok(L.wq) || !pf_gemm_ok(L.wk) || !pf_gemm_ok(L.wv) || !pf_gemm_ok(L.wo) || !pf_gemm_ok(L.w_gate) ||
         !pf_gemm_ok(L.w_up) || !pf_gemm_ok(L.w_down) || L.w_gate.dtype != L.w_up.dtype)
@@ -1338,13 +1444,13 @@ extern "C" int gq_hip_prefill(gq_ctx *c, const int32_t *tokens, int n_tokens, in
     if (tokens[i] < 0 || tokens[i] >= m.vocab) return fail(c, -1, "prefill: token %d out of range", tokens[i]);
   const bool gemm = pf_model_ok(c);
   if (gemm && (rc = pf_alloc(c))) return rc;
+  c->g_valid = false;
   PrefillWs &w = c->pf;
   Workspace &ws = c->ws;
-  hipEvent_t e0 = nullptr, e1 = nullptr;
+  EventPair ev;
   if (ms) {
-    HIPCHK(c, hipEventCreate(&e0));
-    HIPCHK(c, hipEventCreate(&e1));
-    HIPCHK(c, hipEventRecord(e0, c->stream));
+    HIPCHK(c, ev.create());
+    HIPCHK(c, hipEventRecord(ev.e0, c->stream));
   }
   int T = 0;
   if (!gemm) { /* token by token through the decode step */
@@ -1368,7 +1474,7 @@ extern "C" int gq_hip_prefill(gq_ctx *c, const int32_t *tokens, int n_tokens, in
                                c->stream)))
       return fail(c, rc, "prefill: lm head");
   }
-  if (ms) HIPCHK(c, hipEventRecord(e1, c->stream));
+  if (ms) HIPCHK(c, hipEventRecord(ev.e1, c->stream));
   int next = -1;
   HIPCHK(c, hipMemcpyAsync(&next, ws.d_token, sizeof(int), hipMemcpyDeviceToHost, c->stream));
   if (logits)
@@ -1376,14 +1482,24 @@ extern "C" int gq_hip_prefill(gq_ctx *c, const int32_t *tokens, int n_tokens, in
   if (hidden_last)
     HIPCHK(c, hipMemcpyAsync(hidden_last, ws.hidden, sizeof(float) * m.hidden, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));
-  if (ms) {
-    float t = 0.f;
-    (void)hipEventElapsedTime(&t, e0, e1);
-    *ms = t;
-    (void)hipEventDestroy(e0);
-    (void)hipEventDestroy(e1);
-  }
+  if (ms) *ms = ev.ms();
   return next;
+}
+
+extern "C" int gq_hip_bound_layers(gq_ctx *c, int *whole) {
+  if (!c) return -1;
+  int n = 0;
+  if (c->bound)
+    for (char o : c->layer_on) n += o;
+  if (whole) *whole = c->bound && c->whole;
+  return n;
+}
+
+extern "C" int gq_hip_set_prefill_mode(gq_ctx *c, int mode) {
+  if (!c || (mode != 0 && mode != 1)) return -1;
+  const int prev = c->prefill_mode;
+  c->prefill_mode = mode;
+  return prev;
 }
 
 /* ------------------------------------------------------------ measurement */
@@ -1417,11 +1533,12 @@ extern "C" int gq_hip_profile_step(gq_ctx *c, int token, int pos, double ms[GQ_N
 extern "C" float gq_hip_time_op(gq_ctx *c, int op, int pos, int n_iter) {
   if (!c || n_iter <= 0 || op < 0 || op > PC_LM_HEAD) return -1.f;
   if (check_pos(c, pos, 1)) return -1.f;
-  hipEvent_t e0, e1;
-  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return -1.f;
+  EventPair ev;
+  if (ev.create() != hipSuccess) return -1.f;
   float *h = c->ws.hidden;
+  c->g_valid = false;
   int rc = 0;
-  (void)hipEventRecord(e0, c->stream);
+  (void)hipEventRecord(ev.e0, c->stream);
   for (int i = 0; i < n_iter && !rc; i++) {
     const int l = i % c->m.n_layers; /* every layer's weights: no cache reuse */
     switch (op) {
@@ -1433,14 +1550,10 @@ extern "C" float gq_hip_time_op(gq_ctx *c, int op, int pos, int n_iter) {
     default: rc = op_lm_head(c, h); break;
     }
   }
-  (void)hipEventRecord(e1, c->stream);
-  (void)hipEventSynchronize(e1);
-  float t = 0.f;
-  (void)hipEventElapsedTime(&t, e0, e1);
-  (void)hipEventDestroy(e0);
-  (void)hipEventDestroy(e1);
+  (void)hipEventRecord(ev.e1, c->stream);
+  (void)hipEventSynchronize(ev.e1);
   if (rc) return fail(c, rc, "time_op launch failed"), -1.f;
-  return t / n_iter;
+  return ev.ms() / n_iter;
 }
 
 extern "C" float gq_hip_time_matvec(gq_ctx *c, int dtype, const void *const *w_devs, int n_w, int rows,
@@ -1451,18 +1564,17 @@ extern "C" float gq_hip_time_matvec(gq_ctx *c, int dtype, const void *const *w_d
    * kernel is selected */
   std::vector<const uint8_t *> mm(n_w, nullptr);
   for (int i = 0; i < n_w; i++) mm[i] = op_tile(c, dtype, w_devs[i], rows, cols);
-  hipEvent_t e0, e1;
-  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return -1.f;
-  (void)hipEventRecord(e0, c->stream);
-  int rc = 0;
+  EventPair ev;
+  int rc = ev.create() == hipSuccess ? 0 : -4;
+  if (!rc) (void)hipEventRecord(ev.e0, c->stream);
   for (int i = 0; i < n_iter && !rc; i++)
     rc = launch_one_mv(c, dtype, w_devs[i % n_w], rows, cols, x, y + (size_t)(i % n_w) * rows, mm[i % n_w]);
-  (void)hipEventRecord(e1, c->stream);
-  (void)hipEventSynchronize(e1);
   float t = 0.f;
-  (void)hipEventElapsedTime(&t, e0, e1);
-  (void)hipEventDestroy(e0);
-  (void)hipEventDestroy(e1);
+  if (!rc) {
+    (void)hipEventRecord(ev.e1, c->stream);
+    (void)hipEventSynchronize(ev.e1);
+    t = ev.ms();
+  }
   for (const uint8_t *p : mm)
     if (p) gq_hip_free(c, (void *)p);
   return rc ? -1.f : t / n_iter;
@@ -1473,35 +1585,30 @@ extern "C" float gq_hip_time_attention(gq_ctx *c, int layer, int pos, const floa
   if (!c || !c->kslab || !q || !out || n_iter <= 0 || pos < 0 || pos >= c->kv_max_seq) return -1.f;
   const int n_heads = c->bound ? c->m.n_heads : -1;
   if (n_heads <= 0) return -1.f;
-  hipEvent_t e0, e1;
-  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return -1.f;
+  EventPair ev;
+  if (ev.create() != hipSuccess) return -1.f;
   AttnArgs aa{};
   aa.q = q, aa.part_o = c->ws.part_o, aa.part_ml = c->ws.part_ml, aa.out = out;
   aa.pos = pos, aa.n_heads = n_heads, aa.n_kv = c->kv_heads, aa.hd = c->kv_hd;
   aa.max_seq = c->kv_max_seq, aa.nch = c->ws.nch, aa.s_max = c->ws.s_max;
   aa.scale = 1.0f / sqrtf((float)c->kv_hd);
-  (void)hipEventRecord(e0, c->stream);
+  (void)hipEventRecord(ev.e0, c->stream);
   for (int i = 0; i < n_iter; i++) {
     const int l = (layer + i) % c->kv_layers;
     aa.k = gq_hip_kv_k(c, l), aa.v = gq_hip_kv_v(c, l);
     if (gq_launch_attention(aa, c->stream, nullptr)) return -1.f;
   }
-  (void)hipEventRecord(e1, c->stream);
-  (void)hipEventSynchronize(e1);
-  float t = 0.f;
-  (void)hipEventElapsedTime(&t, e0, e1);
-  (void)hipEventDestroy(e0);
-  (void)hipEventDestroy(e1);
-  return t / n_iter;
+  (void)hipEventRecord(ev.e1, c->stream);
+  (void)hipEventSynchronize(ev.e1);
+  return ev.ms() / n_iter;
 }
 
 /* ------------------------------------------------------------ op-level */
 extern "C" int gq_hip_qkv_rope_dev(gq_ctx *c, int layer, int pos, const float *hidden, float *q_out,
                                    int fused) {
   if (!c || !hidden || !q_out) return -1;
-  int rc = check_pos(c, pos, 1);
+  int rc = check_layer_pos(c, layer, pos);
   if (rc) return rc;
-  if (layer < 0 || layer >= c->m.n_layers) return fail(c, -1, "bad layer");
   const gq_model &m = c->m;
   const gq_layer &L = c->layers[layer];
   Workspace &w = c->ws;
@@ -1626,13 +1733,13 @@ static int sample_ensure(gq_ctx *c, int vocab, bool big) {
   SampleWs &w = c->sw;
   if (!c->d_sample && !(c->d_sample = (int *)dev_alloc(c, sizeof(int)))) return -4;
   if (!big || w.cap >= vocab) return 0;
-  const size_t cub = gq_sample_ws_bytes(vocab);
+  const size_t sort_bytes = gq_sample_ws_bytes(vocab);
   float *keys = (float *)dev_alloc(c, sizeof(float) * vocab);
   int *ids_in = (int *)dev_alloc(c, sizeof(int) * vocab), *ids = (int *)dev_alloc(c, sizeof(int) * vocab);
-  void *tmp = dev_alloc(c, cub);
+  void *tmp = dev_alloc(c, sort_bytes);
   if (!keys || !ids_in || !ids || !tmp) return -4;
-  if (w.keys) gq_hip_free(c, w.keys), gq_hip_free(c, w.ids_in), gq_hip_free(c, w.ids), gq_hip_free(c, w.cub);
-  w.keys = keys, w.ids_in = ids_in, w.ids = ids, w.cub = tmp, w.cub_bytes = cub, w.cap = vocab;
+  if (w.keys) gq_hip_free(c, w.keys), gq_hip_free(c, w.ids_in), gq_hip_free(c, w.ids), gq_hip_free(c, w.sort_tmp);
+  w.keys = keys, w.ids_in = ids_in, w.ids = ids, w.sort_tmp = tmp, w.sort_bytes = sort_bytes, w.cap = vocab;
   return 0;
 }
 
@@ -1676,8 +1783,15 @@ extern "C" int gq_hip_forward_sample(gq_ctx *c, int token, int pos, float temper
   int rc = check_pos(c, pos, 1);
   if (rc) return rc;
   if (token < 0 || token >= c->m.vocab) return fail(c, -1, "token %d out of range", token);
-  if ((rc = run_step(c, token, pos, false, nullptr))) return fail(c, rc, "step launch failed");
-  return sample_on_device(c, c->ws.logits, c->m.vocab, temperature, top_k, top_p, rnd);
+  if (temperature <= 0.0f) { /* greedy: the step's own argmax */
+    if ((rc = graph_step(c, token, pos))) return rc;
+    return graph_step_token(c, pos, nullptr);
+  }
+  if ((rc = graph_step(c, token, pos))) return rc;
+  /* the sampled token generally differs from the argmax the replay embedded */
+  const int next = sample_on_device(c, c->ws.logits, c->m.vocab, temperature, top_k, top_p, rnd);
+  c->g_valid = false; /* the replay embedded its argmax, not the sampled token */
+  return next;
 }
 
 /* One turn of the chat REPL (chat_repl, chat.c:157-263) on the device: the
@@ -1693,9 +1807,9 @@ constexpr int kChatMaxReply = 512; /* CHAT_MAX_OUTPUT_TOKENS, chat.c:14 */
 extern "C" int gq_hip_chat_turn(gq_ctx *c, const int32_t *tokens, int n_tokens, int *current_pos, int max_tokens,
                                 int eos_token, float temperature, int top_k, float top_p, const int *rnd,
                                 int32_t *reply) {
-  if (!c || !c->bound || !tokens || n_tokens <= 0 || !current_pos || max_tokens <= 0 || !reply ||
+  if (!c || !c->whole || !tokens || n_tokens <= 0 || !current_pos || max_tokens <= 0 || !reply ||
       (temperature > 0.0f && !rnd))
-    return fail(c, -1, "chat_turn: bad argument");
+    return fail(c, -1, "chat_turn: bad argument or no whole model on the device");
   const int p0 = *current_pos;
   if (p0 < 0 || p0 + n_tokens >= c->kv_max_seq - 1) /* chat.c:169 */
     return fail(c, -6, "chat_turn: %d tokens at %d do not fit the %d-position context", n_tokens, p0,
@@ -1774,19 +1888,17 @@ extern "C" float gq_hip_time_prefill_gemm(gq_ctx *c, int dtype, const void *w, i
   const uint8_t *ps = op_steps(c, dtype, w, n, k);
   a.T = t, a.K = k, a.nseg = 1, a.seg[0] = op_seg(ps, w, y, n, dtype);
   pf_parts(c, a);
-  hipEvent_t e0 = nullptr, e1 = nullptr;
-  int rc = hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess ? 0 : -4;
+  EventPair ev;
+  int rc = ev.create() == hipSuccess ? 0 : -4;
   if (!rc) rc = gq_launch_pgemm(MV_STORE, a, c->stream); /* untimed first launch */
-  if (!rc) (void)hipEventRecord(e0, c->stream);
+  if (!rc) (void)hipEventRecord(ev.e0, c->stream);
   for (int i = 0; i < n_iter && !rc; i++) rc = gq_launch_pgemm(MV_STORE, a, c->stream);
   float ms = 0.f;
   if (!rc) {
-    (void)hipEventRecord(e1, c->stream);
-    (void)hipEventSynchronize(e1);
-    (void)hipEventElapsedTime(&ms, e0, e1);
+    (void)hipEventRecord(ev.e1, c->stream);
+    (void)hipEventSynchronize(ev.e1);
+    ms = ev.ms();
   }
-  if (e0) (void)hipEventDestroy(e0);
-  if (e1) (void)hipEventDestroy(e1);
   if (ps) gq_hip_free(c, (void *)ps);
   if (rc) return fail(c, rc, "time GEMM launch"), -1.f;
   return ms / n_iter;

@@ -20,14 +20,15 @@
  *     For k <= 64 the slots live in registers, one per lane, and a
  *     replacement's new minimum is one DPP reduction.  The softmax over the
  *     slots and the draw then run on one thread in the reference's order.
- *   top-p (tokenizer.c:282-333): stable descending sort (hipCUB radix sort;
- *     the reference's qsort is glibc's merge sort, stable for equal logits),
+ *   top-p (tokenizer.c:282-333): stable descending sort (rocPRIM's device
+ *     radix sort of (logit, index) pairs; the reference's qsort is glibc's
+ *     merge sort, stable for equal logits),
  *     then the cumulative probabilities in double.
  *   temperature (tokenizer.c:187-217): the exponentials in parallel, the
  *     reference's sequential float sum and scan on one thread (see
  *     temp_kernel).
  */
-#include <hipcub/hipcub.hpp>
+#include <rocprim/device/device_radix_sort.hpp>
 
 #include "gq_device.h"
 #include "gq_internal.h"
@@ -462,10 +463,10 @@ __global__ void iota_kernel(int *v, int n) {
 } // namespace
 
 size_t gq_sample_ws_bytes(int vocab) {
-  size_t cub = 0;
-  (void)hipcub::DeviceRadixSort::SortPairsDescending(nullptr, cub, (const float *)nullptr, (float *)nullptr,
-                                                     (const int *)nullptr, (int *)nullptr, vocab, 0, 32);
-  return cub;
+  size_t bytes = 0;
+  (void)rocprim::radix_sort_pairs_desc(nullptr, bytes, (const float *)nullptr, (float *)nullptr,
+                                       (const int *)nullptr, (int *)nullptr, (size_t)vocab);
+  return bytes;
 }
 
 int gq_launch_sample(const float *logits, int vocab, float temperature, int top_k, float top_p, int rnd,
@@ -477,11 +478,11 @@ int gq_launch_sample(const float *logits, int vocab, float temperature, int top_
     hipLaunchKernelGGL(topk_kernel, dim3(1), dim3(kST), 0, s, logits, vocab, top_k, temperature, rnd, out);
   } else if (top_p < 1.0f) {
     if (top_p <= 0.0f) return 1; /* greedy (tokenizer.c:287) */
-    if (!ws.keys || !ws.ids_in || !ws.ids || !ws.cub || ws.cap < vocab) return -1;
+    if (!ws.keys || !ws.ids_in || !ws.ids || !ws.sort_tmp || ws.cap < vocab) return -1;
     hipLaunchKernelGGL(iota_kernel, dim3((vocab + 255) / 256), dim3(256), 0, s, ws.ids_in, vocab);
-    size_t bytes = ws.cub_bytes;
-    if (hipcub::DeviceRadixSort::SortPairsDescending(ws.cub, bytes, logits, ws.keys, ws.ids_in, ws.ids, vocab, 0,
-                                                     32, s) != hipSuccess)
+    size_t bytes = ws.sort_bytes;
+    if (rocprim::radix_sort_pairs_desc(ws.sort_tmp, bytes, logits, ws.keys, ws.ids_in, ws.ids, (size_t)vocab, 0,
+                                       8 * (unsigned)sizeof(float), s) != hipSuccess)
       return -4;
     hipLaunchKernelGGL(topp_kernel, dim3(1), dim3(kST), 0, s, ws.keys, ws.ids, vocab, top_p, temperature, rnd, out);
   } else {

@@ -95,6 +95,20 @@ GQ_HD uint16_t gq_f32_to_f16(float f) {
   return (uint16_t)(sign | q);
 }
 
+/* IEEE binary16 -> fp32, exact (subnormals, inf and NaN included). */
+GQ_HD float gq_f16_to_f32(uint16_t h) {
+  uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  if (e == 0x1fu) return gq_bits_f32(sign | 0x7f800000u | (m << 13));
+  if (e == 0u) { /* zero or subnormal: m * 2^-24, normalised by hand */
+    if (m == 0u) return gq_bits_f32(sign);
+    uint32_t ex = 113u; /* exponent field of 2^-14 */
+    while (!(m & 0x400u)) m <<= 1, ex--;
+    return gq_bits_f32(sign | (ex << 23) | ((m & 0x3ffu) << 13));
+  }
+  return gq_bits_f32(sign | ((e + 112u) << 23) | (m << 13));
+}
+
 /* 24-bit uniform in [0,1) from a hash word. */
 GQ_HD float gq_u01(uint64_t h) {
   return (float)(uint32_t)(h >> 40) * 5.9604644775390625e-08f; /* 2^-24, exact */
@@ -167,6 +181,36 @@ GQ_HD uint8_t gq_q4k_byte(uint64_t seed, uint64_t b, uint32_t o) {
 }
 
 /*
+ * Byte `o` (0..143) of a zero-mean Q4_K super-block `b`.  The plain rule
+ * above gives w = d*sc*q - dmin*m a mean of about 5 (q averages 7.5 and
+ * d, dmin, sc, m are independent and positive), which pushes every hidden
+ * state along one direction.  Here each sub-block's min cancels its scale's
+ * mean: m_j = sc_j and dmin = fp16(7.5 * d), so w = d*sc_j*(q - 7.5) up to
+ * the rounding of dmin.  d and the quants are the plain rule's bytes; the 8
+ * six-bit sc_j come from their own stream and are packed as
+ * get_scale_min_k4 (quant_matvec_q4_k.c:47-56) unpacks them.
+ */
+GQ_HD uint8_t gq_q4k_zm_byte(uint64_t seed, uint64_t b, uint32_t o) {
+  if (o < 2u) return gq_q4k_byte(seed, b, o);
+  if (o < 4u) {
+    uint16_t d = (uint16_t)(gq_q4k_byte(seed, b, 0u) | (gq_q4k_byte(seed, b, 1u) << 8));
+    uint16_t h = gq_f32_to_f16(7.5f * gq_f16_to_f32(d)); /* the product is exact in fp32 */
+    return (uint8_t)(h >> (8u * (o - 2u)));
+  }
+  if (o < 16u) {
+    uint64_t v = gq_hash(gq_subseed(seed, 5u), b); /* sc_j = bits 6j..6j+5 */
+    uint32_t i = o - 4u;
+    if (i < 8u) { /* scales[i], i = j or j + 4 for j < 4: sc_j (and m_j), top bits of sc_{j+4} */
+      uint32_t j = i & 3u;
+      return (uint8_t)(((v >> (6u * j)) & 63u) | (((v >> (6u * (j + 4u) + 4u)) & 3u) << 6));
+    }
+    uint32_t lo = (uint32_t)(v >> (6u * (i - 4u))) & 15u; /* scales[8+j]: low nibbles of sc_{4+j}, m_{4+j} */
+    return (uint8_t)(lo | (lo << 4));
+  }
+  return gq_q4k_byte(seed, b, o);
+}
+
+/*
  * Byte `o` (0..209) of Q6_K super-block `b`: ql[128], qh[64] uniform bytes,
  * scales[16] int8 uniform in -32..31, d fp16 U(0.001,0.05).
  */
@@ -188,5 +232,9 @@ GQ_HD uint8_t gq_q8_0_byte(uint64_t seed, uint64_t b, uint32_t o) {
   }
   return gq_byte(seed, b * 34ULL + o);
 }
+
+/* Generator code of the zero-mean Q4_K rule: this flag or'ed into the Q4_K
+ * dtype code (the blocks are still Q4_K). */
+#define GQ_SYNTH_Q4K_ZERO_MEAN 0x100
 
 #endif /* GQ_SYNTH_H */

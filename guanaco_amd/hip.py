@@ -67,6 +67,8 @@ def _load():
         "gq_hip_host_alloc_pinned": (_vp, [C.c_size_t]),
         "gq_hip_host_free_pinned": (None, [_vp]),
         "gq_hip_model_bind": (C.c_int, [_vp, _vp]),
+        "gq_hip_bound_layers": (C.c_int, [_vp, _vp]),
+        "gq_hip_set_prefill_mode": (C.c_int, [_vp, C.c_int]),
         "gq_hip_decode_layer_dev": (C.c_int, [_vp, C.c_int, C.c_int, _vp]),
         "gq_hip_transformer_layer": (C.c_int, [_vp, C.c_int, C.c_int, _fp, _fp, _fp, C.c_int]),
         "gq_hip_forward_token": (C.c_int, [_vp, C.c_int, C.c_int, _fp, _fp]),
@@ -250,7 +252,8 @@ class Context:
 
     # ---- synthetic inputs ----
     def synth_quant(self, dtype, rows, cols, seed):
-        buf = DevBuf(self, S.qbytes(dtype, rows, cols))
+        """Blocks of a generator code: a dtype, or Q4_K | SYNTH_Q4K_ZERO_MEAN."""
+        buf = DevBuf(self, S.qbytes(dtype & ~S.SYNTH_Q4K_ZERO_MEAN, rows, cols))
         self.check(lib.gq_hip_synth_quant(self.h, buf.ptr, dtype, rows, cols, seed), "synth_quant")
         return buf
 
@@ -259,9 +262,13 @@ class Context:
         self.check(lib.gq_hip_synth_normal(self.h, buf.ptr, n, seed), "synth_normal")
         return buf
 
-    def synth_norm_weight(self, n, seed):
+    def synth_norm_weight(self, n, seed, shift=0):
+        """(1 + N(0,1)/64) * 2^-shift; the power-of-two scale is applied on
+        the host (exact), like the oracle's."""
         buf = DevBuf(self, 4 * n)
         self.check(lib.gq_hip_synth_norm_weight(self.h, buf.ptr, n, seed), "synth_norm_weight")
+        if shift:
+            buf.upload(np.ldexp(buf.download(count=n), -shift).astype(np.float32))
         return buf
 
     # ---- ops ----
@@ -395,17 +402,17 @@ class DeviceModel:
             dts = s.dtypes(l)
             for k, field in names.items():
                 rows, cols = s.shape(k)
-                b = ctx.synth_quant(dts[k], rows, cols, tensor_seed(s.seed, l, S.SLOT[k]))
+                b = ctx.synth_quant(s.gen(dts[k]), rows, cols, tensor_seed(s.seed, l, S.SLOT[k]))
                 self.bufs.append(b)
                 setattr(layers[l], field, GqWeight(b.ptr, dts[k], rows, cols))
-            ra = ctx.synth_norm_weight(s.hidden, tensor_seed(s.seed, l, S.SLOT["rms_att"]))
-            rf = ctx.synth_norm_weight(s.hidden, tensor_seed(s.seed, l, S.SLOT["rms_ffn"]))
+            ra = ctx.synth_norm_weight(s.hidden, tensor_seed(s.seed, l, S.SLOT["rms_att"]), s.norm_shift)
+            rf = ctx.synth_norm_weight(s.hidden, tensor_seed(s.seed, l, S.SLOT["rms_ffn"]), s.norm_shift)
             self.bufs += [ra, rf]
             layers[l].rms_att, layers[l].rms_ffn = ra.ptr, rf.ptr
-        emb = ctx.synth_quant(s.embed_dtype, s.vocab, s.hidden, tensor_seed(s.seed, -1, S.SLOT["embed"]))
-        lm = ctx.synth_quant(s.lm_head_dtype, s.vocab, s.hidden,
+        emb = ctx.synth_quant(s.gen(s.embed_dtype), s.vocab, s.hidden, tensor_seed(s.seed, -1, S.SLOT["embed"]))
+        lm = ctx.synth_quant(s.gen(s.lm_head_dtype), s.vocab, s.hidden,
                              tensor_seed(s.seed, -1, S.SLOT["lm_head"]))
-        rfin = ctx.synth_norm_weight(s.hidden, tensor_seed(s.seed, -1, S.SLOT["rms_final"]))
+        rfin = ctx.synth_norm_weight(s.hidden, tensor_seed(s.seed, -1, S.SLOT["rms_final"]), s.norm_shift)
         self.bufs += [emb, lm, rfin]
         self.layers = layers
         self.model = GqModel(s.n_layers, s.hidden, s.ff, s.n_heads, s.n_kv_heads, s.head_dim, s.vocab,

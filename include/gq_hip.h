@@ -72,7 +72,11 @@ int gq_hip_d2h(gq_ctx *ctx, void *host, const void *dev, size_t bytes);
 /* ------------------------------------------------------- synthetic inputs
  * Device fill with the generator of csrc/gq_synth.h (bit-identical to the
  * host generator the parity oracle uses).  dtype Q4_K/Q6_K/Q8_0: rows x cols
- * blocks; normal: n fp32 ~ N(0,1); norm_weight: n fp32 1 + N(0,1)/64. */
+ * blocks; GQ_Q4_K | GQ_SYNTH_Q4K_ZERO_MEAN: Q4_K blocks whose sub-block mins
+ * cancel the scales' mean (m_j = sc_j, dmin = fp16(7.5 d)), so the weights
+ * are zero-mean; normal: n fp32 ~ N(0,1); norm_weight: n fp32
+ * 1 + N(0,1)/64. */
+#define GQ_SYNTH_Q4K_ZERO_MEAN 0x100
 int gq_hip_synth_quant(gq_ctx *ctx, void *dev, int dtype, int rows, int cols, uint64_t seed);
 int gq_hip_synth_normal(gq_ctx *ctx, float *dev, size_t n, uint64_t seed);
 int gq_hip_synth_norm_weight(gq_ctx *ctx, float *dev, size_t n, uint64_t seed);
@@ -174,8 +178,21 @@ typedef struct {
 } gq_model;
 
 /* Bind a model (after gq_hip_kv_init with matching geometry) and allocate
- * the decode workspace. */
+ * the decode workspace.  A layer whose seven weights and two norm weights
+ * are all NULL stays on the host (the --n-gpu-layers split, loader.c:677-728,
+ * or a projection the device does not take, such as F32); so may the
+ * embedding and the LM head (an F32 LM head stays on the host, as
+ * loader.c:575-585 allows).  The per-layer entry points (decode_layer,
+ * transformer_layer, qkv_rope) then serve the bound layers; the
+ * whole-model ones (forward_token, forward_sample, decode_loop, prefill,
+ * chat_turn, profile_step, time_op) need every layer, the embedding and the
+ * LM head on the device and return -1 otherwise. */
 int gq_hip_model_bind(gq_ctx *ctx, const gq_model *m);
+/* Layers the bound model holds on the device (0 when none is bound); *whole
+ * (may be NULL) is 1 when the whole-model entry points can run.  No
+ * reference counterpart: the engine's IS_GPU_READY test per layer
+ * (engine.c:324-328) asked once for the model. */
+int gq_hip_bound_layers(gq_ctx *ctx, int *whole);
 
 /* One decode layer on a device hidden vector (hidden -> hidden): RMSNorm,
  * QKV, RoPE + KV append, split-K GQA attention, o-proj + residual, RMSNorm,
@@ -332,7 +349,9 @@ int gq_hip_prefill_gate_up_dev(gq_ctx *ctx, int dtype, const void *w_gate, const
  * the cache. */
 int gq_hip_prefill_attention_dev(gq_ctx *ctx, int layer, int pos, int T, int n_heads, float *q,
                                  const float *k, const float *v, float *out);
-/* One turn of the chat REPL (chat_repl, chat.c:157-263) on the bound model,
+/* One turn of the chat REPL (chat_repl, chat.c:157-263) on the bound model
+ * (its prompt through gq_hip_prefill, so with the precision of the context's
+ * prefill mode: gq_hip_set_prefill_mode),
  * KV reused across turns: tokens (BOS first only on a conversation's first
  * turn, as chat.c:157-163 tokenizes) go through the prefill at
  * *current_pos; the reply is sampled until max_tokens, 512 tokens
@@ -357,6 +376,16 @@ int gq_hip_chat_turn(gq_ctx *ctx, const int32_t *tokens, int n_tokens, int *curr
  * negative error (-5: positions outside the cache). */
 int gq_hip_prefill(gq_ctx *ctx, const int32_t *tokens, int n_tokens, int pos, float *logits,
                    float *hidden_last, float *ms);
+/* How gq_hip_prefill (and gq_hip_chat_turn's prompt) runs a prompt on this
+ * context: 0 (default) the chunked matrix-core GEMM path above, whose
+ * products round x and the weights to bf16 (logits within ~5e-3 relative
+ * of an fp32 forward); 1 token by token through the fp32 decode step, the
+ * reference's own precision (forward() over T tokens equals T single-token
+ * steps up to fp32 rounding), at the decode step's speed per token.
+ * Returns the previous mode, or -1.  No reference counterpart: the
+ * reference has no prompt GEMM (linear_dispatch loops over tokens,
+ * engine.c:119-152). */
+int gq_hip_set_prefill_mode(gq_ctx *ctx, int mode);
 /* Device-to-device copy by a plain streaming kernel (bytes and both pointers
  * multiples of 16), asynchronous.  No reference counterpart: the known-size
  * workload that scales the HBM byte counters of the profiles. */

@@ -628,6 +628,7 @@ typedef struct {
   int nb_row;
   int kind;
   float *fout;
+  int zero_mean; /* Q4_K: the zero-mean rule (gq_q4k_zm_byte) */
 } synth_ctx;
 
 static void synth_rows(int r0, int r1, void *vctx) {
@@ -638,7 +639,8 @@ static void synth_rows(int r0, int r1, void *vctx) {
       uint64_t bi = (uint64_t)r * c->nb_row + b;
       uint8_t *o = c->out + bi * bb;
       for (int k = 0; k < bb; k++) {
-        o[k] = c->kind == ORC_Q4_K ? gq_q4k_byte(c->seed, bi, (uint32_t)k)
+        o[k] = c->kind == ORC_Q4_K ? (c->zero_mean ? gq_q4k_zm_byte(c->seed, bi, (uint32_t)k)
+                                                   : gq_q4k_byte(c->seed, bi, (uint32_t)k))
                : c->kind == ORC_Q6_K ? gq_q6k_byte(c->seed, bi, (uint32_t)k)
                                      : gq_q8_0_byte(c->seed, bi, (uint32_t)k);
       }
@@ -647,17 +649,22 @@ static void synth_rows(int r0, int r1, void *vctx) {
 }
 
 void orc_synth_q4k(uint64_t seed, int rows, int cols, uint8_t *out) {
-  synth_ctx c = {seed, out, cols / 256, ORC_Q4_K, NULL};
+  synth_ctx c = {seed, out, cols / 256, ORC_Q4_K, NULL, 0};
+  parallel_for(rows, 64, synth_rows, &c);
+}
+
+void orc_synth_q4k_zm(uint64_t seed, int rows, int cols, uint8_t *out) {
+  synth_ctx c = {seed, out, cols / 256, ORC_Q4_K, NULL, 1};
   parallel_for(rows, 64, synth_rows, &c);
 }
 
 void orc_synth_q6k(uint64_t seed, int rows, int cols, uint8_t *out) {
-  synth_ctx c = {seed, out, cols / 256, ORC_Q6_K, NULL};
+  synth_ctx c = {seed, out, cols / 256, ORC_Q6_K, NULL, 0};
   parallel_for(rows, 64, synth_rows, &c);
 }
 
 void orc_synth_q8_0(uint64_t seed, int rows, int cols, uint8_t *out) {
-  synth_ctx c = {seed, out, cols / 32, ORC_Q8_0, NULL};
+  synth_ctx c = {seed, out, cols / 32, ORC_Q8_0, NULL, 0};
   parallel_for(rows, 64, synth_rows, &c);
 }
 
@@ -668,7 +675,7 @@ static void normal_chunk(int c0, int c1, void *vctx) {
 }
 
 void orc_synth_normal(uint64_t seed, size_t n, float *out) {
-  synth_ctx c = {seed, NULL, (int)n, 0, out};
+  synth_ctx c = {seed, NULL, (int)n, 0, out, 0};
   if (n > 0x7fffffffULL) abort();
   parallel_for((int)((n + 4095) / 4096), 16, normal_chunk, &c);
 }

@@ -96,6 +96,7 @@ int orc_lctx_read(orc_kv *kv, const uint8_t *img, size_t size, int *current_pos,
 
 /* --- synthetic inputs (gq_synth.h) --- */
 void orc_synth_q4k(uint64_t seed, int rows, int cols, uint8_t *out);
+void orc_synth_q4k_zm(uint64_t seed, int rows, int cols, uint8_t *out); /* zero-mean rule */
 void orc_synth_q6k(uint64_t seed, int rows, int cols, uint8_t *out);
 void orc_synth_q8_0(uint64_t seed, int rows, int cols, uint8_t *out);
 void orc_synth_normal(uint64_t seed, size_t n, float *out);

@@ -22,6 +22,7 @@ ORACLE_SO = os.path.join(HERE, "liboracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libref.so")
 
 F32, Q8_0, Q4_K, Q6_K = 0, 2, 4, 5
+SYNTH_Q4K_ZERO_MEAN = 0x100  # gq_synth.h: the zero-mean Q4_K generator code
 _fp = C.POINTER(C.c_float)
 _u8p = C.POINTER(C.c_uint8)
 
@@ -87,7 +88,7 @@ class Oracle:
                                      _u8p, C.c_size_t]
         L.orc_lctx_read.argtypes = [C.POINTER(OrcKV), _u8p, C.c_size_t, C.POINTER(C.c_int),
                                     C.POINTER(C.c_int)]
-        for n in ("orc_synth_q4k", "orc_synth_q6k", "orc_synth_q8_0"):
+        for n in ("orc_synth_q4k", "orc_synth_q4k_zm", "orc_synth_q6k", "orc_synth_q8_0"):
             getattr(L, n).argtypes = [C.c_uint64, C.c_int, C.c_int, _u8p]
         L.orc_synth_normal.argtypes = [C.c_uint64, C.c_size_t, _fp]
         L.orc_synth_norm_weight.argtypes = [C.c_uint64, C.c_size_t, _fp]
@@ -110,10 +111,12 @@ class Oracle:
         return int(self.lib.orc_tensor_seed(model_seed, layer, slot))
 
     def synth_quant(self, dtype, seed, rows, cols):
-        qk, bb = {Q4_K: (256, 144), Q6_K: (256, 210), Q8_0: (32, 34)}[dtype]
+        """Blocks of a generator code: a dtype, or Q4_K | SYNTH_Q4K_ZERO_MEAN."""
+        zm = dtype == (Q4_K | SYNTH_Q4K_ZERO_MEAN)
+        qk, bb = {Q4_K: (256, 144), Q6_K: (256, 210), Q8_0: (32, 34)}[Q4_K if zm else dtype]
         out = np.empty(rows * (cols // qk) * bb, np.uint8)
-        fn = {Q4_K: self.lib.orc_synth_q4k, Q6_K: self.lib.orc_synth_q6k,
-              Q8_0: self.lib.orc_synth_q8_0}[dtype]
+        fn = self.lib.orc_synth_q4k_zm if zm else {Q4_K: self.lib.orc_synth_q4k, Q6_K: self.lib.orc_synth_q6k,
+                                                   Q8_0: self.lib.orc_synth_q8_0}[dtype]
         fn(seed, rows, cols, u8ptr(out))
         return out
 
@@ -122,10 +125,11 @@ class Oracle:
         self.lib.orc_synth_normal(seed, n, fptr(out))
         return out
 
-    def synth_norm_weight(self, seed, n):
+    def synth_norm_weight(self, seed, n, shift=0):
+        """(1 + N(0,1)/64) * 2^-shift, exact in fp32."""
         out = np.empty(n, np.float32)
         self.lib.orc_synth_norm_weight(seed, n, fptr(out))
-        return out
+        return np.ldexp(out, -shift).astype(np.float32) if shift else out
 
     # ---- kernels ----
     def matvec(self, dtype, w, rows, cols, x, nbytes=None):
@@ -198,7 +202,7 @@ class HostModel:
         keep = []
 
         def qt(dtype, seed, rows, cols):
-            data = orc.synth_quant(dtype, seed, rows, cols)
+            data = orc.synth_quant(s.gen(dtype), seed, rows, cols)
             keep.append(data)
             return data, OrcTensor(dtype, rows, cols, u8ptr(data), data.nbytes)
 
@@ -215,12 +219,12 @@ class HostModel:
                 data, t = qt(dts[k], orc.tensor_seed(s.seed, l, slot), rows, cols)
                 arrs[k][l] = t
                 self.layer_w[l][k] = (dts[k], data)
-            self.rms_att[l] = orc.synth_norm_weight(orc.tensor_seed(s.seed, l, 7), s.hidden)
-            self.rms_ffn[l] = orc.synth_norm_weight(orc.tensor_seed(s.seed, l, 8), s.hidden)
+            self.rms_att[l] = orc.synth_norm_weight(orc.tensor_seed(s.seed, l, 7), s.hidden, s.norm_shift)
+            self.rms_ffn[l] = orc.synth_norm_weight(orc.tensor_seed(s.seed, l, 8), s.hidden, s.norm_shift)
         self.embed, embed_t = qt(s.embed_dtype, orc.tensor_seed(s.seed, -1, 10), s.vocab, s.hidden)
         self.lm_head, lm_t = qt(s.lm_head_dtype, orc.tensor_seed(s.seed, -1, 11), s.vocab,
                                 s.hidden)
-        self.rms_final = orc.synth_norm_weight(orc.tensor_seed(s.seed, -1, 12), s.hidden)
+        self.rms_final = orc.synth_norm_weight(orc.tensor_seed(s.seed, -1, 12), s.hidden, s.norm_shift)
         att_p = (_fp * L)(*[fptr(a) for a in self.rms_att])
         ffn_p = (_fp * L)(*[fptr(a) for a in self.rms_ffn])
         self._keep = (keep, arrs, att_p, ffn_p)

@@ -12,13 +12,16 @@ What comes from where (the README next to this script says the same):
                       test_forward_bitexact_vs_reference: whole-step logits)
   kv_tiny.npz/.lctx   slabs after kv_cache_append (with wrap) and the file
                       kv_cache_save writes, from the reference
-  tinyllama_greedy.npz / tinyllama_q8_greedy.npz / llama8b_greedy.npz
+  tinyllama_greedy.npz / tinyllama_q8_greedy.npz / tinyllama_zm_greedy.npz /
+  llama8b_greedy.npz / llama8b_zm_greedy.npz
                       greedy tokens, top-2 logit margins and the 16 largest
                       logits (indices and values) of every step from the
                       reference's forward() + sample_greedy; per-layer hidden
-                      states at steps 0, 63 and 127 from the oracle, run in
-                      lock step (its logits are asserted bit-identical to the
-                      reference's at every step)
+                      states at steps 0, 63, 127 and the smallest-margin
+                      steps from the oracle, run in lock step (its logits are
+                      asserted bit-identical to the reference's at every
+                      step); at a few of those steps the same step in float64
+                      (fp64_forward.py) and the reference's distance from it
 Inputs are the deterministic generator of guanaco_amd/csrc/gq_synth.h
 (GENERATOR_VERSION below); each file records seeds and SHA-256 of weights.
 """
@@ -35,6 +38,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "oracle"))
+sys.path.insert(0, HERE)
 
 from guanaco_amd import spec as S  # noqa: E402
 from oracle import (Q4_K, Q6_K, Q8_0, F32, HostKV, HostModel, Oracle, Ref, RefModel,  # noqa: E402
@@ -123,7 +127,17 @@ def make_kv_tiny(orc, ref):
     log("kv_tiny: 20 appends, .lctx")
 
 
-def make_greedy(orc, ref, spec, max_seq, prefill, start, steps, hidden_steps, name, check_every=True):
+def make_greedy(orc, ref, spec, max_seq, prefill, start, steps, name, hidden_steps=(0, 63, 127), n_low=0,
+                extra=(), n_f64_low=0):
+    """128 greedy steps of the reference's forward() + sample_greedy with the
+    oracle in lock step (its logits asserted bit-identical at every step).
+    Per-layer hidden states are kept for `hidden_steps`, `extra` and the
+    n_low steps with the smallest top-2 margins.  For the n_f64_low
+    smallest-margin steps and `extra`, the step is also run in float64
+    (fp64_forward.py) on the reference's own cache, and the fixture records
+    the exact top-16 logits and hidden states and how far the reference's
+    fp32 result is from them."""
+    from fp64_forward import forward_step
     t0 = time.time()
     hm = HostModel(orc, spec, max_seq)
     kv = hm.new_kv()
@@ -131,36 +145,50 @@ def make_greedy(orc, ref, spec, max_seq, prefill, start, steps, hidden_steps, na
     rm = RefModel(ref, hm)
     rm.load_kv(kv)
     log(f"{name}: model built in {time.time() - t0:.0f}s")
-    toks, margins, hidden, top_idx, top_val = [], [], {}, [], []
+    toks, margins, hid_all, top_idx, top_val, inputs = [], [], [], [], [], []
     tok = start
     for i in range(steps):
         pos = prefill + i
+        inputs.append(tok)
         t_ref, logits = rm.forward(tok, pos)
         top2 = np.sort(logits)[-2:]
         margins.append(float(top2[1] - top2[0]))
         idx = np.argsort(logits, kind="stable")[::-1][:TOPK]
         top_idx.append(idx.astype(np.int32))
         top_val.append(logits[idx].astype(np.float32))
-        if check_every or i in hidden_steps or i == 0:
-            t_orc, l_orc, hid = hm.forward(kv, tok, pos, want_hidden=i in hidden_steps)
-            assert t_orc == t_ref and np.array_equal(l_orc.view(np.uint32), logits.view(np.uint32)), \
-                f"{name}: oracle and reference differ at step {i}"
-            if hid is not None:
-                hidden[i] = hid.copy()
+        t_orc, l_orc, hid = hm.forward(kv, tok, pos, want_hidden=True)
+        assert t_orc == t_ref and np.array_equal(l_orc.view(np.uint32), logits.view(np.uint32)), \
+            f"{name}: oracle and reference differ at step {i}"
+        hid_all.append(hid.copy())
         toks.append(t_ref)
         tok = t_ref
         if i % 16 == 0:
             log(f"{name}: step {i} token {t_ref} margin {margins[-1]:.4g} ({time.time() - t0:.0f}s)")
+    order = [int(i) for i in np.argsort(margins, kind="stable")]
+    keep_h = sorted(set(hidden_steps) | set(extra) | set(order[:n_low]))
+    f64_steps = sorted(set(extra) | set(order[:n_f64_low]))
     out = dict(generator_version=np.int64(GENERATOR_VERSION), model_seed=np.int64(spec.seed),
                start_token=np.int32(start), prefill=np.int32(prefill), max_seq=np.int32(max_seq),
                tokens=np.array(toks, np.int32), margins=np.array(margins, np.float32),
                top_idx=np.stack(top_idx), top_logits=np.stack(top_val),
                embed_sha256=np.array(sha(hm.embed)), lm_head_sha256=np.array(sha(hm.lm_head)))
-    for i, h in hidden.items():
-        out[f"hidden_step{i}"] = h
+    for i in keep_h:
+        out[f"hidden_step{i}"] = hid_all[i]
+    # every step reads cache rows 0..pos only, so the final cache serves them all
+    for i in f64_steps:
+        l64, h64 = forward_step(hm, kv, inputs[i], prefill + i)
+        out[f"f64_top_logits_step{i}"] = l64[top_idx[i]]
+        out[f"f64_hidden_step{i}"] = h64.astype(np.float32)
+        e_l = float(np.linalg.norm(top_val[i] - l64[top_idx[i]]) / np.linalg.norm(l64[top_idx[i]]))
+        e_h = max(float(np.linalg.norm(hid_all[i][l] - h64[l]) / np.linalg.norm(h64[l]))
+                  for l in range(spec.n_layers))
+        out[f"f64_ref_err_step{i}"] = np.array([e_l, e_h], np.float64)
+        log(f"{name}: step {i} (margin {margins[i]:.4g}) reference vs float64: top-16 logits {e_l:.3g}, "
+            f"hidden per layer {e_h:.3g} ({time.time() - t0:.0f}s)")
     np.savez(os.path.join(HERE, f"{name}.npz"), **out)
     rm.close()
-    log(f"{name}: {steps} steps in {time.time() - t0:.0f}s; tokens {toks[:8]}...; min margin {min(margins):.4g}")
+    log(f"{name}: {steps} steps in {time.time() - t0:.0f}s; {len(set(toks))} distinct tokens; "
+        f"min margin {min(margins):.4g}; hidden states at {keep_h}; float64 at {f64_steps}")
 
 
 def main():
@@ -179,11 +207,17 @@ def main():
     if not only or "kv" in only:
         make_kv_tiny(orc, ref)
     if not only or "tinyllama" in only:
-        make_greedy(orc, ref, S.TINYLLAMA, 640, 512, 1, 128, (0, 63, 127), "tinyllama_greedy")
+        make_greedy(orc, ref, S.TINYLLAMA, 640, 512, 1, 128, "tinyllama_greedy")
     if not only or "tinyllama_q8" in only:
-        make_greedy(orc, ref, S.TINYLLAMA_Q8, 640, 512, 1, 128, (0, 63, 127), "tinyllama_q8_greedy")
+        # step 86 has a near-tie of two attention positions at scores ~1e4
+        make_greedy(orc, ref, S.TINYLLAMA_Q8, 640, 512, 1, 128, "tinyllama_q8_greedy", n_low=4, extra=(86,),
+                    n_f64_low=1)
+    if not only or "tinyllama_zm" in only:
+        make_greedy(orc, ref, S.TINYLLAMA_ZM, 640, 512, 1, 128, "tinyllama_zm_greedy", n_low=8, n_f64_low=3)
     if (not only or "llama8b" in only) and not a.skip_8b:
-        make_greedy(orc, ref, S.LLAMA8B, 8320, 8192, 128000, 128, (0, 63, 127), "llama8b_greedy")
+        make_greedy(orc, ref, S.LLAMA8B, 8320, 8192, 128000, 128, "llama8b_greedy")
+    if (not only or "llama8b_zm" in only) and not a.skip_8b:
+        make_greedy(orc, ref, S.LLAMA8B_ZM, 8320, 8192, 128000, 128, "llama8b_zm_greedy", n_low=5, n_f64_low=1)
 
 
 if __name__ == "__main__":

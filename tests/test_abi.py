@@ -56,7 +56,8 @@ def test_reference_patch_applies_and_builds(tmp_path):
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
     names = sorted(set(re.findall(r"\b(hip_\w+|backend_hip_\w+)\s*\(", src)))
     assert {"hip_backend_upload", "hip_backend_bind_model", "hip_backend_prefill", "hip_layer_ready",
-            "hip_backend_layer", "hip_backend_kv_sync", "hip_upload_weight"} <= set(names)
+            "hip_backend_layer", "hip_backend_kv_sync", "hip_upload_weight", "hip_backend_whole",
+            "hip_backend_prompt", "hip_backend_forward_sample", "hip_backend_host_kv"} <= set(names)
     lib = ctypes.CDLL(str(out / "libref_hip.so"))
     missing = [n for n in names + ["backend_create", "backend_kernels", "backend_destroy", "backend_hip_create",
                                    "forward", "transformer_layer", "gpu_prefill", "kv_cache_load"]

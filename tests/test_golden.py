@@ -73,11 +73,14 @@ def test_kv_and_lctx_golden(orc):
     assert np.array_equal(img, np.fromfile(os.path.join(GOLD, "kv_tiny.lctx"), np.uint8))
 
 
-def test_tinyllama_first_steps_golden(orc):
-    """Two decode steps of the TinyLlama-shape model: tokens equal the
-    reference's, per-layer hidden states at step 0 bit for bit."""
-    g = load("tinyllama_greedy.npz")
-    s = S.TINYLLAMA
+@pytest.mark.parametrize("name,spec", [("tinyllama_greedy.npz", S.TINYLLAMA),
+                                       ("tinyllama_zm_greedy.npz", S.TINYLLAMA_ZM)])
+def test_tinyllama_first_steps_golden(orc, name, spec):
+    """Two decode steps of the TinyLlama-shape models (the plain Q4_K
+    generator and the zero-mean one): tokens equal the reference's, per-layer
+    hidden states at step 0 bit for bit."""
+    g = load(name)
+    s = spec
     hm = HostModel(orc, s, int(g["max_seq"]))
     assert hashlib.sha256(hm.lm_head.tobytes()).hexdigest() == str(g["lm_head_sha256"])
     kv = hm.new_kv()
@@ -89,3 +92,41 @@ def test_tinyllama_first_steps_golden(orc):
         assert tok == int(g["tokens"][i])
         if i == 0:
             assert np.array_equal(bits(hid), bits(g["hidden_step0"]))
+
+
+def test_fp64_step_agrees_with_oracle_where_well_conditioned(orc):
+    """The float64 step of tests/golden/fp64_forward.py against the fp32
+    oracle on the tiny model: ~1e-6 apart, so it computes the same function
+    (a dropped term, a wrong index or sign would show as O(1))."""
+    from fp64_forward import forward_step
+    s, ms, pre = S.TINY_ZM, 64, 24
+    hm = HostModel(orc, s, ms)
+    kv = hm.new_kv()
+    kv.prefill(orc, s, pre)
+    tok = 11
+    for i in range(3):
+        l64, h64 = forward_step(hm, kv, tok, pre + i)
+        tok, l32, h32 = hm.forward(kv, tok, pre + i, want_hidden=True)
+        assert np.linalg.norm(l32 - l64) / np.linalg.norm(l64) < 1e-5
+        for l in range(s.n_layers):
+            assert np.linalg.norm(h32[l] - h64[l]) / np.linalg.norm(h64[l]) < 1e-5
+        assert int(np.argmax(l64)) == tok
+
+
+def test_zero_mean_q4k_generator(orc):
+    """gq_q4k_zm_byte: every sub-block's min equals its scale and dmin is
+    fp16(7.5 d), so each row of weights sums to about zero (the plain
+    generator's rows sum to ~5 per weight)."""
+    from util import dequant_q4k_f64
+    zm = orc.synth_quant(S.Q4_K | S.SYNTH_Q4K_ZERO_MEAN, 3, 256, 1024)
+    blk = zm.reshape(256, 4, 144)
+    d = blk[..., 0:2].copy().view(np.float16)[..., 0].astype(np.float64)
+    dmin = blk[..., 2:4].copy().view(np.float16)[..., 0].astype(np.float64)
+    assert np.array_equal(dmin, (7.5 * d).astype(np.float16).astype(np.float64))
+    w = dequant_q4k_f64(zm, 256, 1024)
+    w0 = dequant_q4k_f64(orc.synth_quant(S.Q4_K, 3, 256, 1024), 256, 1024)
+    assert abs(w.mean()) < 0.05 * w.std() and w0.mean() > 0.5 * w0.std()
+    # the scales unpack (get_scale_min_k4) to sc_j == m_j: the mean of each
+    # 32-weight sub-block is d*sc*(mean(q) - 7.5), zero in expectation
+    sub = w.reshape(256, 4, 8, 32)
+    assert np.abs(sub.mean(axis=(0, 3))).max() < 0.1 * w.std()

@@ -4,8 +4,11 @@ reference (tests/golden/make_golden.py): matvec y, attention, KV slabs and
 greedy tokens for 128 steps and per-layer hidden states within 1e-3
 relative L2 — for the TinyLlama-shape (config 2) and Llama-3.1-8B-shape
 (config 3, KV filled to 8192) models, plus the 16 largest logits of every
-step, and a TinyLlama-shape variant with all weights Q8_0 whose tokens vary
-from step to step."""
+step within 1e-3.  Besides the plain models (whose Q4_K generator makes the
+token sequences degenerate) there are variants whose tokens vary from step
+to step: all weights Q8_0, and the Q4_K_M mix with zero-mean Q4_K weights,
+run on every matvec kernel path.  Ill-conditioned steps are also held to a
+float64 evaluation of the step."""
 import os
 
 import numpy as np
@@ -20,16 +23,22 @@ GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 DT = {"q4_k": S.Q4_K, "q6_k": S.Q6_K, "q8_0": S.Q8_0}
 MV_TOL = 1e-5     # per matvec (a correct kernel differs from the CPU order by ~1e-7)
 LAYER_TOL = 1e-3  # per layer
-# the 16 largest logits of each step: the median step within LOGIT_TOL
-# (observed ~1e-6), every step within LOGIT_MAX.  The Q8_0 model's q and k
-# entries are ~80, so its attention scores reach ~1e4, where one fp32 ulp is
-# ~1e-3: at a near-tie between two positions (step 86: a top-2 gap of 0.17
-# in a layer-0 head, scores of standard deviation ~3900) the GPU's and the
-# CPU's summation orders move ~1e-3 of softmax weight between them, and that
-# step's logits differ by 1.2e-3 with the same greedy token.  Steps without
-# such a tie stay at ~1e-6.
+# The 16 largest logits of each step: the median step within LOGIT_TOL
+# (observed ~1e-6), every step within LOGIT_MAX of the reference.
 LOGIT_TOL = 1e-5
-LOGIT_MAX = 5e-3
+LOGIT_MAX = 1e-3
+# Steps where the reference's own fp32 result is F64_FLAG or more from the
+# float64 evaluation of the same step (fp64_forward.py, recorded in the
+# fixture) are ill conditioned, and there the device is held to the exact
+# values as well, within F64_FACTOR times the reference's own distance.  The
+# Q8_0 model's step 86 is one: its q and k entries reach ~80, so attention
+# scores reach ~1e4, and a near-tie of two positions in a layer-0 head puts
+# the reference 2.3e-4 (top-16 logits) and 6.8e-4 (hidden) from exact against
+# ~2e-6 at its other steps.  The device lands as close (and 1e-6 from the
+# reference) since its Q8_0 dot sums q*x on sign-extended quants; summing
+# (q + 128)*x and subtracting 128*sum(x) put it 1.4e-3 / 4.4e-3 from exact.
+F64_FLAG = 1e-4
+F64_FACTOR = 2.0
 
 
 def load(name):
@@ -109,12 +118,16 @@ def test_kv_append_and_lctx_vs_reference(tmp_path):
         c.close()
 
 
-def run_greedy(spec, g):
-    """Greedy decode on the device from the fixture's start, two ways:
-    eager forward_token steps, each step's 16 largest reference logits
-    compared (LOGIT_TOL) and the per-layer hidden states at every step the
-    fixture holds (LAYER_TOL); then the graph-replayed decode loop.  Both
-    must produce the reference's tokens at every step."""
+def run_greedy(spec, g, paths=("auto",)):
+    """Greedy decode on the device from the fixture's start.  For each matvec
+    kernel path in `paths`: eager forward_token steps, each step's 16
+    largest reference logits compared (LOGIT_TOL / LOGIT_MAX) and the
+    per-layer hidden states at every step the fixture holds (LAYER_TOL);
+    where the fixture holds a float64 evaluation of a step that the
+    reference itself misses by F64_FLAG or more, the device is compared
+    with the float64 values too.  Then the graph-replayed decode loop on the
+    default path.  Every run must produce the reference's tokens at every
+    step."""
     import guanaco_amd.hip as H
     from guanaco_amd.synth import tensor_seed
     c = H.Context(0)
@@ -124,31 +137,49 @@ def run_greedy(spec, g):
         seeds = (tensor_seed(spec.seed, -1, 13), tensor_seed(spec.seed, -1, 14))
         tokens, top_idx, top_val = g["tokens"], g["top_idx"], g["top_logits"]
         hsteps = {int(k[len("hidden_step"):]) for k in g.files if k.startswith("hidden_step")}
-        n, tok = len(tokens), int(g["start_token"])
-        worst_h = worst_l = 0.0
-        el, eh = [], {}
-        for i in range(n):
-            t, logits, hid = dm.forward(tok, pre + i, want_hidden=i in hsteps)
-            el.append(rel_l2(logits[top_idx[i]], top_val[i]))
-            worst_l = max(worst_l, el[-1])
-            if hid is not None:
-                eh[i] = [rel_l2(hid[l], g[f"hidden_step{i}"][l]) for l in range(spec.n_layers)]
-                worst_h = max(worst_h, max(eh[i]))
-            assert t == int(tokens[i]), f"eager step {i}: token {t} vs {int(tokens[i])} (margin {g['margins'][i]:.3g})"
-            tok = t
-        print(f"{spec.name}: top-16 logits rel L2 per step: max {max(el):.3g} at step {int(np.argmax(el))}, "
-              f"median {float(np.median(el)):.3g}, steps 0-7 {[f'{e:.2g}' for e in el[:8]]}")
-        for i, e in sorted(eh.items()):
-            print(f"  hidden step {i}: per-layer rel L2 {[f'{x:.2g}' for x in e]}")
-        assert float(np.median(el)) < LOGIT_TOL and worst_l < LOGIT_MAX, (float(np.median(el)), worst_l)
-        assert worst_h < LAYER_TOL, worst_h
+        f64 = {int(k[len("f64_ref_err_step"):]): g[k] for k in g.files if k.startswith("f64_ref_err_step")}
+        flagged = {i for i, e in f64.items() if e[0] >= F64_FLAG or e[1] >= F64_FLAG}
+        n = len(tokens)
+        for path in paths:
+            c.kv_prefill_synth(*seeds, pre)
+            tok = int(g["start_token"])
+            worst_h = worst_l = 0.0
+            el, eh = [], {}
+            with H.matvec_path(path):
+                for i in range(n):
+                    t, logits, hid = dm.forward(tok, pre + i, want_hidden=i in hsteps or i in f64)
+                    got = logits[top_idx[i]]
+                    el.append(rel_l2(got, top_val[i]))
+                    if i in f64:
+                        e_l = rel_l2(got, g[f"f64_top_logits_step{i}"])
+                        e_h = max(rel_l2(hid[l], g[f"f64_hidden_step{i}"][l]) for l in range(spec.n_layers))
+                        print(f"  {path} step {i} (margin {float(g['margins'][i]):.3g}): float64 distance of the "
+                              f"device {e_l:.3g} / {e_h:.3g}, of the reference {f64[i][0]:.3g} / {f64[i][1]:.3g} "
+                              f"(top-16 logits / hidden); device vs reference {el[-1]:.3g}")
+                    if i in flagged:
+                        assert e_l <= max(LOGIT_MAX, F64_FACTOR * f64[i][0]), (path, i, e_l, f64[i])
+                        assert e_h <= max(LAYER_TOL, F64_FACTOR * f64[i][1]), (path, i, e_h, f64[i])
+                    worst_l = max(worst_l, el[-1])
+                    if i in hsteps:
+                        eh[i] = [rel_l2(hid[l], g[f"hidden_step{i}"][l]) for l in range(spec.n_layers)]
+                        worst_h = max(worst_h, max(eh[i]))
+                    assert t == int(tokens[i]), \
+                        f"{path} eager step {i}: token {t} vs {int(tokens[i])} (margin {g['margins'][i]:.3g})"
+                    tok = t
+            print(f"{spec.name} [{path}]: top-16 logits rel L2 per step: max {max(el):.3g} at step "
+                  f"{int(np.argmax(el))}, median {float(np.median(el)):.3g}; hidden states at the recorded steps "
+                  f"worst {worst_h:.3g}; ill-conditioned steps checked against float64: {sorted(flagged)}")
+            for i, e in sorted(eh.items()):
+                print(f"  hidden step {i}: per-layer rel L2 max {max(e):.2g}")
+            assert float(np.median(el)) < LOGIT_TOL and worst_l < LOGIT_MAX, (path, float(np.median(el)), worst_l)
+            assert worst_h < LAYER_TOL, (path, worst_h)
         c.kv_prefill_synth(*seeds, pre)
         toks, _ = dm.decode_loop(int(g["start_token"]), pre, n, use_graph=True)
         mism = [i for i in range(n) if toks[i] != tokens[i]]
         assert not mism, f"graph: first mismatch at step {mism[0]}: {toks[mism[0]]} vs {tokens[mism[0]]}"
-        print(f"{spec.name}: {n} tokens identical ({len(set(tokens.tolist()))} distinct, min margin "
-              f"{float(g['margins'].min()):.3g}); top-16 logits worst rel L2 {worst_l:.3g}; hidden states "
-              f"at steps {sorted(hsteps)} worst per-layer rel L2 {worst_h:.3g}")
+        print(f"{spec.name}: {n} tokens identical on {', '.join(paths)} and in the graph loop "
+              f"({len(set(tokens.tolist()))} distinct, min margin {float(g['margins'].min()):.3g}); hidden "
+              f"states at steps {sorted(hsteps)}")
     finally:
         c.close()
 
@@ -165,3 +196,16 @@ def test_tinyllama_q8_0_128_greedy_steps_vs_reference():
 
 def test_llama8b_128_greedy_steps_vs_reference():
     run_greedy(S.LLAMA8B, load("llama8b_greedy.npz"))
+
+
+def test_tinyllama_zero_mean_q4_k_m_greedy_all_paths():
+    """The TinyLlama shape with zero-mean Q4_K weights (Q4_K_M mix): tokens
+    differ at nearly every step, so they discriminate on the Q4_K / Q6_K
+    kernels; run on the vector-ALU, default and matrix-core matvec paths."""
+    run_greedy(S.TINYLLAMA_ZM, load("tinyllama_zm_greedy.npz"), paths=("auto", "mfma", "valu"))
+
+
+def test_llama8b_zero_mean_q4_k_m_greedy_all_paths():
+    """The benchmark's 8B Q4_K_M shape (KV at 8192) with zero-mean Q4_K
+    weights, on the default and matrix-core matvec paths."""
+    run_greedy(S.LLAMA8B_ZM, load("llama8b_zm_greedy.npz"), paths=("auto", "mfma"))

@@ -129,6 +129,25 @@ def test_argmax_first_max(ctx):
     assert ctx.argmax_dev(ctx.upload(x), x.size) == 0
 
 
+def test_argmax_nan(ctx, orc):
+    """NaN logits as sample_greedy (tokenizer.c:175-185) treats them: a NaN at
+    index 0 is never replaced (no value compares greater), a NaN anywhere
+    else is never taken.  Checked against the oracle's restatement of that
+    scan, which test_oracle pins against the compiled reference."""
+    base = np.random.default_rng(1).standard_normal(128256).astype(np.float32)
+    base[70000] = 40.0
+    cases = []
+    x = base.copy(); x[0] = np.nan; cases.append((x, 0))
+    x = base.copy(); x[0] = np.nan; x[9] = np.inf; cases.append((x, 0))
+    x = base.copy(); x[5000] = np.nan; cases.append((x, 70000))
+    x = base.copy(); x[70000] = np.nan; x[[3, 99999]] = 39.0; cases.append((x, 3))
+    x = base.copy(); x[1:] = np.nan; cases.append((x, 0))
+    x = np.full(128256, np.nan, np.float32); x[64000] = -1.0; cases.append((x, 0))
+    for x, want in cases:
+        assert orc.argmax(x) == want
+        assert ctx.argmax_dev(ctx.upload(x), x.size) == want
+
+
 def test_silu_mul(ctx, orc):
     n = 14336
     g = orc.synth_normal(1, n) * np.float32(4)

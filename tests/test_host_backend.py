@@ -192,6 +192,7 @@ def test_bind_model_and_gpu_prefill_slot(host, ref, orc):
     for l in range(spec.n_layers):
         for f in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down"):
             assert host.hip_backend_upload(b, getattr(gpu.mw.layers[l], f)) == 0
+    assert host.hip_backend_upload(b, gpu.mw.lm_head) == 0  # the loader's upload with any device layer
     assert host.hip_backend_bind_model(b, C.byref(gpu.mw), gpu.kv) == 0
     toks = np.random.default_rng(7).integers(0, spec.vocab, n).astype(np.int32)
     prompt = (C.c_int * (n - 1))(*[int(t) for t in toks[:-1]])

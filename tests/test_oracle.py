@@ -144,6 +144,28 @@ def test_greedy_first_max(orc):
     assert orc.argmax(np.array([3, 1, 3, 2], np.float32)) == 0
 
 
+def test_greedy_nan_vs_reference(orc, ref):
+    """NaN logits: the oracle's scan picks what the compiled sample_greedy
+    (tokenizer.c:175-185) picks — index 0 when logits[0] is NaN, and a NaN
+    anywhere else skipped."""
+    import ctypes as C
+    ref.lib.sample_greedy.argtypes = [C.POINTER(C.c_float), C.c_int]
+    ref.lib.sample_greedy.restype = C.c_int
+    base = np.random.default_rng(1).standard_normal(4096).astype(np.float32)
+    base[3000] = 40.0
+    xs = []
+    for idx, val in ((0, np.nan), (5, np.nan), (3000, np.nan), (0, np.inf)):
+        x = base.copy()
+        x[idx] = val
+        xs.append(x)
+    x = base.copy(); x[0] = np.nan; x[7] = np.inf; xs.append(x)
+    xs.append(np.full(64, np.nan, np.float32))
+    for x in xs:
+        got = ref.lib.sample_greedy(x.ctypes.data_as(C.POINTER(C.c_float)), x.size)
+        assert orc.argmax(x) == got
+    assert orc.argmax(xs[0]) == 0 and orc.argmax(xs[1]) == 3000
+
+
 def test_rope_closed_form(orc):
     """Adjacent-pair rotation by pos * theta^(-i/hd) (kernels_cpu.c:391-431)."""
     hd, theta = 128, 500000.0
