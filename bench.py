@@ -23,8 +23,9 @@ and the copy-kernel scaling).
 cpu_baseline = the reference's own CPU forward() (oracle/_ref/libref.so, or
 the oracle's C restatement when that build is absent) on this host: the
 median of 5 timed greedy tokens at nproc threads (the headline) and at 8,
-plus the reference's Q4_K and Q6_K matvec GB/s on the down-projection shape
-(median of 5 each).
+plus the reference's Q4_K, Q6_K and Q8_0 matvec GB/s on the down-projection
+shape (median over a rotation of ~1.5 GB of distinct matrices per dtype, so
+every call reads DRAM), and what lscpu and /proc/meminfo say of the host.
 """
 import argparse
 import json
@@ -86,6 +87,41 @@ def cpu_model():
     return None
 
 
+def host_info():
+    """What the host tells about its CPUs and memory (lscpu, /proc/meminfo,
+    the NUMA nodes and the last-level cache): no root is needed for any of it."""
+    import subprocess
+    info = {"cpu": cpu_model()}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        want = ("Model name", "Socket(s)", "Core(s) per socket", "Thread(s) per core", "CPU(s)",
+                "NUMA node(s)", "L3 cache", "CPU max MHz")
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() in want:
+                info[k.strip()] = v.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        with open("/proc/meminfo") as f:
+            for line in f:
+                if line.startswith("MemTotal"):
+                    info["MemTotal"] = line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    try:
+        info["numa_nodes"] = len([d for d in os.listdir("/sys/devices/system/node") if d.startswith("node")])
+    except OSError:
+        pass
+    try:
+        with open("/sys/devices/system/cpu/cpu0/cache/index3/size") as f:
+            info["L3_per_cpu0_domain"] = f.read().strip()
+    except OSError:
+        pass
+    info["affinity_cpus"] = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None
+    return info
+
+
 def cpu_baseline(spec, n_tok=5):
     """The reference's CPU forward() on the 8B shape at pos 8192: n_tok timed
     greedy tokens (after one untimed) at nproc threads and at 8, and its
@@ -104,7 +140,14 @@ def cpu_baseline(spec, n_tok=5):
     kind = "reference" if ref_available() else "port"
     rows, cols = spec.hidden, spec.ff
     x = orc.synth_normal(7, cols)
-    mats = {dt: orc.synth_quant(dt, 99, rows, cols) for dt in (S.Q4_K, S.Q6_K)}
+    # matvec inputs rotated over ~1.5 GB per dtype, far past any host's L3,
+    # so each call streams its weights from DRAM
+    mats = {}
+    for dt in (S.Q4_K, S.Q6_K, S.Q8_0):
+        n = max(2, int(1.5e9 // S.qbytes(dt, rows, cols)))
+        mats[dt] = [orc.synth_quant(dt, 99 + i, rows, cols) for i in range(n)]
+    log(f"cpu baseline: {sum(len(v) for v in mats.values())} matvec inputs in "
+        f"{sum(w.nbytes for v in mats.values() for w in v) / 1e9:.1f} GB")
     runs = {}
     for threads in sorted({nproc, 8}, reverse=True):
         if kind == "reference":
@@ -125,14 +168,13 @@ def cpu_baseline(spec, n_tok=5):
             tok = step(tok, CTX + 1 + n)
             dts.append(time.perf_counter() - t1)
         gbs = {}
-        for dt, w in mats.items():
-            mv(dt, w, rows, cols, x)
+        for dt, ws in mats.items():
             ts = []
-            for _ in range(5):
+            for w in ws:  # each call on a matrix the previous ones evicted from the caches
                 t1 = time.perf_counter()
                 mv(dt, w, rows, cols, x)
                 ts.append(time.perf_counter() - t1)
-            gbs[S.DTYPE_NAME[dt]] = round((w.nbytes + 4 * (rows + cols)) / statistics.median(ts) / 1e9, 2)
+            gbs[S.DTYPE_NAME[dt]] = round((ws[0].nbytes + 4 * (rows + cols)) / statistics.median(ts) / 1e9, 2)
         runs[threads] = {"tok_s": round(1.0 / statistics.median(dts), 4),
                          "tok_s_each": [round(1.0 / d, 4) for d in dts],
                          "matvec_GB_per_s": gbs}
@@ -141,14 +183,15 @@ def cpu_baseline(spec, n_tok=5):
             rm.close()
     head = runs[nproc]
     return {"value": head["tok_s"], "unit": "tok/s", "cores": nproc, "kind": kind,
-            "cpu": cpu_model(), "nproc": nproc,
+            "cpu": cpu_model(), "nproc": nproc, "host": host_info(),
             "runs": {str(k): v for k, v in runs.items()},
             "sample": f"median of {n_tok} greedy decode tokens (after one untimed) of the same 8B-shape "
                       f"Q4_K_M model at positions {CTX + 1}..{CTX + n_tok} through the reference CPU "
                       f"forward() ({'compiled reference' if kind == 'reference' else 'C restatement'}), "
                       f"at nproc = {nproc} threads (value) and at 8 (runs); Q6_K and Q8_0 matvecs are "
-                      f"single-threaded in the reference.  matvec_GB_per_s: the reference's Q4_K and "
-                      f"Q6_K matvec on {rows} x {cols}, median of 5"}
+                      f"single-threaded in the reference.  matvec_GB_per_s: the reference's Q4_K, Q6_K and "
+                      f"Q8_0 matvec on {rows} x {cols}, the median over a rotation of ~1.5 GB of distinct "
+                      f"matrices per dtype (each call from DRAM, not the L3)"}
 
 
 def main():

@@ -36,6 +36,8 @@ typedef struct {
   /* device cache rows [dirty_lo, dirty_hi) written by whole-model steps and
    * not yet in the host cache */
   int dirty_lo, dirty_hi;
+  int device;
+  size_t free0; /* free HBM when the backend was made (before any upload) */
 } HipImpl;
 
 static HipImpl *g_hip; /* the live HIP backend (see the file comment) */
@@ -122,6 +124,9 @@ static Backend *hip_create(const BackendConfig *cfg) {
   }
   impl->ctx = ctx;
   impl->cpu = cpu;
+  impl->device = cfg->device_id;
+  size_t total = 0;
+  if (gq_hip_mem_info(cfg->device_id, &impl->free0, &total)) impl->free0 = 0;
   /* GQ_HIP_PREFILL=steps: prompts token by token through the fp32 decode
    * step (the reference's precision) instead of the bf16 matrix-core GEMM */
   const char *pm = getenv("GQ_HIP_PREFILL");
@@ -307,9 +312,13 @@ static int bind_model(Backend *b, ModelWeights *mw, KVCache *kv) {
   int whole = 0;
   const int n_dev = gq_hip_bound_layers(ctx, &whole);
   const Tensor *lm = mw->lm_head;
-  fprintf(stderr, "[hip] %d of %d layers on the device, LM head on the %s; %s\n", n_dev, c->n_layers,
-          lm && lm->device_residency == 1 && lm->d_data ? "device" : "host",
-          whole ? "prompts and decode steps run whole on the device" : "forward() runs, device layers through the layer hook");
+  size_t free1 = 0, total = 0;
+  const double used = !gq_hip_mem_info(impl->device, &free1, &total) && impl->free0 >= free1
+                          ? (double)(impl->free0 - free1) / 1e9 : -1.0;
+  fprintf(stderr, "[hip] %d of %d layers on the device, LM head on the %s; %s; %.2f GB of HBM in use\n", n_dev,
+          c->n_layers, lm && lm->device_residency == 1 && lm->d_data ? "device" : "host",
+          whole ? "prompts and decode steps run whole on the device" : "forward() runs, device layers through the layer hook",
+          used);
   /* the host cache may already hold a prefix (a restored session) */
   const int hs = kv_cache_head_stride(kv);
   for (int l = 0; l < c->n_layers; l++)
