@@ -252,8 +252,8 @@ int gq_launch_copy(void *dst, const void *src, size_t bytes, int n_cu, hipStream
 
 /* ---- prefill chunk ---------------------------------------------------
  * Y[T][rows] = X[T][K] . W^T on the bf16 matrix cores for up to three weight
- * segments in one launch (each rows % 128 == 0, Q4_K, or Q6_K with
- * K % 512 == 0), X bf16 row-major.  MV_STORE writes y, MV_RESID adds into
+ * segments in one launch (each rows % 128 == 0, Q4_K, Q8_0, or Q6_K with
+ * K % 512 == 0; K % 256 == 0), X bf16 row-major.  MV_STORE writes y, MV_RESID adds into
  * y; MV_SWIGLU takes gate (seg 0) and up (seg 1) of equal rows
  * (rows % 64 == 0) and writes act[T][rows] = bf16(silu(gate) * up). */
 struct PgSeg {

@@ -6,7 +6,8 @@
  * The reference computes a prefill projection as T sequential matvecs
  * (linear_dispatch, engine.c:119-152).  Here Y[T][N] = X[T][K] . W^T for
  * all T tokens in one launch, where W is N rows of Q4_K blocks
- * (quant_matvec_q4_k.c:9-16) or Q6_K blocks (quant_matvec_q6_k.c:5-12) and
+ * (quant_matvec_q4_k.c:9-16), Q6_K blocks (quant_matvec_q6_k.c:5-12) or Q8_0
+ * blocks (quant_matvec_q8_0.c:5-10) and
  * X is bf16 row-major (its producer rounds it: RMSNorm, the attention merge,
  * the gate/up epilogue, or the fp32 -> bf16 pass of the op-level entry).
  *
@@ -306,6 +307,78 @@ struct PW<GQ_Q6_KP> {
   }
 };
 
+/* Q8_0 (quant_matvec_q8_0.c:5-10): 34-byte blocks of an fp16 d and 32 int8
+ * quants, w = d q (exact in fp32: 11 x 8 significant bits).  A 64-weight
+ * step is two whole blocks, 68 bytes, and rows of K % 64 == 0 weights are
+ * 68 K / 64 bytes, so every step starts on a dword: per row and step the 17
+ * dwords land in LDS as they are (nine dword DMA instructions per wave, 544
+ * of 576 lanes used).  Lane (r, h) reads quants 16 kk + 8 h .. + 7 of the
+ * step, 2-byte aligned, as three dwords and a funnel shift. */
+template <>
+struct PW<GQ_Q8_0> {
+  static constexpr int kRowLds = 68;
+  static constexpr int kWaveLds = 9 * 256;
+  static constexpr int kDma = 9;
+  struct Plan {
+    uint32_t off[9]; /* row * rowbytes + 4 * dword of the row's step */
+    bool on[9];
+  };
+  __device__ static void plan(Plan &p, int lane, uint32_t rowbytes) {
+#pragma unroll
+    for (int i = 0; i < 9; i++) {
+      const int dw = 64 * i + lane, row = dw / 17, w = dw - 17 * row;
+      p.on[i] = dw < 32 * 17;
+      p.off[i] = (uint32_t)row * rowbytes + 4u * (uint32_t)w;
+    }
+  }
+  __device__ static void issue(const Plan &p, const uint8_t *w, int s, uint32_t lds) {
+#pragma unroll
+    for (int i = 0; i < 9; i++) {
+      const uint32_t d = __builtin_amdgcn_readfirstlane(lds + 256u * i);
+      if (p.on[i]) dma4(w + (size_t)68 * s + p.off[i], d);
+    }
+  }
+  struct Raw {
+    uint2 q[4];
+    uint32_t d0, d1;
+  };
+  __device__ static void read(Raw &w, const GQ_LDS uint8_t *ws, int lane, int) {
+    const uint32_t r = (uint32_t)(lane & 31), h = (uint32_t)(lane >> 5), base = r * kRowLds + 8u * h;
+    /* block kk / 2, quants 16 (kk & 1) + 8 h .. after the block's 2-byte d:
+     * bytes 2 + 16 kk + 8 h of block 0 (2 mod 4), 36 + 16 (kk - 2) + 8 h of
+     * block 1 (dword aligned) */
+#pragma unroll
+    for (int kk = 0; kk < 2; kk++) {
+      const uint32_t a = base + 16u * (uint32_t)kk;
+      const uint32_t w0 = lld<uint32_t>(ws, a), w1 = lld<uint32_t>(ws, a + 4u), w2 = lld<uint32_t>(ws, a + 8u);
+      w.q[kk] = make_uint2(__builtin_amdgcn_alignbyte(w1, w0, 2), __builtin_amdgcn_alignbyte(w2, w1, 2));
+      w.q[kk + 2] = make_uint2(lld<uint32_t>(ws, a + 36u), lld<uint32_t>(ws, a + 40u));
+    }
+    w.d0 = lld<uint32_t>(ws, r * kRowLds);
+    w.d1 = lld<uint32_t>(ws, r * kRowLds + 32u) >> 16;
+  }
+  /* d q as d (q + 128) - 128 d in one fma: both products exact, so the
+   * result is d q exactly, then bf16 */
+  __device__ static void dequant(const Raw &rw, int, gq_bf16x8 b[4]) {
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+      const float d = gq_h2f(kk < 2 ? rw.d0 : rw.d1), m = -128.0f * d;
+      const uint32_t pw[2] = {rw.q[kk].x ^ 0x80808080u, rw.q[kk].y ^ 0x80808080u};
+      uint32_t o[4];
+#pragma unroll
+      for (int k = 0; k < 2; k++) {
+        const float v0 = __builtin_fmaf(d, (float)(pw[k] & 0xffu), m);
+        const float v1 = __builtin_fmaf(d, (float)((pw[k] >> 8) & 0xffu), m);
+        const float v2 = __builtin_fmaf(d, (float)((pw[k] >> 16) & 0xffu), m);
+        const float v3 = __builtin_fmaf(d, (float)(pw[k] >> 24), m);
+        o[2 * k] = pack_bf16x2(v0, v1);
+        o[2 * k + 1] = pack_bf16x2(v2, v3);
+      }
+      b[kk] = __builtin_bit_cast(gq_bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
+    }
+  }
+};
+
 /* One thread per (row, step): a Q6_K row in the reference layout (src) to the
  * step layout above (dst, same size). */
 __global__ __launch_bounds__(256) void q6k_steps_kernel(const uint8_t *src, uint8_t *dst, int rows, int nb) {
@@ -365,7 +438,8 @@ constexpr bool fits() {
 }
 static_assert(fits<GQ_Q4_K, 1, 2>() && fits<GQ_Q4_K, 2, 2>() && fits<GQ_Q6_K, 1, 2>() && fits<GQ_Q6_K, 2, 2>() &&
                   fits<GQ_Q6_KP, 1, 2>() && fits<GQ_Q6_KP, 2, 2>() &&
-                  fits<GQ_Q4_K, 1, 4>() && fits<GQ_Q4_K, 2, 4>(),
+                  fits<GQ_Q4_K, 1, 4>() && fits<GQ_Q4_K, 2, 4>() && fits<GQ_Q8_0, 1, 2>() && fits<GQ_Q8_0, 2, 2>() &&
+                  fits<GQ_Q8_0, 1, 4>() && fits<GQ_Q8_0, 2, 4>(),
               "ring shapes");
 
 /* One tile: tokens t0 .. t0 + 32 TT - 1 against this wave's 32 rows starting
@@ -502,7 +576,7 @@ __global__ __launch_bounds__(kPThreads * KS) void pgemm_kernel(PgArgs a) {
   if (MODE == MV_SWIGLU) ws = rw >> 1, r0 = tb * (kBN / 2) + 32 * (rw & 1);
   const PgSeg &S = a.seg[ws];
   const int dt = a.seg[sg].dtype;
-  const uint32_t rowbytes = (uint32_t)(a.K / 256) * (dt == GQ_Q4_K ? 144u : 210u);
+  const uint32_t rowbytes = dt == GQ_Q8_0 ? (uint32_t)(a.K / 32) * 34u : (uint32_t)(a.K / 256) * (dt == GQ_Q4_K ? 144u : 210u);
   const uint8_t *w = S.w + (size_t)r0 * rowbytes;
   gq_f32x16 acc[TT];
   if constexpr (fits<GQ_Q6_K, KS, TT>() && fits<GQ_Q6_KP, KS, TT>()) {
@@ -510,15 +584,22 @@ __global__ __launch_bounds__(kPThreads * KS) void pgemm_kernel(PgArgs a) {
       tile_loop<GQ_Q4_K, KS, TT>(a, w, rowbytes, t0, smem, acc);
     else if (dt == GQ_Q6_KP)
       tile_loop<GQ_Q6_KP, KS, TT>(a, w, rowbytes, t0, smem, acc);
+    else if (dt == GQ_Q8_0)
+      tile_loop<GQ_Q8_0, KS, TT>(a, w, rowbytes, t0, smem, acc);
     else
       tile_loop<GQ_Q6_K, KS, TT>(a, w, rowbytes, t0, smem, acc);
   } else if constexpr (fits<GQ_Q6_KP, KS, TT>()) { /* the launcher sends Q6_K to shapes that fit */
     if (dt == GQ_Q6_KP)
       tile_loop<GQ_Q6_KP, KS, TT>(a, w, rowbytes, t0, smem, acc);
+    else if (dt == GQ_Q8_0)
+      tile_loop<GQ_Q8_0, KS, TT>(a, w, rowbytes, t0, smem, acc);
     else
       tile_loop<GQ_Q4_K, KS, TT>(a, w, rowbytes, t0, smem, acc);
   } else {
-    tile_loop<GQ_Q4_K, KS, TT>(a, w, rowbytes, t0, smem, acc);
+    if (dt == GQ_Q8_0)
+      tile_loop<GQ_Q8_0, KS, TT>(a, w, rowbytes, t0, smem, acc);
+    else
+      tile_loop<GQ_Q4_K, KS, TT>(a, w, rowbytes, t0, smem, acc);
   }
   constexpr int XS = 4 * TT * 16 * 64 * 4; /* bytes of one K-half's tiles */
   GQ_LDS float *xk = (GQ_LDS float *)smem;
@@ -655,9 +736,10 @@ int launch_mode(const PgArgs &a0, int row_tiles, hipStream_t s) {
   PgArgs a = a0;
   a.kparts = 1;
   if (a.kparts_out) *a.kparts_out = 1;
-  bool q4 = false, q6 = false, q6p = false;
+  bool q4 = false, q6 = false, q6p = false, q8 = false;
   for (int i = 0; i < a.nseg; i++)
-    q4 |= a.seg[i].dtype == GQ_Q4_K, q6 |= a.seg[i].dtype == GQ_Q6_K, q6p |= a.seg[i].dtype == GQ_Q6_KP;
+    q4 |= a.seg[i].dtype == GQ_Q4_K, q6 |= a.seg[i].dtype == GQ_Q6_K, q6p |= a.seg[i].dtype == GQ_Q6_KP,
+        q8 |= a.seg[i].dtype == GQ_Q8_0;
   const int tiles4 = row_tiles * ((a.T + 127) / 128);
   a.rows_total = 0;
   for (int i = 0; i < a.nseg; i++) a.rows_total += a.seg[i].rows;
@@ -678,9 +760,11 @@ int launch_mode(const PgArgs &a0, int row_tiles, hipStream_t s) {
     a.kparts = KP;
     int rc;
     if (q6) {
-      rc = launch_shape<MODE, 1, 2>(a, row_tiles, std::max(ring_bytes<GQ_Q6_K, 1, 2>(), ring_bytes<GQ_Q4_K, 1, 2>()), s);
+      rc = launch_shape<MODE, 1, 2>(
+          a, row_tiles, std::max({ring_bytes<GQ_Q6_K, 1, 2>(), ring_bytes<GQ_Q4_K, 1, 2>(), ring_bytes<GQ_Q8_0, 1, 2>()}), s);
     } else {
-      const size_t lds = std::max(q6p ? ring_bytes<GQ_Q6_KP, 1, 4>() : 0, ring_bytes<GQ_Q4_K, 1, 4>());
+      const size_t lds = std::max({q6p ? ring_bytes<GQ_Q6_KP, 1, 4>() : 0, q8 ? ring_bytes<GQ_Q8_0, 1, 4>() : 0,
+                                   ring_bytes<GQ_Q4_K, 1, 4>()});
       rc = launch_shape<MODE, 1, 4>(a, row_tiles, lds, s);
     }
     if (rc) return rc;
@@ -698,17 +782,19 @@ int launch_mode(const PgArgs &a0, int row_tiles, hipStream_t s) {
   int ks = wgs <= n_cus() ? 2 : 1;
   if ((a.K / kBK) % 2) ks = 1;
   if (tt == 4) {
-    const size_t lds = ks == 2 ? std::max(q6p ? ring_bytes<GQ_Q6_KP, 2, 4>() : 0, ring_bytes<GQ_Q4_K, 2, 4>())
-                               : std::max(q6p ? ring_bytes<GQ_Q6_KP, 1, 4>() : 0, ring_bytes<GQ_Q4_K, 1, 4>());
+    const size_t lds = ks == 2 ? std::max({q6p ? ring_bytes<GQ_Q6_KP, 2, 4>() : 0, q8 ? ring_bytes<GQ_Q8_0, 2, 4>() : 0,
+                                           ring_bytes<GQ_Q4_K, 2, 4>()})
+                               : std::max({q6p ? ring_bytes<GQ_Q6_KP, 1, 4>() : 0, q8 ? ring_bytes<GQ_Q8_0, 1, 4>() : 0,
+                                           ring_bytes<GQ_Q4_K, 1, 4>()});
     return ks == 2 ? launch_shape<MODE, 2, 4>(a, row_tiles, lds, s) : launch_shape<MODE, 1, 4>(a, row_tiles, lds, s);
   }
   if (ks == 2) {
     const size_t lds = std::max({q6 ? ring_bytes<GQ_Q6_K, 2, 2>() : 0, q6p ? ring_bytes<GQ_Q6_KP, 2, 2>() : 0,
-                                 q4 ? ring_bytes<GQ_Q4_K, 2, 2>() : 0});
+                                 q4 ? ring_bytes<GQ_Q4_K, 2, 2>() : 0, q8 ? ring_bytes<GQ_Q8_0, 2, 2>() : 0});
     return launch_shape<MODE, 2, 2>(a, row_tiles, lds, s);
   }
   const size_t lds = std::max({q6 ? ring_bytes<GQ_Q6_K, 1, 2>() : 0, q6p ? ring_bytes<GQ_Q6_KP, 1, 2>() : 0,
-                               q4 ? ring_bytes<GQ_Q4_K, 1, 2>() : 0});
+                               q4 ? ring_bytes<GQ_Q4_K, 1, 2>() : 0, q8 ? ring_bytes<GQ_Q8_0, 1, 2>() : 0});
   return launch_shape<MODE, 1, 2>(a, row_tiles, lds, s);
 }
 
@@ -720,7 +806,7 @@ int gq_launch_pgemm(int mode, const PgArgs &a, hipStream_t s) {
   for (int i = 0; i < a.nseg; i++) {
     const PgSeg &g = a.seg[i];
     if (!g.w || g.rows <= 0) return -1;
-    if (g.dtype != GQ_Q4_K && g.dtype != GQ_Q6_K && g.dtype != GQ_Q6_KP) return -1;
+    if (g.dtype != GQ_Q4_K && g.dtype != GQ_Q6_K && g.dtype != GQ_Q6_KP && g.dtype != GQ_Q8_0) return -1;
     if ((g.dtype == GQ_Q6_K && a.K % 512) || (g.dtype == GQ_Q6_KP && a.K % 2048)) return -2;
     if (mode == MV_SWIGLU) {
       if (g.rows % (kBN / 2) || g.dtype != a.seg[0].dtype || g.rows != a.seg[0].rows) return -1;
@@ -732,10 +818,10 @@ int gq_launch_pgemm(int mode, const PgArgs &a, hipStream_t s) {
   /* the K-half exchange (4 TT tiles) and the SwiGLU exchange (2 TT tiles)
    * reuse the ring, which is larger */
   static_assert(ring_bytes<GQ_Q4_K, 1, 2>() >= 2 * 2 * 16 * 64 * 4 && ring_bytes<GQ_Q6_K, 1, 2>() >= 2 * 2 * 16 * 64 * 4 &&
-                    ring_bytes<GQ_Q4_K, 1, 4>() >= 2 * 4 * 16 * 64 * 4,
+                    ring_bytes<GQ_Q4_K, 1, 4>() >= 2 * 4 * 16 * 64 * 4 && ring_bytes<GQ_Q8_0, 1, 2>() >= 2 * 2 * 16 * 64 * 4,
                 "exchange fits the ring");
   static_assert(ring_bytes<GQ_Q4_K, 2, 2>() >= 6 * 2 * 16 * 64 * 4 && ring_bytes<GQ_Q6_K, 2, 2>() >= 6 * 2 * 16 * 64 * 4 &&
-                    ring_bytes<GQ_Q4_K, 2, 4>() >= 6 * 4 * 16 * 64 * 4,
+                    ring_bytes<GQ_Q4_K, 2, 4>() >= 6 * 4 * 16 * 64 * 4 && ring_bytes<GQ_Q8_0, 2, 2>() >= 6 * 2 * 16 * 64 * 4,
                 "exchanges fit the ring");
   if (mode == MV_SWIGLU) {
     if (a.nseg != 2 || !a.act) return -1;

@@ -1339,12 +1339,12 @@ static int pf_alloc(gq_ctx *c) {
   return 0;
 }
 
-/* The GEMM takes Q4_K rows in multiples of 128 and Q6_K rows likewise with
- * cols % 512 == 0; a model with any other projection prefills token by
- * token through the decode step instead. */
+/* The GEMM takes Q4_K and Q8_0 rows in multiples of 128 and Q6_K rows
+ * likewise with cols % 512 == 0; a model with any other projection
+ * prefills token by token through the decode step instead. */
 static bool pf_gemm_ok(const gq_weight &w) {
-  return (w.dtype == GQ_Q4_K || (w.dtype == GQ_Q6_K && w.cols % 512 == 0)) && w.rows % 128 == 0 &&
-         w.cols % 256 == 0;
+  return (w.dtype == GQ_Q4_K || w.dtype == GQ_Q8_0 || (w.dtype == GQ_Q6_K && w.cols % 512 == 0)) &&
+         w.rows % 128 == 0 && w.cols % 256 == 0;
 }
 
 static bool pf_model_ok(const gq_ctx *c) {
@@ -1863,7 +1863,8 @@ extern "C" int gq_hip_prefill_gemm_dev(gq_ctx *c, int dtype, int mode, const voi
                                        const float *x, int t, float *y, const float *r) {
   if (!c || !w || !x || !y || t <= 0 || n <= 0 || k <= 0 || (mode == 1 && !r) || (mode != 0 && mode != 1))
     return fail(c, -1, "prefill GEMM: bad argument");
-  if (dtype != GQ_Q4_K && dtype != GQ_Q6_K) return fail(c, -1, "prefill GEMM: Q4_K or Q6_K weights only");
+  if (dtype != GQ_Q4_K && dtype != GQ_Q6_K && dtype != GQ_Q8_0)
+    return fail(c, -1, "prefill GEMM: Q4_K, Q6_K or Q8_0 weights only");
   if (k % 256 || (dtype == GQ_Q6_K && k % 512)) return fail(c, -2, "prefill GEMM: cols %% 256 (Q6_K: %% 512)");
   if (n % 128) return fail(c, -1, "prefill GEMM: rows must be a multiple of 128");
   PgArgs a{};
@@ -1881,7 +1882,8 @@ extern "C" int gq_hip_prefill_gemm_dev(gq_ctx *c, int dtype, int mode, const voi
 extern "C" float gq_hip_time_prefill_gemm(gq_ctx *c, int dtype, const void *w, int n, int k, const float *x, int t,
                                          float *y, int n_iter) {
   if (!c || !w || !x || !y || t <= 0 || n <= 0 || k <= 0 || n_iter <= 0) return fail(c, -1, "time GEMM: bad argument"), -1.f;
-  if (dtype != GQ_Q4_K && dtype != GQ_Q6_K) return fail(c, -1, "time GEMM: Q4_K or Q6_K weights only"), -1.f;
+  if (dtype != GQ_Q4_K && dtype != GQ_Q6_K && dtype != GQ_Q8_0)
+    return fail(c, -1, "time GEMM: Q4_K, Q6_K or Q8_0 weights only"), -1.f;
   if (k % 256 || (dtype == GQ_Q6_K && k % 512) || n % 128) return fail(c, -2, "time GEMM: shape"), -1.f;
   PgArgs a{};
   if (!(a.x = pf_x16(c, x, (size_t)t * k))) return fail(c, -4, "time GEMM: x conversion"), -1.f;
@@ -1908,7 +1910,8 @@ extern "C" int gq_hip_prefill_gate_up_dev(gq_ctx *c, int dtype, const void *w_ga
                                           const float *x, int t, uint16_t *act) {
   if (!c || !w_gate || !w_up || !x || !act || t <= 0 || n <= 0 || k <= 0)
     return fail(c, -1, "prefill gate/up: bad argument");
-  if (dtype != GQ_Q4_K && dtype != GQ_Q6_K) return fail(c, -1, "prefill gate/up: Q4_K or Q6_K weights only");
+  if (dtype != GQ_Q4_K && dtype != GQ_Q6_K && dtype != GQ_Q8_0)
+    return fail(c, -1, "prefill gate/up: Q4_K, Q6_K or Q8_0 weights only");
   if (k % 256 || (dtype == GQ_Q6_K && k % 512)) return fail(c, -2, "prefill gate/up: cols %% 256 (Q6_K: %% 512)");
   if (n % 64) return fail(c, -1, "prefill gate/up: rows must be a multiple of 64");
   PgArgs a{};

@@ -318,7 +318,7 @@ int gq_hip_silu_mul_dev(gq_ctx *ctx, float *gate, const float *up, int n);
  * y[t][n] = sum_k x[t][k] w[n][k] for t < T tokens at once on the bf16
  * matrix cores, fp32 accumulation: the projections of a prefill chunk, which
  * the reference runs as T sequential matvecs (linear_dispatch,
- * engine.c:119-152).  w: rows x cols Q4_K or Q6_K on the device
+ * engine.c:119-152).  w: rows x cols Q4_K, Q6_K or Q8_0 on the device
  * (rows % 128 == 0, cols % 256 == 0, Q6_K cols % 512 == 0: -2 otherwise);
  * x: T x cols fp32, y: T x rows fp32, device pointers.  mode 0 stores, mode 1 adds r (T x rows, may alias y).
  * x and the dequantized weights are rounded to bf16 (nearest even) before
@@ -337,7 +337,7 @@ float gq_hip_time_prefill_gemm(gq_ctx *ctx, int dtype, const void *w, int rows, 
 /* act[t][n] = bf16(silu(g) * u) with g = x w_gate^T and u = x w_up^T on the
  * matrix cores in one launch (silu_inplace + elemwise_mul after the two
  * linear_dispatch calls, engine.c:524-549): w_gate and w_up rows x cols of
- * one dtype (Q4_K, or Q6_K with cols % 512 == 0), rows % 64 == 0; x T x
+ * one dtype (Q4_K, Q8_0, or Q6_K with cols % 512 == 0), rows % 64 == 0; x T x
  * cols fp32, act T x rows bf16 (uint16 bit patterns), device pointers. */
 int gq_hip_prefill_gate_up_dev(gq_ctx *ctx, int dtype, const void *w_gate, const void *w_up, int rows,
                                int cols, const float *x, int T, uint16_t *act);

@@ -27,7 +27,7 @@ import numpy as np
 import pytest
 
 from guanaco_amd import spec as S
-from util import bits, dequant_q4k_f64, dequant_q6k_f64, rel_l2
+from util import bits, dequant_q4k_f64, dequant_q6k_f64, dequant_q8_0_f64, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -77,6 +77,27 @@ def test_prefill_gemm_q6k(ctx, orc, T, N, K, mode):
     _gemm_case(ctx, orc, S.Q6_K, T, N, K, mode)
 
 
+@pytest.mark.parametrize("T,N,K", [(64, 128, 256), (100, 256, 512), (512, 1024, 4096), (77, 384, 1536),
+                                   (33, 128, 5632), (512, 2048, 2048)])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_prefill_gemm_q8_0(ctx, orc, T, N, K, mode):
+    """Q8_0 weights (quant_matvec_q8_0.c:5-10): w = d q is exact in fp32, so
+    the exact-input reference is bf16(d q) against bf16(x)."""
+    _gemm_case(ctx, orc, S.Q8_0, T, N, K, mode)
+
+
+def _dequant(dtype, w, rows, cols):
+    return {S.Q4_K: dequant_q4k_f64, S.Q6_K: dequant_q6k_f64, S.Q8_0: dequant_q8_0_f64}[dtype](w, rows, cols)
+
+
+def _kernel_weights(dtype, w, rows, cols):
+    """The fp32 weights the kernel rounds to bf16: Q4_K in its fma order,
+    Q6_K and Q8_0 exact."""
+    if dtype == S.Q4_K:
+        return q4k_dequant_kernel_order(w, rows, cols)
+    return _dequant(dtype, w, rows, cols).astype(np.float32)
+
+
 def _gemm_case(ctx, orc, dtype, T, N, K, mode):
     import guanaco_amd.hip as H
     seed = (T << 20) ^ (N << 8) ^ K ^ (dtype << 28)
@@ -90,8 +111,8 @@ def _gemm_case(ctx, orc, dtype, T, N, K, mode):
     assert rc == 0
     y = yd.download(count=T * N).reshape(T, N)
     base = r.astype(np.float64) if mode == 1 else 0.0
-    wf = dequant_q4k_f64(w, N, K) if dtype == S.Q4_K else dequant_q6k_f64(w, N, K)
-    wk = q4k_dequant_kernel_order(w, N, K) if dtype == S.Q4_K else wf.astype(np.float32)
+    wf = _dequant(dtype, w, N, K)
+    wk = _kernel_weights(dtype, w, N, K)
     exact_in = bf16_round(x).astype(np.float64) @ bf16_round(wk).astype(np.float64).T
     assert rel_l2(y, base + exact_in) < 1e-5
     full = x.astype(np.float64) @ wf.T
@@ -144,7 +165,8 @@ def test_prefill_gemm_rejects_bad_shapes(ctx):
     buf = ctx.alloc(1 << 20)
     assert H.lib.gq_hip_prefill_gemm_dev(ctx.h, S.Q4_K, 0, buf.ptr, 100, 256, buf.ptr, 4, buf.ptr, None) != 0
     assert H.lib.gq_hip_prefill_gemm_dev(ctx.h, S.Q4_K, 0, buf.ptr, 128, 300, buf.ptr, 4, buf.ptr, None) != 0
-    assert H.lib.gq_hip_prefill_gemm_dev(ctx.h, S.Q8_0, 0, buf.ptr, 128, 256, buf.ptr, 4, buf.ptr, None) != 0
+    assert H.lib.gq_hip_prefill_gemm_dev(ctx.h, S.F32, 0, buf.ptr, 128, 256, buf.ptr, 4, buf.ptr, None) != 0
+    assert H.lib.gq_hip_prefill_gemm_dev(ctx.h, S.Q8_0, 0, buf.ptr, 128, 288, buf.ptr, 4, buf.ptr, None) != 0
     assert H.lib.gq_hip_prefill_gemm_dev(ctx.h, S.Q6_K, 0, buf.ptr, 128, 256, buf.ptr, 4, buf.ptr, None) == -2
     buf.free()
 
@@ -157,7 +179,8 @@ def silu_mul_f32(g, u):
 
 
 @pytest.mark.parametrize("dtype,T,N,K", [(S.Q4_K, 512, 1024, 4096), (S.Q4_K, 70, 192, 512),
-                                         (S.Q6_K, 100, 256, 1024), (S.Q6_K, 100, 256, 4096)])
+                                         (S.Q6_K, 100, 256, 1024), (S.Q6_K, 100, 256, 4096),
+                                         (S.Q8_0, 100, 256, 1024), (S.Q8_0, 512, 1024, 2048)])
 def test_prefill_gate_up_swiglu(ctx, orc, dtype, T, N, K):
     """gate and up in one launch with SiLU(gate) * up in the epilogue
     (kernels_cpu.c:312-389), bf16 out: against the exact-input reference
@@ -172,8 +195,8 @@ def test_prefill_gate_up_swiglu(ctx, orc, dtype, T, N, K):
     assert H.lib.gq_hip_prefill_gate_up_dev(ctx.h, dtype, gd, ud, N, K, xd.ptr, T, act.ptr) == 0
     a16 = act.download(np.uint16, count=T * N).reshape(T, N)
     got = (a16.astype(np.uint32) << 16).view(np.float32)
-    deq = dequant_q4k_f64 if dtype == S.Q4_K else dequant_q6k_f64
-    kern = (lambda w: q4k_dequant_kernel_order(w, N, K)) if dtype == S.Q4_K else (lambda w: deq(w, N, K).astype(np.float32))
+    deq = lambda w, n, k: _dequant(dtype, w, n, k)  # noqa: E731
+    kern = lambda w: _kernel_weights(dtype, w, N, K)  # noqa: E731
     xb = bf16_round(x).astype(np.float64)
     g = xb @ bf16_round(kern(wg)).astype(np.float64).T
     u = xb @ bf16_round(kern(wu)).astype(np.float64).T
@@ -333,6 +356,42 @@ def test_prefill_q6k_step_layout_model(orc):
         for t in range(len(toks)):
             t_cpu, lc, _ = hm.forward(kv, int(toks[t]), t)
         assert rel_l2(lg, lc) < PF_TOL and nxt == t_cpu
+    finally:
+        c.close()
+
+
+def test_prefill_q8_0_model(orc):
+    """A model with every weight Q8_0 prefills through the GEMM (the
+    reference's prefill takes Q8_0 through linear_dispatch,
+    engine.c:119-152): last-token logits and the new cache rows against T
+    sequential oracle steps (PF_TOL), the next greedy token equal, and the
+    result not the token-by-token one (prefill mode 1), which is held to
+    the decode tolerance."""
+    import guanaco_amd.hip as H
+    from oracle import HostModel
+    spec = S.ModelSpec("tiny-q8_0", n_layers=2, hidden=512, ff=1024, n_heads=8, n_kv_heads=2, vocab=1000,
+                       layer_dtypes={k: S.Q8_0 for k in S.LAYER_WEIGHTS}, embed_dtype=S.Q8_0,
+                       lm_head_dtype=S.Q8_0)
+    c = H.Context(0)
+    try:
+        hm = HostModel(orc, spec, 64)
+        dm = H.DeviceModel(c, spec, 64)
+        toks = np.random.default_rng(8).integers(0, spec.vocab, 48).astype(np.int32)
+        kv = hm.new_kv()
+        for t in range(len(toks)):
+            t_cpu, lc, _ = hm.forward(kv, int(toks[t]), t)
+        nxt, lg, _, _ = dm.prefill(toks, 0)
+        assert rel_l2(lg, lc) < PF_TOL and nxt == t_cpu
+        for l in range(spec.n_layers):
+            dk, dv = c.kv_read_layer(l)
+            for d, h in ((dk, kv.view("k")[l]), (dv, kv.view("v")[l])):
+                d = d.reshape(h.shape)
+                assert rel_l2(d[:, :len(toks)], h[:, :len(toks)]) < PF_TOL
+        assert H.lib.gq_hip_set_prefill_mode(c.h, 1) == 0
+        nxt1, lg1, _, _ = dm.prefill(toks, 0)
+        assert rel_l2(lg1, lc) < 1e-3 and nxt1 == t_cpu
+        assert not np.array_equal(bits(lg), bits(lg1))  # the GEMM path ran in mode 0
+        print(f"Q8_0 model prefill: GEMM {rel_l2(lg, lc):.2e}, token by token {rel_l2(lg1, lc):.2e}")
     finally:
         c.close()
 
