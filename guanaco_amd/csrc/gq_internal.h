@@ -32,10 +32,8 @@ enum { MV_STORE = 0, MV_RESID = 1, MV_SWIGLU = 2 };
 enum { SEG_PLAIN = 0, SEG_ROPE = 1, SEG_ROPE_KV = 2, SEG_KV = 3 };
 
 /* Q6_K in the vector-ALU matvec's unit layout: an internal weight type,
- * never seen at the C ABI */
+ * never seen at the C ABI; the prefill GEMM reads it too (cols % 2048) */
 #define GQ_Q6_KX 65
-/* Q6_K in the prefill GEMM's step layout (gq_launch_q6k_steps): internal too */
-#define GQ_Q6_KP 66
 
 struct MvSeg {
   const uint8_t *w;
@@ -157,8 +155,9 @@ void gq_matvec_set_cus(int n_cu);
 size_t gq_mm_tile_bytes(int dtype, int rows, int cols, bool swiglu);
 int gq_launch_mm_tile(void *dst, int dtype, const void *w0, const void *w1, int rows, int cols, hipStream_t s);
 /* Q6_K weights (rows x cols, cols a multiple of 512) re-laid out for the
- * vector-ALU matvec: each 32-column unit's quants, high bits, scales and d
- * at naturally aligned offsets, the same bytes (gq_q6k_units_bytes). */
+ * vector-ALU matvec and the prefill GEMM: each 32-column unit's quants, high
+ * bits, scales and d at naturally aligned offsets, the same bytes
+ * (gq_q6k_units_bytes). */
 size_t gq_q6k_units_bytes(int rows, int cols);
 int gq_launch_q6k_units(void *dst, const void *src, int rows, int cols, hipStream_t s);
 /* whether the matrix-core kernel is selected for every launch it fits
@@ -252,8 +251,9 @@ int gq_launch_copy(void *dst, const void *src, size_t bytes, int n_cu, hipStream
 
 /* ---- prefill chunk ---------------------------------------------------
  * Y[T][rows] = X[T][K] . W^T on the bf16 matrix cores for up to three weight
- * segments in one launch (each rows % 128 == 0, Q4_K, Q8_0, or Q6_K with
- * K % 512 == 0; K % 256 == 0), X bf16 row-major.  MV_STORE writes y, MV_RESID adds into
+ * segments in one launch (each rows % 128 == 0, Q4_K, Q8_0, Q6_K with
+ * K % 512 == 0, or Q6_K in the unit layout, GQ_Q6_KX, with K % 2048 == 0;
+ * K % 256 == 0), X bf16 row-major.  MV_STORE writes y, MV_RESID adds into
  * y; MV_SWIGLU takes gate (seg 0) and up (seg 1) of equal rows
  * (rows % 64 == 0) and writes act[T][rows] = bf16(silu(gate) * up). */
 struct PgSeg {
@@ -283,12 +283,6 @@ int gq_launch_pgemm(int mode, const PgArgs &a, hipStream_t s);
 /* at most this many K parts in a split launch: PgArgs.part needs
  * kPgKParts * T * (all segments' rows) floats */
 constexpr int kPgKParts = 4;
-/* Q6_K weights (rows x cols, cols a multiple of 2048) re-laid out for the
- * prefill GEMM: each 64-weight step's quant bytes together, then the scales
- * and d, the same bytes (gq_q6k_steps_bytes); segments then take dtype
- * GQ_Q6_KP. */
-size_t gq_q6k_steps_bytes(int rows, int cols);
-int gq_launch_q6k_steps(void *dst, const void *src, int rows, int cols, hipStream_t s);
 int gq_launch_to_bf16(const float *x, __bf16 *y, size_t n, hipStream_t s);
 /* RMSNorm of `rows` consecutive rows of dim floats, one workgroup per row;
  * out16 != NULL writes bf16 there instead of fp32 to out.  parts != NULL

@@ -261,7 +261,7 @@ struct Ux<GQ_Q8_0> {
  * order are Q6_K's: results are bit-identical to it. */
 template <>
 struct Ux<GQ_Q6_KX> {
-  static constexpr int BB = 210, XHI = 64;
+  static constexpr int XHI = 64;
   struct Raw {
     uint4 q;
     uint2 h;

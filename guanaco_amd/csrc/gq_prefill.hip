@@ -227,21 +227,22 @@ struct PW<GQ_Q6_K> {
 };
 
 
-/* Q6_K in the prefill step layout (gq_launch_q6k_steps, made once at model
- * bind for rows whose 210-byte blocks fall on 16-byte boundaries, K % 2048
- * == 0): per row, the 48 quant bytes of each 64-weight step s at 48 s (32
- * bytes whose byte j holds the 4-bit parts of step weights j (low nibble)
- * and j + 32 (high nibble), then 16 bytes whose byte j holds the 2-bit parts
- * of weights j, j + 16, j + 32, j + 48 at bits 0, 2, 4, 6), the blocks'
- * 16 scale bytes as they are at 192 nb, their d at 208 nb: the same 210
- * bytes per block.  A wave stages its 32 rows' step in two 16-byte DMA
- * instructions plus one dword instruction (scales and d) instead of the
- * reference layout's fifteen dword instructions, and reads every quant
- * byte once.  Weights and their order are the reference layout's, so the
- * GEMM's results are bit-identical to it. */
+/* Q6_K in the decode matvec's unit layout (gq_launch_q6k_units; made once
+ * at model bind, and read here too for rows on 16-byte boundaries, K % 2048
+ * == 0).  Unit u (block u/8, half n, group v) holds the 16 ql bytes whose
+ * low nibbles are weights 128 n + 16 v + i and high nibbles 128 n + 64 +
+ * 16 v + i (i < 16), then two dwords of their 2-bit fields; its two int8
+ * scales at 192 nb + 2u; the block's d at 208 nb + 2 (u/8).  Step s = 4 b +
+ * 2 n + p takes units 8 b + 4 n + 2 p and the next: 48 contiguous quant
+ * bytes at 48 s, 4 scale bytes at 192 nb + 4 s.  Its 64 weights are not
+ * consecutive columns: k-octets 0-3 are the two units' low nibbles, columns
+ * 256 b + 128 n + 32 p + 0..31, and octets 4-7 their high nibbles, the same
+ * plus 64: k-octet o of step s is columns 64 s - 32 (s & 1) + 8 o (+32 for
+ * o >= 4), and the X staging of this type fetches those.  Per weight w = (d sc) q - 32 (d sc) with PW<GQ_Q6_K>'s
+ * roundings, so the bf16 weights are the reference layout's; only the order
+ * of the K sums differs. */
 template <>
-struct PW<GQ_Q6_KP> {
-  static constexpr int BB = 210;
+struct PW<GQ_Q6_KX> {
   static constexpr int kWaveLds = 2048 + 256; /* quants (96 16-byte pieces), then 32 scale + 32 d dwords */
   static constexpr int kDma = 3;
   struct Plan {
@@ -270,31 +271,39 @@ struct PW<GQ_Q6_KP> {
          __builtin_amdgcn_readfirstlane(lds + 2048u));
   }
   struct Raw {
-    uint2 q0, q1, hb;
+    uint2 q0, q1;      /* ql bytes 8 h .. 8 h + 7 of the two units */
+    uint32_t h0, h1;   /* their 2-bit fields (dword h of each unit's pair) */
     uint32_t sc, dd;
   };
   __device__ static void read(Raw &w, const GQ_LDS uint8_t *ws, int lane, int) {
     const uint32_t r = (uint32_t)(lane & 31), h = (uint32_t)(lane >> 5);
     w.q0 = lld<uint2>(ws, 48u * r + 8u * h);
-    w.q1 = lld<uint2>(ws, 48u * r + 16u + 8u * h);
-    w.hb = lld<uint2>(ws, 48u * r + 32u + 8u * h);
+    w.h0 = lld<uint32_t>(ws, 48u * r + 16u + 4u * h);
+    w.q1 = lld<uint2>(ws, 48u * r + 24u + 8u * h);
+    w.h1 = lld<uint32_t>(ws, 48u * r + 40u + 4u * h);
     w.sc = lld<uint32_t>(ws, 2048u + 4u * r);
     w.dd = lld<uint32_t>(ws, 2176u + 4u * r);
   }
-  /* w = (d sc) q - 32 (d sc) as PW<GQ_Q6_K>::dequant (the same roundings) */
+  /* b[kk]: octet 2 kk + h = unit kk & 1, low (kk < 2) or high nibbles of
+   * its quant dwords 2h, 2h + 1; the unit decode of the matvec
+   * (Ux<GQ_Q6_KX>::dot): 6-bit q = nibble | field << 4 */
   __device__ static void dequant(const Raw &rw, int s, gq_bf16x8 b[4]) {
     const float d = gq_h2f(rw.dd >> (16u * (uint32_t)((s >> 2) & 1)));
 #pragma unroll
     for (int kk = 0; kk < 4; kk++) {
-      const float a = d * (float)(int8_t)((rw.sc >> (8 * kk)) & 0xffu);
+      const int un = kk & 1;
+      const bool hi = kk >= 2;
+      /* scale bytes: unit 0 (low, high), unit 1 (low, high) */
+      const float a = d * (float)(int8_t)((rw.sc >> (8 * (2 * un + (hi ? 1 : 0)))) & 0xffu);
       const float m = 32.0f * a;
-      const uint2 q = (kk & 1) ? rw.q1 : rw.q0;
-      const uint32_t sh = kk >= 2 ? 4u : 0u;
-      const uint32_t pw[2] = {q.x, q.y}, hw[2] = {rw.hb.x, rw.hb.y};
+      const uint2 q = un ? rw.q1 : rw.q0;
+      const uint32_t hf = un ? rw.h1 : rw.h0;
+      const uint32_t qw[2] = {q.x, q.y}, fw[2] = {hf, hf >> 2};
       uint32_t o[4];
 #pragma unroll
       for (int k = 0; k < 2; k++) {
-        const uint32_t u = ((pw[k] >> sh) & 0x0f0f0f0fu) | (((hw[k] >> (2 * kk)) & 0x03030303u) << 4);
+        const uint32_t u = hi ? (((qw[k] >> 4) & 0x0F0F0F0Fu) | (fw[k] & 0x30303030u))
+                              : ((qw[k] & 0x0F0F0F0Fu) | ((fw[k] << 4) & 0x30303030u));
         const float v0 = __builtin_fmaf(a, (float)(u & 0xffu), -m);
         const float v1 = __builtin_fmaf(a, (float)((u >> 8) & 0xffu), -m);
         const float v2 = __builtin_fmaf(a, (float)((u >> 16) & 0xffu), -m);
@@ -379,35 +388,6 @@ struct PW<GQ_Q8_0> {
   }
 };
 
-/* One thread per (row, step): a Q6_K row in the reference layout (src) to the
- * step layout above (dst, same size). */
-__global__ __launch_bounds__(256) void q6k_steps_kernel(const uint8_t *src, uint8_t *dst, int rows, int nb) {
-  const int sp = 4 * nb;
-  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (t >= (long long)rows * sp) return;
-  const int row = (int)(t / sp), s = (int)(t - (long long)row * sp);
-  const int b = s >> 2, cc = s & 3, n = cc >> 1, par = cc & 1;
-  const uint8_t *blk = src + ((size_t)row * nb + b) * 210;
-  uint8_t *drow = dst + (size_t)row * nb * 210, *dq = drow + 48 * s;
-  /* step weight tt < 64 is block weight 128 n + 32 g + l, g = 2 par + tt / 32,
-   * l = tt % 32 (quant_matvec_q6_k.c:70-90) */
-  auto q4 = [&](int tt) -> uint32_t {
-    const int g = 2 * par + (tt >> 5), l = tt & 31;
-    return ((uint32_t)blk[64 * n + 32 * (g & 1) + l] >> (4 * (g >> 1))) & 15u;
-  };
-  auto q2 = [&](int tt) -> uint32_t {
-    const int g = 2 * par + (tt >> 5), l = tt & 31;
-    return ((uint32_t)blk[128 + 32 * n + l] >> (2 * g)) & 3u;
-  };
-  for (int j = 0; j < 32; j++) dq[j] = (uint8_t)(q4(j) | (q4(j + 32) << 4));
-  for (int j = 0; j < 16; j++) dq[32 + j] = (uint8_t)(q2(j) | (q2(j + 16) << 2) | (q2(j + 32) << 4) | (q2(j + 48) << 6));
-  for (int k = 0; k < 4; k++) drow[192 * nb + 4 * s + k] = blk[192 + 4 * cc + k];
-  if (cc == 0) {
-    drow[208 * nb + 2 * b] = blk[208];
-    drow[208 * nb + 2 * b + 1] = blk[209];
-  }
-}
-
 /* KS = 1 or 2 K-splits per workgroup: with KS = 2, eight waves, the second
  * four running the upper half of K for the same tile; their sums are added
  * through LDS at the end.  Two waves per SIMD hide each other's LDS, DMA and
@@ -437,7 +417,7 @@ constexpr bool fits() {
   return ring<DT, KS, TT>() >= 3 && (ring<DT, KS, TT>() - 2) * (TT + PW<DT>::kDma) < 64;
 }
 static_assert(fits<GQ_Q4_K, 1, 2>() && fits<GQ_Q4_K, 2, 2>() && fits<GQ_Q6_K, 1, 2>() && fits<GQ_Q6_K, 2, 2>() &&
-                  fits<GQ_Q6_KP, 1, 2>() && fits<GQ_Q6_KP, 2, 2>() &&
+                  fits<GQ_Q6_KX, 1, 2>() && fits<GQ_Q6_KX, 2, 2>() &&
                   fits<GQ_Q4_K, 1, 4>() && fits<GQ_Q4_K, 2, 4>() && fits<GQ_Q8_0, 1, 2>() && fits<GQ_Q8_0, 2, 2>() &&
                   fits<GQ_Q8_0, 1, 4>() && fits<GQ_Q8_0, 2, 4>(),
               "ring shapes");
@@ -469,14 +449,16 @@ __device__ __forceinline__ void tile_loop(const PgArgs &a, const uint8_t *w, uin
   for (int j = 0; j < TT; j++) {
     const int tl = 8 * (TT * rw + j) + (lane >> 3), q = lane & 7;
     const int oct = q ^ ((tl >> 1) & 7);
-    xsrc[j] = a.x + (size_t)min(t0 + tl, a.T - 1) * a.K + 8 * oct;
+    /* the unit layout's steps take columns 64 s - 32 (s & 1) + 8 o (+32 for
+     * o >= 4): PW<GQ_Q6_KX> */
+    xsrc[j] = a.x + (size_t)min(t0 + tl, a.T - 1) * a.K + 8 * oct + (DT == GQ_Q6_KX && oct >= 4 ? 32 : 0);
   }
   auto issue = [&](int st) {
     const uint32_t slot = sbase + (uint32_t)((st % kRing) * SB);
+    const int s = s0 + st, xs = DT == GQ_Q6_KX ? s * kBK - 32 * (s & 1) : s * kBK;
 #pragma unroll
     for (int j = 0; j < TT; j++)
-      dma16(xsrc[j] + (s0 + st) * kBK,
-            __builtin_amdgcn_readfirstlane(slot + xreg + 1024u * (uint32_t)(TT * rw + j)));
+      dma16(xsrc[j] + xs, __builtin_amdgcn_readfirstlane(slot + xreg + 1024u * (uint32_t)(TT * rw + j)));
     PW<DT>::issue(pl, w, s0 + st, slot + wreg);
   };
   for (int st = 0; st < kRing - 1 && st < ns; st++) issue(st);
@@ -579,18 +561,18 @@ __global__ __launch_bounds__(kPThreads * KS) void pgemm_kernel(PgArgs a) {
   const uint32_t rowbytes = dt == GQ_Q8_0 ? (uint32_t)(a.K / 32) * 34u : (uint32_t)(a.K / 256) * (dt == GQ_Q4_K ? 144u : 210u);
   const uint8_t *w = S.w + (size_t)r0 * rowbytes;
   gq_f32x16 acc[TT];
-  if constexpr (fits<GQ_Q6_K, KS, TT>() && fits<GQ_Q6_KP, KS, TT>()) {
+  if constexpr (fits<GQ_Q6_K, KS, TT>() && fits<GQ_Q6_KX, KS, TT>()) {
     if (dt == GQ_Q4_K)
       tile_loop<GQ_Q4_K, KS, TT>(a, w, rowbytes, t0, smem, acc);
-    else if (dt == GQ_Q6_KP)
-      tile_loop<GQ_Q6_KP, KS, TT>(a, w, rowbytes, t0, smem, acc);
+    else if (dt == GQ_Q6_KX)
+      tile_loop<GQ_Q6_KX, KS, TT>(a, w, rowbytes, t0, smem, acc);
     else if (dt == GQ_Q8_0)
       tile_loop<GQ_Q8_0, KS, TT>(a, w, rowbytes, t0, smem, acc);
     else
       tile_loop<GQ_Q6_K, KS, TT>(a, w, rowbytes, t0, smem, acc);
-  } else if constexpr (fits<GQ_Q6_KP, KS, TT>()) { /* the launcher sends Q6_K to shapes that fit */
-    if (dt == GQ_Q6_KP)
-      tile_loop<GQ_Q6_KP, KS, TT>(a, w, rowbytes, t0, smem, acc);
+  } else if constexpr (fits<GQ_Q6_KX, KS, TT>()) { /* the launcher sends Q6_K to shapes that fit */
+    if (dt == GQ_Q6_KX)
+      tile_loop<GQ_Q6_KX, KS, TT>(a, w, rowbytes, t0, smem, acc);
     else if (dt == GQ_Q8_0)
       tile_loop<GQ_Q8_0, KS, TT>(a, w, rowbytes, t0, smem, acc);
     else
@@ -736,9 +718,9 @@ int launch_mode(const PgArgs &a0, int row_tiles, hipStream_t s) {
   PgArgs a = a0;
   a.kparts = 1;
   if (a.kparts_out) *a.kparts_out = 1;
-  bool q4 = false, q6 = false, q6p = false, q8 = false;
+  bool q4 = false, q6 = false, q6x = false, q8 = false;
   for (int i = 0; i < a.nseg; i++)
-    q4 |= a.seg[i].dtype == GQ_Q4_K, q6 |= a.seg[i].dtype == GQ_Q6_K, q6p |= a.seg[i].dtype == GQ_Q6_KP,
+    q4 |= a.seg[i].dtype == GQ_Q4_K, q6 |= a.seg[i].dtype == GQ_Q6_K, q6x |= a.seg[i].dtype == GQ_Q6_KX,
         q8 |= a.seg[i].dtype == GQ_Q8_0;
   const int tiles4 = row_tiles * ((a.T + 127) / 128);
   a.rows_total = 0;
@@ -763,7 +745,7 @@ int launch_mode(const PgArgs &a0, int row_tiles, hipStream_t s) {
       rc = launch_shape<MODE, 1, 2>(
           a, row_tiles, std::max({ring_bytes<GQ_Q6_K, 1, 2>(), ring_bytes<GQ_Q4_K, 1, 2>(), ring_bytes<GQ_Q8_0, 1, 2>()}), s);
     } else {
-      const size_t lds = std::max({q6p ? ring_bytes<GQ_Q6_KP, 1, 4>() : 0, q8 ? ring_bytes<GQ_Q8_0, 1, 4>() : 0,
+      const size_t lds = std::max({q6x ? ring_bytes<GQ_Q6_KX, 1, 4>() : 0, q8 ? ring_bytes<GQ_Q8_0, 1, 4>() : 0,
                                    ring_bytes<GQ_Q4_K, 1, 4>()});
       rc = launch_shape<MODE, 1, 4>(a, row_tiles, lds, s);
     }
@@ -782,18 +764,18 @@ int launch_mode(const PgArgs &a0, int row_tiles, hipStream_t s) {
   int ks = wgs <= n_cus() ? 2 : 1;
   if ((a.K / kBK) % 2) ks = 1;
   if (tt == 4) {
-    const size_t lds = ks == 2 ? std::max({q6p ? ring_bytes<GQ_Q6_KP, 2, 4>() : 0, q8 ? ring_bytes<GQ_Q8_0, 2, 4>() : 0,
+    const size_t lds = ks == 2 ? std::max({q6x ? ring_bytes<GQ_Q6_KX, 2, 4>() : 0, q8 ? ring_bytes<GQ_Q8_0, 2, 4>() : 0,
                                            ring_bytes<GQ_Q4_K, 2, 4>()})
-                               : std::max({q6p ? ring_bytes<GQ_Q6_KP, 1, 4>() : 0, q8 ? ring_bytes<GQ_Q8_0, 1, 4>() : 0,
+                               : std::max({q6x ? ring_bytes<GQ_Q6_KX, 1, 4>() : 0, q8 ? ring_bytes<GQ_Q8_0, 1, 4>() : 0,
                                            ring_bytes<GQ_Q4_K, 1, 4>()});
     return ks == 2 ? launch_shape<MODE, 2, 4>(a, row_tiles, lds, s) : launch_shape<MODE, 1, 4>(a, row_tiles, lds, s);
   }
   if (ks == 2) {
-    const size_t lds = std::max({q6 ? ring_bytes<GQ_Q6_K, 2, 2>() : 0, q6p ? ring_bytes<GQ_Q6_KP, 2, 2>() : 0,
+    const size_t lds = std::max({q6 ? ring_bytes<GQ_Q6_K, 2, 2>() : 0, q6x ? ring_bytes<GQ_Q6_KX, 2, 2>() : 0,
                                  q4 ? ring_bytes<GQ_Q4_K, 2, 2>() : 0, q8 ? ring_bytes<GQ_Q8_0, 2, 2>() : 0});
     return launch_shape<MODE, 2, 2>(a, row_tiles, lds, s);
   }
-  const size_t lds = std::max({q6 ? ring_bytes<GQ_Q6_K, 1, 2>() : 0, q6p ? ring_bytes<GQ_Q6_KP, 1, 2>() : 0,
+  const size_t lds = std::max({q6 ? ring_bytes<GQ_Q6_K, 1, 2>() : 0, q6x ? ring_bytes<GQ_Q6_KX, 1, 2>() : 0,
                                q4 ? ring_bytes<GQ_Q4_K, 1, 2>() : 0, q8 ? ring_bytes<GQ_Q8_0, 1, 2>() : 0});
   return launch_shape<MODE, 1, 2>(a, row_tiles, lds, s);
 }
@@ -806,8 +788,8 @@ int gq_launch_pgemm(int mode, const PgArgs &a, hipStream_t s) {
   for (int i = 0; i < a.nseg; i++) {
     const PgSeg &g = a.seg[i];
     if (!g.w || g.rows <= 0) return -1;
-    if (g.dtype != GQ_Q4_K && g.dtype != GQ_Q6_K && g.dtype != GQ_Q6_KP && g.dtype != GQ_Q8_0) return -1;
-    if ((g.dtype == GQ_Q6_K && a.K % 512) || (g.dtype == GQ_Q6_KP && a.K % 2048)) return -2;
+    if (g.dtype != GQ_Q4_K && g.dtype != GQ_Q6_K && g.dtype != GQ_Q6_KX && g.dtype != GQ_Q8_0) return -1;
+    if ((g.dtype == GQ_Q6_K && a.K % 512) || (g.dtype == GQ_Q6_KX && a.K % 2048)) return -2; /* Q6_KX: 16-byte rows */
     if (mode == MV_SWIGLU) {
       if (g.rows % (kBN / 2) || g.dtype != a.seg[0].dtype || g.rows != a.seg[0].rows) return -1;
     } else {
@@ -830,16 +812,6 @@ int gq_launch_pgemm(int mode, const PgArgs &a, hipStream_t s) {
   if (mode == MV_RESID) return launch_mode<MV_RESID>(a, tiles, s);
   if (mode == MV_STORE) return launch_mode<MV_STORE>(a, tiles, s);
   return -1;
-}
-
-size_t gq_q6k_steps_bytes(int rows, int cols) { return (size_t)rows * (size_t)(cols / 256) * 210; }
-
-int gq_launch_q6k_steps(void *dst, const void *src, int rows, int cols, hipStream_t s) {
-  if (!dst || !src || rows <= 0 || cols <= 0 || cols % 2048) return -1; /* 16-byte aligned rows */
-  const long long n = (long long)rows * (cols / 64);
-  hipLaunchKernelGGL(q6k_steps_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (const uint8_t *)src,
-                     (uint8_t *)dst, rows, cols / 256);
-  return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
 int gq_launch_to_bf16(const float *x, __bf16 *y, size_t n, hipStream_t s) {

@@ -87,9 +87,9 @@ struct gq_ctx {
   struct MmLayer {
     const uint8_t *gu = nullptr;
     const uint8_t *dx = nullptr; /* Q6_K down in the vector-ALU unit layout (gq_launch_q6k_units) */
-    /* Q6_K projections in the prefill GEMM's step layout (gq_launch_q6k_steps):
-     * wq, wk, wv, wo, gate, up, down */
-    const uint8_t *ps[7] = {};
+    /* Q6_K projections in the same unit layout for the prefill GEMM (cols %
+     * 2048): wq, wk, wv, wo, gate, up, down; ux[6] is dx itself */
+    const uint8_t *ux[7] = {};
   };
   std::vector<MmLayer> mm;
   const uint8_t *mm_lm = nullptr;
@@ -805,8 +805,9 @@ static void mm_free(gq_ctx *c) {
     p = nullptr;
   };
   for (auto &L : c->mm) {
+    if (L.ux[6] == L.dx) L.ux[6] = nullptr; /* one allocation */
     rel(L.gu), rel(L.dx);
-    for (auto &p : L.ps) rel(p);
+    for (auto &p : L.ux) rel(p);
   }
   c->mm.clear();
   rel(c->mm_lm);
@@ -879,14 +880,20 @@ extern "C" int gq_hip_model_bind(gq_ctx *c, const gq_model *m) {
       if (d && gq_launch_q6k_units(d, L.w_down.data, L.w_down.rows, L.w_down.cols, c->stream) == 0) c->mm[l].dx = d;
       else if (d) gq_hip_free(c, d);
     }
-    /* Q6_K projections the prefill GEMM takes, re-laid out so a step's quant
-     * bytes are one 16-byte-aligned range (rows on 16-byte boundaries) */
+    /* the prefill GEMM reads Q6_K projections whose rows fall on 16-byte
+     * boundaries in the same unit layout, where a step's quant bytes are one
+     * 16-byte-aligned range: the down projection's copy above, one of their
+     * own for the others */
     const gq_weight *pw[7] = {&L.wq, &L.wk, &L.wv, &L.wo, &L.w_gate, &L.w_up, &L.w_down};
     for (int i = 0; i < 7; i++) {
       const gq_weight &g = *pw[i];
       if (g.dtype != GQ_Q6_K || g.cols % 2048 || g.rows % 128) continue;
-      uint8_t *d = (uint8_t *)dev_alloc(c, gq_q6k_steps_bytes(g.rows, g.cols));
-      if (d && gq_launch_q6k_steps(d, g.data, g.rows, g.cols, c->stream) == 0) c->mm[l].ps[i] = d;
+      if (i == 6) {
+        c->mm[l].ux[6] = c->mm[l].dx;
+        continue;
+      }
+      uint8_t *d = (uint8_t *)dev_alloc(c, gq_q6k_units_bytes(g.rows, g.cols));
+      if (d && gq_launch_q6k_units(d, g.data, g.rows, g.cols, c->stream) == 0) c->mm[l].ux[i] = d;
       else if (d) gq_hip_free(c, d);
     }
   }
@@ -1357,10 +1364,10 @@ static bool pf_model_ok(const gq_ctx *c) {
 }
 
 /* weight i (wq, wk, wv, wo, gate, up, down) of layer l as a GEMM segment:
- * its step-layout copy where model bind made one */
+ * its unit-layout copy where model bind made one */
 static PgSeg pg_seg(const gq_ctx *c, int l, int i, const gq_weight &w, float *y) {
-  const uint8_t *ps = (size_t)l < c->mm.size() && !gq_matvec_q6k_ref() ? c->mm[l].ps[i] : nullptr;
-  return ps ? PgSeg{ps, y, w.rows, GQ_Q6_KP} : PgSeg{(const uint8_t *)w.data, y, w.rows, w.dtype};
+  const uint8_t *ux = (size_t)l < c->mm.size() && !gq_matvec_q6k_ref() ? c->mm[l].ux[i] : nullptr;
+  return ux ? PgSeg{ux, y, w.rows, GQ_Q6_KX} : PgSeg{(const uint8_t *)w.data, y, w.rows, w.dtype};
 }
 
 /* RoPE + append of T tokens at pos..pos+T-1 (q: T x n_heads*hd in place,
@@ -1835,13 +1842,13 @@ extern "C" int gq_hip_chat_turn(gq_ctx *c, const int32_t *tokens, int n_tokens, 
   return n;
 }
 
-/* Q6_K weights the prefill GEMM can read in its step layout (cols % 2048):
+/* Q6_K weights the prefill GEMM can read in the unit layout (cols % 2048):
  * a copy for the call, as a bound model keeps from gq_hip_model_bind;
  * matvec path 3 keeps the reference layout.  Freed by the caller. */
-static const uint8_t *op_steps(gq_ctx *c, int dtype, const void *w, int rows, int cols) {
+static const uint8_t *op_units(gq_ctx *c, int dtype, const void *w, int rows, int cols) {
   if (dtype != GQ_Q6_K || cols % 2048 || gq_matvec_q6k_ref()) return nullptr;
-  uint8_t *d = (uint8_t *)dev_alloc(c, gq_q6k_steps_bytes(rows, cols));
-  if (d && gq_launch_q6k_steps(d, w, rows, cols, c->stream)) {
+  uint8_t *d = (uint8_t *)dev_alloc(c, gq_q6k_units_bytes(rows, cols));
+  if (d && gq_launch_q6k_units(d, w, rows, cols, c->stream)) {
     gq_hip_free(c, d);
     return nullptr;
   }
@@ -1849,7 +1856,7 @@ static const uint8_t *op_steps(gq_ctx *c, int dtype, const void *w, int rows, in
 }
 
 static PgSeg op_seg(const uint8_t *ps, const void *w, float *y, int n, int dtype) {
-  return ps ? PgSeg{ps, y, n, GQ_Q6_KP} : PgSeg{(const uint8_t *)w, y, n, dtype};
+  return ps ? PgSeg{ps, y, n, GQ_Q6_KX} : PgSeg{(const uint8_t *)w, y, n, dtype};
 }
 
 /* fp32 x -> the bf16 copy the GEMM reads */
@@ -1869,7 +1876,7 @@ extern "C" int gq_hip_prefill_gemm_dev(gq_ctx *c, int dtype, int mode, const voi
   if (n % 128) return fail(c, -1, "prefill GEMM: rows must be a multiple of 128");
   PgArgs a{};
   if (!(a.x = pf_x16(c, x, (size_t)t * k))) return fail(c, -4, "prefill GEMM: x conversion");
-  const uint8_t *ps = op_steps(c, dtype, w, n, k);
+  const uint8_t *ps = op_units(c, dtype, w, n, k);
   a.T = t, a.K = k, a.nseg = 1, a.seg[0] = op_seg(ps, w, y, n, dtype);
   pf_parts(c, a);
   if (mode == 1 && r != y)
@@ -1887,7 +1894,7 @@ extern "C" float gq_hip_time_prefill_gemm(gq_ctx *c, int dtype, const void *w, i
   if (k % 256 || (dtype == GQ_Q6_K && k % 512) || n % 128) return fail(c, -2, "time GEMM: shape"), -1.f;
   PgArgs a{};
   if (!(a.x = pf_x16(c, x, (size_t)t * k))) return fail(c, -4, "time GEMM: x conversion"), -1.f;
-  const uint8_t *ps = op_steps(c, dtype, w, n, k);
+  const uint8_t *ps = op_units(c, dtype, w, n, k);
   a.T = t, a.K = k, a.nseg = 1, a.seg[0] = op_seg(ps, w, y, n, dtype);
   pf_parts(c, a);
   EventPair ev;
@@ -1916,7 +1923,7 @@ extern "C" int gq_hip_prefill_gate_up_dev(gq_ctx *c, int dtype, const void *w_ga
   if (n % 64) return fail(c, -1, "prefill gate/up: rows must be a multiple of 64");
   PgArgs a{};
   if (!(a.x = pf_x16(c, x, (size_t)t * k))) return fail(c, -4, "prefill gate/up: x conversion");
-  const uint8_t *pg = op_steps(c, dtype, w_gate, n, k), *pu = pg ? op_steps(c, dtype, w_up, n, k) : nullptr;
+  const uint8_t *pg = op_units(c, dtype, w_gate, n, k), *pu = pg ? op_units(c, dtype, w_up, n, k) : nullptr;
   if (pg && !pu) gq_hip_free(c, (void *)pg), pg = nullptr;
   a.T = t, a.K = k, a.nseg = 2, a.act = (__bf16 *)act;
   a.seg[0] = op_seg(pg, w_gate, nullptr, n, dtype);

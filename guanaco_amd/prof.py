@@ -166,7 +166,7 @@ def config5(ctx, T=512, iters=20):
             y = ctx.alloc(4 * T * N)
 
             # device time of the GEMM launches alone (x's bf16 copy and the
-            # Q6_K step-layout copy made before the timed region)
+            # Q6_K unit-layout copy made before the timed region)
             ms = H.lib.gq_hip_time_prefill_gemm(ctx.h, dt, w.ptr, N, K, x.ptr, T, y.ptr, iters)
             if ms < 0:
                 ctx.raise_last("time_prefill_gemm")

@@ -323,14 +323,14 @@ int gq_hip_silu_mul_dev(gq_ctx *ctx, float *gate, const float *up, int n);
  * x: T x cols fp32, y: T x rows fp32, device pointers.  mode 0 stores, mode 1 adds r (T x rows, may alias y).
  * x and the dequantized weights are rounded to bf16 (nearest even) before
  * the products.  Q6_K weights with cols % 2048 == 0 are read through a
- * step-layout copy made for the call (a bound model keeps its copies from
+ * unit-layout copy made for the call (a bound model keeps its copies from
  * gq_hip_model_bind); results equal the reference layout's bit for bit.
  * Asynchronous on the context stream. */
 int gq_hip_prefill_gemm_dev(gq_ctx *ctx, int dtype, int mode, const void *w, int rows, int cols,
                             const float *x, int T, float *y, const float *r);
 /* Average device time (ms) of n_iter back-to-back launches of that GEMM
  * (mode 0), timed with HIP events on the context stream; the bf16 copy of
- * x and any Q6_K step-layout copy are made before the timed region.  No
+ * x and any Q6_K unit-layout copy are made before the timed region.  No
  * reference counterpart: a measurement entry, as gq_hip_time_matvec. */
 float gq_hip_time_prefill_gemm(gq_ctx *ctx, int dtype, const void *w, int rows, int cols, const float *x, int T,
                                float *y, int n_iter);

@@ -127,7 +127,7 @@ def _gemm_case(ctx, orc, dtype, T, N, K, mode):
     (S.Q4_K, 14336, 4096, 0),   # gate / up
     (S.Q4_K, 4096, 14336, 1),   # down + residual
     (S.Q6_K, 4096, 14336, 1),   # the Q6_K down of the Q4_K_M mix
-    (S.Q6_K, 14336, 4096, 0),   # Q6_K gate / up: 128-token tiles from the step layout
+    (S.Q6_K, 14336, 4096, 0),   # Q6_K gate / up: 128-token tiles from the unit layout
 ])
 def test_prefill_gemm_config5_shapes(ctx, orc, dtype, N, K, mode):
     """Config 5's full 512-token GEMMs on the 8B projection shapes; every
@@ -306,12 +306,14 @@ def test_prefill_model_vs_oracle(ctx, orc, pre, T, ms):
 
 
 @pytest.mark.parametrize("T,N,K,mode", [(96, 256, 4096, 0), (77, 384, 2048, 1), (512, 4096, 14336, 1)])
-def test_prefill_q6k_step_layout_bit_identical(ctx, orc, T, N, K, mode):
+def test_prefill_q6k_unit_layout_vs_reference_layout(ctx, orc, T, N, K, mode):
     """Q6_K weights whose rows fall on 16-byte boundaries (K % 2048 == 0) go
-    through the GEMM in the step layout (a copy made per call here, at model
-    bind for a bound model): the same bf16 weights in the same K order as the
-    reference layout, so the outputs are bit-identical to those of matvec
-    path 3, which reads the reference layout."""
+    through the GEMM in the decode matvec's unit layout (a copy made per call
+    here; a bound model reads the copy model bind made for the decode step):
+    the same bf16 weights as the reference layout, which matvec path 3
+    reads, summed in another K order.  The two agree to the accumulation
+    order (1e-5, as against the exact-input reference) and are not the same
+    bits, so the unit layout was read."""
     import guanaco_amd.hip as H
     seed = 0x5E9 ^ (T << 16) ^ (N << 4) ^ K
     w = orc.synth_quant(S.Q6_K, seed, N, K)
@@ -327,16 +329,19 @@ def test_prefill_q6k_step_layout_bit_identical(ctx, orc, T, N, K, mode):
         out[path] = yd.download(count=T * N)
         yd.free()
     assert np.abs(out["auto"]).sum() > 0
-    assert np.array_equal(bits(out["auto"]), bits(out["auto_q6k_ref"]))
+    assert rel_l2(out["auto"], out["auto_q6k_ref"]) < 1e-5
+    assert not np.array_equal(bits(out["auto"]), bits(out["auto_q6k_ref"]))
     H.lib.gq_hip_free(ctx.h, wd)
     xd.free()
 
 
-def test_prefill_q6k_step_layout_model(orc):
+def test_prefill_q6k_unit_layout_model(orc):
     """A model whose Q6_K projections (v, o, down) have K % 2048 == 0 prefills
-    from the step-layout copies made at model bind: logits and the last hidden
-    state bit-identical to the reference layout (matvec path 3), and the
-    prompt against the oracle as for the other models."""
+    from the unit-layout copies made at model bind (the down projection's is
+    the decode step's own): logits and the last hidden state within 2e-3 of
+    the reference layout's (matvec path 3; the K order of the sums differs,
+    and the bf16 activations may round apart), and the prompt against the
+    oracle as for the other models, on both."""
     import guanaco_amd.hip as H
     from oracle import HostModel
     spec = S.ModelSpec("q6k-steps-test", n_layers=2, hidden=2048, ff=4096, n_heads=16, n_kv_heads=4, vocab=1000,
@@ -351,11 +356,12 @@ def test_prefill_q6k_step_layout_model(orc):
             with H.matvec_path(path):
                 res[path] = dm.prefill(toks, 0, want_hidden=True)
         (nxt, lg, hg, _), (nxt2, lg2, hg2, _) = res["auto"], res["auto_q6k_ref"]
-        assert nxt == nxt2 and np.array_equal(bits(lg), bits(lg2)) and np.array_equal(bits(hg), bits(hg2))
+        assert rel_l2(lg, lg2) < 2e-3 and rel_l2(hg, hg2) < 2e-3
         kv = hm.new_kv()
         for t in range(len(toks)):
             t_cpu, lc, _ = hm.forward(kv, int(toks[t]), t)
-        assert rel_l2(lg, lc) < PF_TOL and nxt == t_cpu
+        assert rel_l2(lg, lc) < PF_TOL and rel_l2(lg2, lc) < PF_TOL and nxt == t_cpu and nxt2 == t_cpu
+        print(f"unit layout vs reference layout: logits {rel_l2(lg, lg2):.2e}, hidden {rel_l2(hg, hg2):.2e}")
     finally:
         c.close()
 
