@@ -9,9 +9,13 @@ advanced by the prompt and the reply (the last sampled token counted, not
 fed), and a restart at position 0 with BOS when a turn would not fit
 (:169-190).  The device side drives gq_hip_chat_turn with the same inputs
 and restarts on its -6.  Three turns (the third restarts the conversation)
-on four layers of the TinyLlama-shape Q8_0 model, whose greedy tokens vary
-from step to step; an EOS token taken from the third turn's reply (and found nowhere
-before it) stops that turn early.  Every reference forward() stays inside
+on four layers of the TinyLlama-shape Q8_0 model and of the zero-mean
+Q4_K_M one, whose greedy tokens vary from step to step; an EOS token taken
+from the third turn's reply (and found nowhere before it) stops that turn
+early.  The prompts run in prefill mode 1, token by token through the fp32
+decode step (the reference's precision), where token parity is claimed;
+prefill mode 0 (the bf16 prompt GEMM) is run too, for the positions and
+the reply lengths, its token agreement printed.  Every reference forward() stays inside
 the cache: chat.c's reply loop does not stop at max_seq, and the reference
 engine asserts there (engine.c:422).  The reply tokens and the positions
 after every turn must be identical."""
@@ -78,10 +82,12 @@ def device_chat(dm, turns, eos):
     return log
 
 
-def test_chat_three_turns_vs_reference(ref, orc):
+@pytest.mark.parametrize("base", ["q8_0", "q4_k_m"])
+def test_chat_three_turns_vs_reference(ref, orc, base):
     import guanaco_amd.hip as H
     from oracle import HostModel, RefModel
-    spec = dataclasses.replace(S.TINYLLAMA_Q8, name="chat-q8_0-4-layers", n_layers=4)
+    spec = dataclasses.replace(S.TINYLLAMA_Q8 if base == "q8_0" else S.TINYLLAMA_ZM, name=f"chat-{base}-4-layers",
+                               n_layers=4)
     rng = np.random.default_rng(5)
     turns = [rng.integers(3, spec.vocab, 20) for _ in range(3)]
     hm = HostModel(orc, spec, MAX_SEQ)
@@ -99,10 +105,17 @@ def test_chat_three_turns_vs_reference(ref, orc):
     assert cpu[:2] == plain[:2] and cpu[2][1][-1] == eos and len(cpu[2][1]) < MAX_TOKENS
     with H.Context(0) as ctx:
         dm = H.DeviceModel(ctx, spec, MAX_SEQ)
+        assert H.lib.gq_hip_set_prefill_mode(ctx.h, 1) == 0
         dev = device_chat(dm, turns, eos)
+        assert H.lib.gq_hip_set_prefill_mode(ctx.h, 0) == 1
+        gemm = device_chat(dm, turns, -1)
     for t, (c, d) in enumerate(zip(cpu, dev)):
         print(f"turn {t}: reference pos {c[0]} reply {c[1]}; device pos {d[0]}")
         assert d[0] == c[0] and d[1] == c[1], t
+    for t, (c, d) in enumerate(zip(plain, gemm)):
+        same = sum(a == b for a, b in zip(c[1], d[1]))
+        print(f"turn {t}, bf16 prompt GEMM: pos {d[0]}, {same} of {len(c[1])} reply tokens as the reference's")
+        assert d[0] == c[0] and len(d[1]) == len(c[1]) and all(0 <= x < spec.vocab for x in d[1]), t
 
 
 def test_chat_turn_rejects(ctx):
