@@ -248,6 +248,11 @@ int gq_launch_sample(const float *logits, int vocab, float temperature, int top_
                      const SampleWs &ws, int *out, hipStream_t s);
 int gq_launch_silu_mul(float *gate, const float *up, int n, hipStream_t s);
 int gq_launch_copy(void *dst, const void *src, size_t bytes, int n_cu, hipStream_t s);
+/* Read bytes (a multiple of 16, 16-byte aligned) from src and store nothing:
+ * at most sink_n workgroups of eight 16-byte loads per thread per pass
+ * (sink: sink_n words the kernel only writes in a case that does not occur
+ * in practice). */
+int gq_launch_stream_read(const void *src, size_t bytes, uint32_t *sink, size_t sink_n, hipStream_t s);
 
 /* ---- prefill chunk ---------------------------------------------------
  * Y[T][rows] = X[T][K] . W^T on the bf16 matrix cores for up to three weight

@@ -1933,6 +1933,31 @@ extern "C" int gq_hip_prefill_gate_up_dev(gq_ctx *c, int dtype, const void *w_ga
   return rc ? fail(c, rc, "prefill gate/up launch") : 0;
 }
 
+extern "C" float gq_hip_time_read(gq_ctx *c, const void *src, size_t bytes, size_t stride, int n_buf, int n_iter) {
+  if (!c || !src || !bytes || n_buf <= 0 || n_iter <= 0 || (bytes & 15) || (stride & 15) ||
+      (n_buf > 1 && stride < bytes))
+    return fail(c, -1, "time read: bad argument"), -1.f;
+  constexpr size_t kSink = 4096;
+  uint32_t *sink = (uint32_t *)dev_alloc(c, sizeof(uint32_t) * kSink);
+  if (!sink) return fail(c, -4, "time read: sink"), -1.f;
+  const uint8_t *base = (const uint8_t *)src;
+  EventPair ev;
+  int rc = ev.create() == hipSuccess ? 0 : -4;
+  if (!rc) rc = gq_launch_stream_read(base, bytes, sink, kSink, c->stream); /* untimed first launch */
+  if (!rc) (void)hipEventRecord(ev.e0, c->stream);
+  for (int i = 0; i < n_iter && !rc; i++)
+    rc = gq_launch_stream_read(base + (size_t)((i + 1) % n_buf) * stride, bytes, sink, kSink, c->stream);
+  float ms = 0.f;
+  if (!rc) {
+    (void)hipEventRecord(ev.e1, c->stream);
+    (void)hipEventSynchronize(ev.e1);
+    ms = ev.ms();
+  }
+  gq_hip_free(c, sink);
+  if (rc) return fail(c, rc, "time read launch"), -1.f;
+  return ms / n_iter;
+}
+
 extern "C" int gq_hip_copy_dev(gq_ctx *c, void *dst, const void *src, size_t bytes) {
   if (!c || !dst || !src) return -1;
   const int rc = gq_launch_copy(dst, src, bytes, c->n_cu, c->stream);

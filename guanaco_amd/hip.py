@@ -92,6 +92,7 @@ def _load():
         "gq_hip_argmax_dev": (C.c_int, [_vp, _vp, C.c_int, _vp]),
         "gq_hip_silu_mul_dev": (C.c_int, [_vp, _vp, _vp, C.c_int]),
         "gq_hip_copy_dev": (C.c_int, [_vp, _vp, _vp, C.c_size_t]),
+        "gq_hip_time_read": (C.c_float, [_vp, _vp, C.c_size_t, C.c_size_t, C.c_int, C.c_int]),
         "gq_hip_time_prefill_gemm": (C.c_float, [_vp, C.c_int, _vp, C.c_int, C.c_int, _vp, C.c_int, _vp, C.c_int]),
         "gq_hip_prefill_gemm_dev": (C.c_int, [_vp, C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp,
                                               C.c_int, _vp, _vp]),

@@ -30,6 +30,11 @@
         pageable host memory (gq_hip_upload_weight's pinned staging): GB/s,
         and hipMemGetInfo before, while resident and after gq_hip_destroy.
 
+    python3 -m guanaco_amd.prof floor --iters 64
+        a read-only streaming kernel (gq_hip_time_read) launched once per size
+        over a 2 GiB buffer: the time one launch needs just to read the bytes
+        each decode kernel moves, and a 1-512 MiB sweep.
+
     python3 -m guanaco_amd.prof sample --vocab 128256 --iters 50
         on-device sampling (gq_hip_sample_dev) of N(0, 3^2) logits already
         in HBM: greedy, top-k 40, top-p 0.9 and plain temperature, each the
@@ -69,6 +74,36 @@ def run_copy(mib, iters):
 
 def emit(**kw):
     print(json.dumps(kw), flush=True)
+
+
+# algorithmic bytes per launch of the decode step's kernels on the 8B shape at
+# ctx 8192 (the figures bench.py's roofline uses)
+DECODE_BYTES = [("q/k/v (even layers)", 15278080), ("q/k/v (odd layers)", 14196736), ("o", 9486336),
+                ("gate/up", 66134016), ("down Q6_K", 48259072), ("down Q4_K", 33120256),
+                ("attention K/V at ctx 8192", 67133440), ("LM head", 431408128)]
+
+
+def run_floor(iters):
+    """One launch of the read-only streaming kernel per size, rotating over
+    a 2 GiB buffer so that every launch reads HBM (up to 128 regions, each
+    2 MiB-aligned): the time a single launch needs just to read that many
+    bytes, at the decode kernels' sizes and on a sweep."""
+    ctx = H.Context(0)
+    span = 2 << 30
+    buf = ctx.alloc(span)
+    sizes = [(name, b) for name, b in DECODE_BYTES]
+    sizes += [(f"{m} MiB", m << 20) for m in (1, 2, 4, 8, 16, 32, 64, 128, 256, 512)]
+    for name, b in sizes:
+        b16 = (b + 15) // 16 * 16
+        stride = (b16 + (2 << 20) - 1) // (2 << 20) * (2 << 20)
+        n_buf = max(1, min(128, span // stride))
+        ms = H.lib.gq_hip_time_read(ctx.h, buf.ptr, b16, stride, n_buf, iters)
+        if ms < 0:
+            ctx.raise_last("time_read")
+        emit(what=f"read-only stream, {name}", bytes=b16, regions=n_buf, us_per_launch=round(ms * 1e3, 2),
+             GB_per_s=round(b16 / ms / 1e6, 1), frac_of_8TB=round(b16 / ms / 1e6 / 8000, 3))
+    buf.free()
+    ctx.close()
 
 
 def config1(ctx, nbuf=48, iters=96):
@@ -325,6 +360,8 @@ def main():
     smp.add_argument("--iters", type=int, default=50)
     sub.add_parser("config5")
     sub.add_parser("upload")
+    fl = sub.add_parser("floor")
+    fl.add_argument("--iters", type=int, default=64)
     g = sub.add_parser("gemm")
     g.add_argument("--dtype", type=int, default=S.Q4_K)
     g.add_argument("--rows", type=int, default=4096)
@@ -342,6 +379,8 @@ def main():
         config5(H.Context(0))
     elif a.cmd == "upload":
         run_upload()
+    elif a.cmd == "floor":
+        run_floor(a.iters)
     elif a.cmd == "gemm":
         run_gemm(a.dtype, a.rows, a.cols, a.tokens, a.iters)
 

@@ -390,6 +390,15 @@ int gq_hip_set_prefill_mode(gq_ctx *ctx, int mode);
  * multiples of 16), asynchronous.  No reference counterpart: the known-size
  * workload that scales the HBM byte counters of the profiles. */
 int gq_hip_copy_dev(gq_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Average device time (ms) of one launch of a read-only streaming kernel
+ * over `bytes` (a multiple of 16): eight 16-byte loads per thread issued
+ * before use, nothing stored.  Launch i reads src + (i mod n_buf) * stride,
+ * so src must hold (n_buf - 1) * stride + bytes bytes (stride >= bytes when
+ * n_buf > 1, a multiple of 16); 1 untimed + n_iter timed launches between
+ * HIP events on the context stream.  No reference counterpart: the floor a
+ * single launch reading that many bytes reaches, beside which the decode
+ * kernels' durations are set (-1 on a bad argument). */
+float gq_hip_time_read(gq_ctx *ctx, const void *src, size_t bytes, size_t stride, int n_buf, int n_iter);
 
 #ifdef __cplusplus
 }

@@ -169,3 +169,19 @@ def test_copy_kernel(ctx):
     assert np.array_equal(dst.download(count=n // 4), np.arange(n // 4, dtype=np.float32))
     assert H.lib.gq_hip_copy_dev(ctx.h, dst.ptr, src.ptr, 8) == -1  # not a multiple of 16
     src.free(), dst.free()
+
+
+def test_time_read_floor_kernel(ctx):
+    """gq_hip_time_read: the read-only streaming kernel behind the single-
+    launch floor of the profiles.  It times launches over rotating regions
+    (a 3 MiB + 48 B region, not a multiple of the grid's pass) and rejects
+    sizes that are not multiples of 16 and regions that overlap."""
+    import guanaco_amd.hip as H
+    buf = ctx.upload(np.arange(4 << 20, dtype=np.float32))  # 16 MiB
+    n = (3 << 20) + 48
+    ms = H.lib.gq_hip_time_read(ctx.h, buf.ptr, n, 4 << 20, 4, 8)
+    assert ms > 0, ms
+    assert H.lib.gq_hip_time_read(ctx.h, buf.ptr, 1000, 0, 1, 4) < 0           # not a multiple of 16
+    assert H.lib.gq_hip_time_read(ctx.h, buf.ptr, 4 << 20, 2 << 20, 2, 4) < 0  # regions overlap
+    assert np.array_equal(buf.download(count=16), np.arange(16, dtype=np.float32))  # nothing stored
+    buf.free()
