@@ -635,6 +635,8 @@ void plan(int dt, int mode, const MvArgs &a, int total, MxPlan &p, int &r, int &
     r = 4;
   else if (dt == GQ_Q6_K && total >= 4096)
     r = 6; /* 8 rows of Q6_K quants do not fit 128 VGPRs */
+  else if (mode == MV_STORE && a.rope.cs)
+    r = 4; /* the decode step's q/k/v launch: twice the workgroups (768 at the 8B shape) */
   else
     r = total >= 4096 ? 8 : 4;
   if (mode != MV_SWIGLU && a.nseg > 1) { /* groups must not straddle segments */
@@ -830,11 +832,8 @@ int gq_launch_matvec_pair(int dt0, const MvArgs &a0, int dt1, const MvArgs &a1, 
     return hipGetLastError() == hipSuccess ? 0 : -4;
   };
   if (!a0.norm_w != !a1.norm_w) return 1;
-  const bool big = t0 >= 4096, nrm = a0.norm_w != nullptr;
   if (sw0 != 16) return 1;
-  if (nrm)
-    return big ? launch(mvx_pair_kernel<GQ_Q4_K, 8, GQ_Q6_K, 4, 16, 256, kNorm>, 8, 4)
-               : launch(mvx_pair_kernel<GQ_Q4_K, 4, GQ_Q6_K, 4, 16, 256, kNorm>, 4, 4);
-  return big ? launch(mvx_pair_kernel<GQ_Q4_K, 8, GQ_Q6_K, 4, 16, 256, 0>, 8, 4)
-             : launch(mvx_pair_kernel<GQ_Q4_K, 4, GQ_Q6_K, 4, 16, 256, 0>, 4, 4);
+  /* 4-row groups on both sides, as plan() gives the q/k/v launch */
+  if (a0.norm_w) return launch(mvx_pair_kernel<GQ_Q4_K, 4, GQ_Q6_K, 4, 16, 256, kNorm>, 4, 4);
+  return launch(mvx_pair_kernel<GQ_Q4_K, 4, GQ_Q6_K, 4, 16, 256, 0>, 4, 4);
 }
