@@ -637,6 +637,8 @@ void plan(int dt, int mode, const MvArgs &a, int total, MxPlan &p, int &r, int &
     r = 6; /* 8 rows of Q6_K quants do not fit 128 VGPRs */
   else if (mode == MV_STORE && a.rope.cs)
     r = 4; /* the decode step's q/k/v launch: twice the workgroups (768 at the 8B shape) */
+  else if (mode == MV_RESID && a.cols <= 4096)
+    r = 4; /* the o projection + residual: 512 workgroups at the 8B shape */
   else
     r = total >= 4096 ? 8 : 4;
   if (mode != MV_SWIGLU && a.nseg > 1) { /* groups must not straddle segments */
