@@ -93,12 +93,14 @@ __global__ __launch_bounds__(kThreads) void rope_append_kernel(RopeArgs a) {
 }
 
 /* Positions per split-K chunk (one workgroup), chosen by the cache
- * capacity.  64 gives 1024 workgroups at the 8B shape and ctx 8192, four per
- * CU, whose load and compute phases overlap each other (measured 1.3% faster
- * per decode step than 128, the same as 32).  Past 12288 positions the merge,
- * which reads every chunk's partials, grows enough that 128 wins (16384:
- * 32.7 vs 34.7 us per layer; 32768: 57.0 vs 61.9). */
-int chunk_for(int max_seq) { return max_seq > 12288 ? 128 : 64; }
+ * capacity.  32 gives 2080 workgroups at the 8B shape and ctx 8192 (79
+ * VGPRs, six waves per SIMD): measured in the graph-replayed decode step
+ * 0.9% faster than 64 (four workgroups per CU), although the attention op
+ * alone, launched back to back, is 0.4 us slower; 64 had in turn measured
+ * 1.3% faster per step than 128.  Past 12288 positions the merge, which
+ * reads every chunk's partials, grows enough that 128 wins (16384: 32.7 vs
+ * 34.7 us per layer with 64; 32768: 57.0 vs 61.9). */
+int chunk_for(int max_seq) { return max_seq > 12288 ? 128 : 32; }
 
 /* Workgroup (g, c) handles positions [Sc, Sc + S) of KV head g for the G
  * query heads sharing it.  Every K and V load of the chunk is issued before
@@ -281,7 +283,7 @@ int launch_partial(const AttnArgs &a, hipStream_t s) {
   if (a.s_max == 128)
     hipLaunchKernelGGL((attn_partial_kernel<HD, G, 128>), dim3(a.n_kv, a.nch), dim3(kThreads), 0, s, a);
   else
-    hipLaunchKernelGGL((attn_partial_kernel<HD, G, 64>), dim3(a.n_kv, a.nch), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL((attn_partial_kernel<HD, G, 32>), dim3(a.n_kv, a.nch), dim3(kThreads), 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 

@@ -279,7 +279,7 @@ int gq_hip_attention_dev(gq_ctx *ctx, int layer, int pos, int n_heads, const flo
  * hipMalloc).  The split-K partials go to a static 8 MiB device array that
  * the library holds on every GPU it runs on until the process ends, so the
  * call allocates nothing.  They take n_heads x nch x (head_dim + 2) floats,
- * nch = ceil(max_seq / 64) up to max_seq 12288 and ceil(max_seq / 128) past
+ * nch = ceil(max_seq / 32) up to max_seq 12288 and ceil(max_seq / 128) past
  * it (the 8B shape fits up to max_seq 64512); -1 with an error message when
  * they do not fit.  Every call on one GPU shares that array and leaves its
  * partials there: calls that overlap on one GPU (other streams or contexts
