@@ -266,7 +266,9 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(AttnArgs a) {
   const int d = blockIdx.y * kMergeDims + tid % kMergeDims, cg = tid / kMergeDims;
   const float *o = a.part_o + (size_t)h * a.nch * a.hd + d;
   float acc = 0.f;
-#pragma unroll 8
+  /* unrolled so a thread's ~16 chunk loads (260 chunks at ctx 8192 over 16
+   * chunk groups) go out in one batch: decode +0.4% against unroll 8 */
+#pragma unroll 16
   for (int c = cg; c < nc; c += NG) acc = __builtin_fmaf(gld<float>(o + (size_t)c * a.hd), sw[c], acc);
   sacc[cg][tid % kMergeDims] = acc;
   __syncthreads();
