@@ -19,7 +19,9 @@
  * reads the quants of 8 whole blocks of a row; rows of more than 1024 units
  * loop over column tiles.  Measured against a plain streaming-read kernel on
  * MI355X this layout was 1.5x faster than staging x in LDS per workgroup for
- * the long rows of the down projection (x re-reads were the cost).
+ * the long rows of the down projection (x re-reads were the cost).  Where a
+ * workgroup holds two or more row groups of one column tile, they split the x
+ * loads and share the unit through LDS instead (kShx below).
  *
  * Per unit and row a lane decodes only what its 32 weights need.  Q4_K lanes
  * share the 16-byte block header: each of the 8 lanes of a block loads one of
@@ -352,9 +354,18 @@ __device__ __forceinline__ float seg_sum(float v) {
  * more than one column tile (cols > 32768): both compile-time, a runtime
  * branch or loop around the loads measured 0.6-2 us slower. */
 constexpr int kNorm = 1, kMT = 2;
+/* SHX: launches of two or more row groups (G >= 2, so L <= 128) share x
+ * (times the norm weights) through LDS: groups 0 and 1 load the low and the
+ * high half of each unit, every group reads the whole unit back.  With every
+ * group loading its own copy the 8B q/k/v launch took 8.5 us (49 MB of
+ * L2-to-CU reads at 768 workgroups) and o 5.1; shared, 7.5 and 4.65, and the
+ * graph-replayed decode step 499 -> 509 tok/s. */
+constexpr int kShx = 4;
+constexpr int kShxLanes = 128; /* xsh: 8 float4 per lane, lane-major rows */
 
 template <int DT, int MODE, int R, int SEGW, bool UNI, int FL>
-__device__ __forceinline__ void mvx_body(const MvArgs &a, const MxPlan &p, int bid, float *red, float2 *scs) {
+__device__ __forceinline__ void mvx_body(const MvArgs &a, const MxPlan &p, int bid, float *red, float2 *scs,
+                                         float4 *xsh) {
 #pragma clang fp contract(off)
   using T = Ux<DT>;
   static_assert(R % 2 == 0, "row pairs (RoPE, SwiGLU) stay inside a group");
@@ -389,7 +400,8 @@ __device__ __forceinline__ void mvx_body(const MvArgs &a, const MxPlan &p, int b
    * and their addresses are wave-uniform (scalar registers) */
   const int g = UNI ? __builtin_amdgcn_readfirstlane(tid / L) : tid / L;
   const int ul = tid - g * L;
-  constexpr bool norm = (FL & kNorm) != 0, MT = (FL & kMT) != 0;
+  constexpr bool norm = (FL & kNorm) != 0, MT = (FL & kMT) != 0, SHX = (FL & kShx) != 0;
+  static_assert(!(SHX && MT), "shared x covers one column tile");
 #define GQ_SEL3(s, a0, a1, a2) ((s) == 0 ? (a0) : (s) == 1 ? (a1) : (a2))
 #define GQ_LOCATE(gr, s, lr)                                                                                \
   do {                                                                                                      \
@@ -447,14 +459,26 @@ __device__ __forceinline__ void mvx_body(const MvArgs &a, const MxPlan &p, int b
       /* x slices first (their latency hides under the rows'), then every
        * row's quants */
       const int c0 = act ? T::col(u) : 0;
-      float4 xl[4], xh[4];
+      float4 xl[4], xh[4], wv[4];
+      if constexpr (SHX) { /* this group's half: x in xl, norm weights in wv */
+        if (g < 2) {
+          const int cb = c0 + (g ? T::XHI : 0);
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        xl[i] = gld<float4>(xp + c0 + 4 * i);
-        xh[i] = gld<float4>(xp + c0 + T::XHI + 4 * i);
-        if (!act) xl[i] = xh[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+          for (int i = 0; i < 4; i++) xl[i] = gld<float4>(xp + cb + 4 * i);
+          if constexpr (norm) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) wv[i] = gld<float4>(nw + cb + 4 * i);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          xl[i] = gld<float4>(xp + c0 + 4 * i);
+          xh[i] = gld<float4>(xp + c0 + T::XHI + 4 * i);
+          if (!act) xl[i] = xh[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
       }
-      if constexpr (norm) { /* y = r * W (w .* x): raw sum of squares, x times w */
+      if constexpr (norm && !SHX) { /* y = r * W (w .* x): raw sum of squares, x times w */
         float4 wl[4], wh[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -492,6 +516,31 @@ __device__ __forceinline__ void mvx_body(const MvArgs &a, const MxPlan &p, int b
         epos = rpd ? gq_sld<int>(rpd) : rpos;
         if (tid < (hd >> 1) && epos >= 0 && epos < msq) cs_pre = gld<float2>(rcs + (size_t)epos * (hd >> 1) + tid);
       }
+      if constexpr (SHX) {
+        if (g < 2) {
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            float4 v = act ? xl[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            if constexpr (norm) {
+              ss = __builtin_fmaf(v.x, v.x, ss);
+              ss = __builtin_fmaf(v.y, v.y, ss);
+              ss = __builtin_fmaf(v.z, v.z, ss);
+              ss = __builtin_fmaf(v.w, v.w, ss);
+              v = make_float4(v.x * wv[i].x, v.y * wv[i].y, v.z * wv[i].z, v.w * wv[i].w);
+            }
+            xsh[(4 * g + i) * kShxLanes + ul] = v;
+          }
+        }
+        /* LDS only: the rows' loads stay in flight across this barrier */
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          xl[i] = xsh[i * kShxLanes + ul];
+          xh[i] = xsh[(4 + i) * kShxLanes + ul];
+        }
+      }
       if (!act) continue;
       const float sxl = (sum4(xl[0]) + sum4(xl[1])) + (sum4(xl[2]) + sum4(xl[3]));
       const float sxh = (sum4(xh[0]) + sum4(xh[1])) + (sum4(xh[2]) + sum4(xh[3]));
@@ -528,7 +577,10 @@ __device__ __forceinline__ void mvx_body(const MvArgs &a, const MxPlan &p, int b
   float rs = 1.f;
   if constexpr (norm) { /* 1/sqrt(mean(x^2) + eps) (kernels_cpu.c:242-253) */
     float tot = 0.f;
-    for (int s = 0; s < spg; s++) tot += rr[s * NV + R];
+    if constexpr (SHX) /* groups 0 and 1 summed the halves of x */
+      for (int s = 0; s < 2 * spg; s++) tot += red[s * NV + R];
+    else
+      for (int s = 0; s < spg; s++) tot += rr[s * NV + R];
     tot = tot / (float)cols;
     tot = tot + eps;
     rs = 1.0f / sqrtf(tot);
@@ -583,7 +635,8 @@ template <int DT, int MODE, int R, int SEGW, int MAXNT, bool UNI, int FL>
 __global__ __launch_bounds__(MAXNT) void mvx_kernel(MvArgs a, MxPlan p) {
   __shared__ float red[(MAXNT / SEGW) * (R + 1)];
   __shared__ float2 scs[MODE == MV_STORE ? 256 : 1]; /* RoPE row (head_dim <= 512) */
-  mvx_body<DT, MODE, R, SEGW, UNI, FL>(a, p, blockIdx.x, red, scs);
+  __shared__ float4 xsh[(FL & kShx) ? 8 * kShxLanes : 1];
+  mvx_body<DT, MODE, R, SEGW, UNI, FL>(a, p, blockIdx.x, red, scs, xsh);
 }
 
 /* Two MV_STORE launches of different dtypes over the same x in one grid:
@@ -593,12 +646,13 @@ template <int DT0, int R0, int DT1, int R1, int SEGW, int MAXNT, int FL>
 __global__ __launch_bounds__(MAXNT) void mvx_pair_kernel(MvArgs a0, MxPlan p0, MvArgs a1, MxPlan p1) {
   __shared__ float red[(MAXNT / SEGW) * ((R0 > R1 ? R0 : R1) + 1)];
   __shared__ float2 scs[256];
+  __shared__ float4 xsh[(FL & kShx) ? 8 * kShxLanes : 1];
   /* the second launch's workgroups first: its (Q6_K) rows cost more each,
    * so they do not form the tail */
   if ((int)blockIdx.x < p1.nwg)
-    mvx_body<DT1, MV_STORE, R1, SEGW, true, FL>(a1, p1, blockIdx.x, red, scs);
+    mvx_body<DT1, MV_STORE, R1, SEGW, true, FL>(a1, p1, blockIdx.x, red, scs, xsh);
   else
-    mvx_body<DT0, MV_STORE, R0, SEGW, true, FL>(a0, p0, (int)blockIdx.x - p1.nwg, red, scs);
+    mvx_body<DT0, MV_STORE, R0, SEGW, true, FL>(a0, p0, (int)blockIdx.x - p1.nwg, red, scs, xsh);
 }
 
 /* 0: this kernel for every launch; 1 (default): the matrix-core kernel for
@@ -672,14 +726,20 @@ int launch_one(const MvArgs &a, const MxPlan &p, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
-/* the RMSNorm flag: only launches that take it (STORE, SWIGLU) */
+/* the RMSNorm flag: only launches that take it (STORE, SWIGLU); shared x
+ * for launches of two or more row groups (plan() gives those 256 threads) */
 template <int DT, int MODE, int R, int SEGW, int MAXNT, int FL>
 int launch_fl(const MvArgs &a, const MxPlan &p, hipStream_t s) {
+  constexpr bool shx = !(FL & kMT) && MAXNT == 256;
   if constexpr (MODE != MV_RESID) {
+    if constexpr (shx)
+      if (a.norm_w && p.G >= 2) return launch_one<DT, MODE, R, SEGW, MAXNT, FL | kNorm | kShx>(a, p, s);
     if (a.norm_w) return launch_one<DT, MODE, R, SEGW, MAXNT, FL | kNorm>(a, p, s);
   } else {
     if (a.norm_w) return -1;
   }
+  if constexpr (shx)
+    if (p.G >= 2) return launch_one<DT, MODE, R, SEGW, MAXNT, FL | kShx>(a, p, s);
   return launch_one<DT, MODE, R, SEGW, MAXNT, FL>(a, p, s);
 }
 
@@ -836,6 +896,6 @@ int gq_launch_matvec_pair(int dt0, const MvArgs &a0, int dt1, const MvArgs &a1, 
   if (!a0.norm_w != !a1.norm_w) return 1;
   if (sw0 != 16) return 1;
   /* 4-row groups on both sides, as plan() gives the q/k/v launch */
-  if (a0.norm_w) return launch(mvx_pair_kernel<GQ_Q4_K, 4, GQ_Q6_K, 4, 16, 256, kNorm>, 4, 4);
-  return launch(mvx_pair_kernel<GQ_Q4_K, 4, GQ_Q6_K, 4, 16, 256, 0>, 4, 4);
+  if (a0.norm_w) return launch(mvx_pair_kernel<GQ_Q4_K, 4, GQ_Q6_K, 4, 16, 256, kNorm | kShx>, 4, 4);
+  return launch(mvx_pair_kernel<GQ_Q4_K, 4, GQ_Q6_K, 4, 16, 256, kShx>, 4, 4);
 }
