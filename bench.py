@@ -44,9 +44,10 @@ CTX = 8192
 # are Q6_K alternate with all-Q4_K layers)
 CLASS_KERNELS = {
     "qkv": "mvx_pair_kernel (Q4_K q/k + Q6_K v) / mvx_kernel<Q4_K, STORE> (q/k/v): RMSNorm, "
-           "RoPE and K/V append fused",
-    "attention": "attn_partial_kernel<128, 4, 64> + attn_merge_kernel (split-K partials, merge)",
-    "o_proj": "mvx_kernel<Q4_K, RESID> (o + residual)",
+           "RoPE and K/V append fused, x * w shared in LDS",
+    "attention": "attn_partial_kernel<128, 4, 32> + attn_merge_kernel (split-K partials over 32-position "
+                 "chunks, merge)",
+    "o_proj": "mvx_kernel<Q4_K, RESID> (o + residual, x shared in LDS)",
     "gate_up": "mvm_kernel<Q4_K, SWIGLU> (int8 matrix cores, RMSNorm + SwiGLU fused)",
     "down": "mvx_kernel<Q6_K in the unit layout / Q4_K, RESID> (down + residual)",
     "lm_head": "mvm_kernel<Q6_K, STORE> (int8 matrix cores, final RMSNorm fused)",
