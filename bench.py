@@ -45,7 +45,7 @@ CTX = 8192
 CLASS_KERNELS = {
     "qkv": "mvx_pair_kernel (Q4_K q/k + Q6_K v) / mvx_kernel<Q4_K, STORE> (q/k/v): RMSNorm, "
            "RoPE and K/V append fused, x * w shared in LDS",
-    "attention": "attn_partial_kernel<128, 4, 32> + attn_merge_kernel (split-K partials over 32-position "
+    "attention": "attn_partial32_kernel<128, 4> + attn_merge_kernel (split-K partials over 32-position "
                  "chunks, merge)",
     "o_proj": "mvx_kernel<Q4_K, RESID> (o + residual, x shared in LDS)",
     "gate_up": "mvm_kernel<Q4_K, SWIGLU> (int8 matrix cores, RMSNorm + SwiGLU fused)",
