@@ -66,6 +66,38 @@ def test_matvec_vs_oracle(ctx, orc, dt, rows, cols, path):
     __import__("guanaco_amd.hip").hip.lib.gq_hip_free(ctx.h, wd)
 
 
+# Rows of 32 .. 4096 columns: a 256-thread workgroup holds 32 .. 2 row groups
+# (8- to 128-lane groups; below 64 lanes a group is part of a wave), which
+# share x times the norm weights through LDS; Q8_0 rows of 9 and 1 units
+# leave lanes of every group idle.
+NORM_SHAPES = [
+    (Q4_K, 64, 256), (Q4_K, 48, 512), (Q4_K, 96, 1024), (Q4_K, 40, 2048), (Q4_K, 36, 4096),
+    (Q6_K, 64, 512), (Q6_K, 40, 2048), (Q8_0, 40, 32), (Q8_0, 37, 288), (Q8_0, 24, 1024),
+]
+
+
+@pytest.mark.parametrize("dt,rows,cols", NORM_SHAPES)
+def test_matvec_norm_vs_oracle(ctx, orc, dt, rows, cols):
+    """The fused RMSNorm prologue (kernels_cpu.c:242-253, then the matvec of
+    the normalised x) at every row-group count, on the vector-ALU path."""
+    import guanaco_amd.hip as H
+    seed = 0x5E0 + 7 * dt + cols
+    w = orc.synth_quant(dt, seed, rows, cols)
+    x = orc.synth_normal(seed + 1, cols)
+    nw = orc.synth_norm_weight(seed + 2, cols)
+    wd = ctx.upload_weight(w)
+    xb, nwb, yb = ctx.upload(x), ctx.upload(nw), ctx.alloc(4 * rows)
+    with H.matvec_path("valu"):
+        ctx.matvec_norm_dev(dt, wd, rows, cols, xb, nwb, 1e-5, yb)
+        ctx.sync()
+    y = yb.download(count=rows)
+    ref = orc.matvec(dt, w, rows, cols, orc.rmsnorm(x, nw, 1e-5))
+    assert rel_l2(y, ref) < MV_TOL
+    assert np.abs(y - ref).max() <= MV_TOL * np.abs(ref).max()
+    xb.free(), nwb.free(), yb.free()
+    H.lib.gq_hip_free(ctx.h, wd)
+
+
 def test_matvec_error_codes(ctx):
     """The vtable convention (quant_matvec_q4_k.c:143-158, test_backend.c:71-86):
     NULL/zeroed tensor -1, cols % 256 -2, short byte_size -3."""
