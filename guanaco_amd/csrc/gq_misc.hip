@@ -238,9 +238,12 @@ __global__ __launch_bounds__(kThreads) void copy_kernel(const uint4 *src, uint4 
  * grid apart before it uses any, folds them into an XOR, and writes only in
  * the (data-dependent, practically never taken) case that the XOR equals a
  * marker, so the loads cannot be dropped and the kernel stores nothing.  The
- * floor a launch of this many bytes can reach: what the decode kernels'
+ * grid covers the bytes in one pass at every size (a grid capped at 4096
+ * workgroups, looping, read 431 MB at 4.9 TB/s against 5.9 in one pass).
+ * The floor a launch of this many bytes can reach: what the decode kernels'
  * durations are set beside. */
-__global__ __launch_bounds__(kThreads) void stream_read_kernel(const uint4 *src, size_t n16, uint32_t *sink) {
+__global__ __launch_bounds__(kThreads) void stream_read_kernel(const uint4 *src, size_t n16, uint32_t *sink,
+                                                               unsigned sink_n) {
   const size_t stride = (size_t)gridDim.x * kThreads;
   uint32_t acc = 0;
   /* every pass issues all eight loads (those past the end masked off)
@@ -252,7 +255,7 @@ __global__ __launch_bounds__(kThreads) void stream_read_kernel(const uint4 *src,
 #pragma unroll
     for (int k = 0; k < 8; k++) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
   }
-  if (acc == 0x9E3779B9u) gst<uint32_t>(sink + blockIdx.x, acc);
+  if (acc == 0x9E3779B9u) gst<uint32_t>(sink + blockIdx.x % sink_n, acc);
 }
 
 /* ---- synthetic fills: one thread per 4 output bytes / one float ---- */
@@ -356,10 +359,11 @@ int gq_launch_copy(void *dst, const void *src, size_t bytes, int n_cu, hipStream
 int gq_launch_stream_read(const void *src, size_t bytes, uint32_t *sink, size_t sink_n, hipStream_t s) {
   if ((bytes & 15) || ((uintptr_t)src & 15) || !sink) return -1;
   const size_t n16 = bytes / 16;
-  /* eight loads per thread in one pass where the grid allows it */
-  const size_t blocks = std::min((n16 + 8 * kThreads - 1) / (8 * kThreads), sink_n);
-  if (!blocks) return 0;
-  hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, s, (const uint4 *)src, n16, sink);
+  /* eight loads per thread, one pass */
+  const size_t blocks = (n16 + 8 * kThreads - 1) / (8 * kThreads);
+  if (!blocks || !sink_n || blocks > 0x7fffffffu) return blocks ? -1 : 0;
+  hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, s, (const uint4 *)src, n16, sink,
+                     (unsigned)std::min<size_t>(sink_n, 0xffffffffu));
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 

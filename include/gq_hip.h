@@ -392,7 +392,7 @@ int gq_hip_set_prefill_mode(gq_ctx *ctx, int mode);
 int gq_hip_copy_dev(gq_ctx *ctx, void *dst, const void *src, size_t bytes);
 /* Average device time (ms) of one launch of a read-only streaming kernel
  * over `bytes` (a multiple of 16): eight 16-byte loads per thread issued
- * before use, nothing stored.  Launch i reads src + (i mod n_buf) * stride,
+ * before use, a grid that covers the bytes in one pass, nothing stored.  Launch i reads src + (i mod n_buf) * stride,
  * so src must hold (n_buf - 1) * stride + bytes bytes (stride >= bytes when
  * n_buf > 1, a multiple of 16); 1 untimed + n_iter timed launches between
  * HIP events on the context stream.  No reference counterpart: the floor a
