@@ -641,7 +641,8 @@ __global__ __launch_bounds__(MAXNT) void mvx_kernel(MvArgs a, MxPlan p) {
 
 /* Two MV_STORE launches of different dtypes over the same x in one grid:
  * workgroups [0, p1.nwg) run the second, the rest the first (Q4_K q/k and
- * Q6_K v of a Q4_K_M layer). */
+ * Q6_K v of a Q4_K_M layer; v from its unit-layout copy where bind made one:
+ * 8B decode 514.9-515.1 -> 515.2-515.9 tok/s). */
 template <int DT0, int R0, int DT1, int R1, int SEGW, int MAXNT, int FL>
 __global__ __launch_bounds__(MAXNT) void mvx_pair_kernel(MvArgs a0, MxPlan p0, MvArgs a1, MxPlan p1) {
   __shared__ float red[(MAXNT / SEGW) * ((R0 > R1 ? R0 : R1) + 1)];
@@ -881,21 +882,28 @@ int gq_launch_matvec_pair(int dt0, const MvArgs &a0, int dt1, const MvArgs &a1, 
     return 1;
   const int t0 = check_args(MV_STORE, a0), t1 = check_args(MV_STORE, a1);
   if (t0 <= 0 || t1 <= 0) return -1;
+  /* the Q6_K side from its unit-layout copy when one is given (bit-identical
+   * outputs, aligned loads) */
+  const bool ux = a1.dx && a1.nseg == 1 && (a1.cols / 256) % 2 == 0 && g_path != 3;
+  MvArgs b1 = a1;
+  if (ux) b1.seg[0].w = a1.dx;
   MxPlan p0, p1;
   int r0, r1, sw0, sw1, m0, m1;
   plan(GQ_Q4_K, MV_STORE, a0, t0, p0, r0, sw0, m0);
-  plan(GQ_Q6_K, MV_STORE, a1, t1, p1, r1, sw1, m1);
+  plan(ux ? GQ_Q6_KX : GQ_Q6_K, MV_STORE, b1, t1, p1, r1, sw1, m1);
   /* one block shape for both sides */
   if (p0.G * p0.L != p1.G * p1.L || sw0 != sw1 || m0 != 256 || m1 != 256 || p0.L % 64) return 1;
   auto launch = [&](auto kern, int ra, int rb) {
     p0.nwg = ((t0 + ra - 1) / ra + p0.G - 1) / p0.G;
     p1.nwg = ((t1 + rb - 1) / rb + p1.G - 1) / p1.G;
-    hipLaunchKernelGGL(kern, dim3(p0.nwg + p1.nwg), dim3(p0.G * p0.L), 0, s, a0, p0, a1, p1);
+    hipLaunchKernelGGL(kern, dim3(p0.nwg + p1.nwg), dim3(p0.G * p0.L), 0, s, a0, p0, b1, p1);
     return hipGetLastError() == hipSuccess ? 0 : -4;
   };
   if (!a0.norm_w != !a1.norm_w) return 1;
   if (sw0 != 16) return 1;
   /* 4-row groups on both sides, as plan() gives the q/k/v launch */
+  if (ux && a0.norm_w) return launch(mvx_pair_kernel<GQ_Q4_K, 4, GQ_Q6_KX, 4, 16, 256, kNorm | kShx>, 4, 4);
+  if (ux) return launch(mvx_pair_kernel<GQ_Q4_K, 4, GQ_Q6_KX, 4, 16, 256, kShx>, 4, 4);
   if (a0.norm_w) return launch(mvx_pair_kernel<GQ_Q4_K, 4, GQ_Q6_K, 4, 16, 256, kNorm | kShx>, 4, 4);
   return launch(mvx_pair_kernel<GQ_Q4_K, 4, GQ_Q6_K, 4, 16, 256, kShx>, 4, 4);
 }

@@ -979,8 +979,12 @@ static int op_qkv(gq_ctx *c, int l, int pos, const int *pos_dev, float *hidden) 
         done[j] = true;
       }
   }
-  /* Q4_K q, k and Q6_K v (the Q4_K_M mix): one paired launch */
+  /* Q4_K q, k and Q6_K v (the Q4_K_M mix): one paired launch, v from its
+   * unit-layout copy where bind made one */
   if (ng == 2) {
+    if (gdt[1] == GQ_Q6_K && g[1].nseg == 1 && g[1].seg[0].w == (const uint8_t *)L.wv.data && (size_t)l < c->mm.size() &&
+        !gq_matvec_q6k_ref())
+      g[1].dx = c->mm[l].ux[2];
     const int rc = gq_launch_matvec_pair(gdt[0], g[0], gdt[1], g[1], c->stream);
     if (rc <= 0) {
       if (rc == 0) mark(c, PC_QKV, bytes);
