@@ -217,3 +217,8 @@ def test_time_read_floor_kernel(ctx):
     assert H.lib.gq_hip_time_read(ctx.h, buf.ptr, 4 << 20, 2 << 20, 2, 4) < 0  # regions overlap
     assert np.array_equal(buf.download(count=16), np.arange(16, dtype=np.float32))  # nothing stored
     buf.free()
+    # one pass at any size: 272 MiB takes 8704 workgroups, more than the
+    # 4096-entry sink the (never taken) marker store indexes modulo
+    big = ctx.alloc(272 << 20)
+    assert H.lib.gq_hip_time_read(ctx.h, big.ptr, 272 << 20, 0, 1, 2) > 0
+    big.free()
