@@ -58,8 +58,8 @@ __device__ __forceinline__ float dpp_f(float v) {
 /* quad_perm controls: broadcast lane 0/1/2/3 of the quad, and the pair
  * selections [0,0,2,2] / [1,1,3,3] */
 constexpr int kQuad0 = 0x00, kQuad1 = 0x55, kQuad2 = 0xAA, kQuad3 = 0xFF, kQuadEven = 0xA0, kQuadOdd = 0xF5;
-/* [0,0,1,1] and [2,2,3,3] */
-constexpr int kQuadLoPair = 0x50, kQuadHiPair = 0xFA;
+/* [0,0,1,1] and [2,2,3,3]; [1,0,3,2] */
+constexpr int kQuadLoPair = 0x50, kQuadHiPair = 0xFA, kQuadSwap = 0xB1;
 
 __device__ __forceinline__ float sum4(const float4 &v) { return (v.x + v.y) + (v.z + v.w); }
 
@@ -617,8 +617,9 @@ __device__ __forceinline__ void mvx_body(const MvArgs &a, const MxPlan &p, int b
      * (kernels_cpu.c:415-429: products and difference rounded apart);
      * rows 2m, 2m+1 are in the same group */
     const float2 cs = scs[d >> 1];
-    float partner;
-    GQ_ROWSUM(ei ^ 1, partner);
+    /* the partner row is the adjacent lane's (P is even, so row parity is
+     * lane parity), active here with this one: its finished sum by DPP */
+    const float partner = dpp_f<kQuadSwap>(val);
     const float x0 = (d & 1) ? partner : val, x1 = (d & 1) ? val : partner;
     val = (d & 1) ? x0 * cs.y + x1 * cs.x : x0 * cs.x - x1 * cs.y;
   }
