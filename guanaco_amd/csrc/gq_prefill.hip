@@ -29,6 +29,10 @@
  * row, its k-octets), so a weight is converted once per token tile and never
  * round-trips through LDS in bf16.  One barrier per step.
  *
+ * The fused Q4_K gate/up launch runs a wide variant of the tile when its grid
+ * fills the GPU: 64 rows per wave, so each A operand read feeds two MFMAs
+ * (pgemm_wide_swiglu_kernel).
+ *
  * MFMA operand layout (32x32x16, checked on the device): A[i][k] is element
  * k % 8 of lane i + 32 (k / 8); B[k][j] element k % 8 of lane j + 32 (k / 8);
  * D[i][j] element 4 (i / 8) + i % 4 of lane j + 32 ((i / 4) % 2).
@@ -649,6 +653,193 @@ __global__ __launch_bounds__(kPThreads * KS) void pgemm_kernel(PgArgs a) {
   }
 }
 
+/* Q4_K for waves of 64 rows: per step 64 rows x 48 bytes (header + the
+ * chunk's 32 quant bytes), three 1-KB DMA instructions, every piece used. */
+struct PW4W {
+  static constexpr int kRowLds = 48;
+  static constexpr int kWaveLds = 3072;
+  static constexpr int kDma = 3;
+  struct Plan {
+    uint32_t off[3];
+    bool qs[3];
+  };
+  __device__ static void plan(Plan &p, int lane, uint32_t rowbytes) {
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+      const int pc = 64 * i + lane, row = pc / 3, part = pc - 3 * row;
+      p.qs[i] = part != 0;
+      p.off[i] = (uint32_t)row * rowbytes + 16u * (uint32_t)part;
+    }
+  }
+  __device__ static void issue(const Plan &p, const uint8_t *w, int s, uint32_t lds) {
+#pragma unroll
+    for (int i = 0; i < 3; i++)
+      dma16(w + p.off[i] + (size_t)(s >> 2) * 144 + (p.qs[i] ? 32 * (s & 3) : 0),
+            __builtin_amdgcn_readfirstlane(lds + 1024u * i));
+  }
+  /* row block rb: rows 32 rb + lane % 32 */
+  __device__ static void read(PW<GQ_Q4_K>::Raw &w, const GQ_LDS uint8_t *ws, int lane, int rb) {
+    const uint32_t r = (uint32_t)(lane & 31) + 32u * (uint32_t)rb, h = (uint32_t)(lane >> 5);
+    w.hd = lld<uint4>(ws, r * kRowLds);
+    w.q0 = lld<uint2>(ws, r * kRowLds + 16u + 8u * h);
+    w.q1 = lld<uint2>(ws, r * kRowLds + 32u + 8u * h);
+  }
+};
+
+/* The wide tile: each wave owns 64 weight rows (two 32-row blocks) for 32 TT
+ * tokens, so every A operand read from LDS feeds two MFMAs, and a step holds
+ * twice the matrix work of the 32-row tile: the DMA issued two steps ahead
+ * has twice as long to land, and there is one barrier per 32 MFMAs instead
+ * of per 16.  X takes a 3-slot ring; the weights need only 2 slots, since a
+ * step's bytes are read in the iteration before their own.  At TT = 4 the
+ * ring is 3 x 16 + 2 x 12 KB = 72 KB, so two workgroups share a CU (two waves
+ * per SIMD, 225 VGPRs).  Fused gate/up + SwiGLU at 512 tokens (Q4_K, 2 x
+ * 14336 x 4096): 145 us against 172 us on the 32-row tile (kernel trace),
+ * 512-token forward 13.56 -> 12.74 ms.  The STORE / RESID launches (o,
+ * down, q/k/v) keep the 32-row tile: there the wide tile needs twice the K
+ * parts for the same number of workgroups, and measured slower (q/o 45.8
+ * against 39.0 us, forward 14.2 ms). */
+template <int TT>
+constexpr int wide_ring_bytes() {
+  return 3 * x_bytes<TT>() + 2 * 4 * PW4W::kWaveLds;
+}
+
+template <int TT>
+__device__ __forceinline__ void tile_loop_wide(const PgArgs &a, const uint8_t *w, uint32_t rowbytes, int t0,
+                                               GQ_LDS uint8_t *smem, gq_f32x16 (&acc)[2][TT]) {
+  constexpr int XB = x_bytes<TT>();
+  constexpr int WSB = 4 * PW4W::kWaveLds;
+  constexpr int NPS = TT + PW4W::kDma;
+  constexpr int kRing = 3;
+  static_assert((kRing - 2) * NPS < 64, "vmcnt");
+  const int lane = threadIdx.x & 63, rw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ns = a.K / kBK / a.kparts, s0 = (int)blockIdx.z * ns;
+  PW4W::Plan pl;
+  PW4W::plan(pl, lane, rowbytes);
+  const uint32_t sbase = (uint32_t)(uintptr_t)smem;
+  const uint32_t wreg = (uint32_t)(kRing * XB + rw * PW4W::kWaveLds);
+  const __bf16 *xsrc[TT];
+#pragma unroll
+  for (int j = 0; j < TT; j++) {
+    const int tl = 8 * (TT * rw + j) + (lane >> 3), q = lane & 7;
+    const int oct = q ^ ((tl >> 1) & 7);
+    xsrc[j] = a.x + (size_t)min(t0 + tl, a.T - 1) * a.K + 8 * oct;
+  }
+  auto issue = [&](int st) {
+    const uint32_t xslot = sbase + (uint32_t)((st % kRing) * XB);
+    const int s = s0 + st;
+#pragma unroll
+    for (int j = 0; j < TT; j++)
+      dma16(xsrc[j] + s * kBK, __builtin_amdgcn_readfirstlane(xslot + 1024u * (uint32_t)(TT * rw + j)));
+    PW4W::issue(pl, w, s, sbase + wreg + (uint32_t)((st & 1) * WSB));
+  };
+  for (int st = 0; st < kRing - 1 && st < ns; st++) issue(st);
+#pragma unroll
+  for (int r = 0; r < 2; r++)
+#pragma unroll
+    for (int i = 0; i < TT; i++) acc[r][i] = gq_f32x16{};
+  const int h = lane >> 5, i32 = lane & 31;
+  uint32_t aoff[4][TT];
+#pragma unroll
+  for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+    for (int i = 0; i < TT; i++) {
+      const int tl = 32 * i + i32, q = (2 * kk + h) ^ ((tl >> 1) & 7);
+      aoff[kk][i] = (uint32_t)((tl * 8 + q) * 16);
+    }
+  auto wslot = [&](int st) { return smem + wreg + (st & 1) * WSB; };
+  gq_bf16x8 b[2][4], av[2][TT];
+  PW<GQ_Q4_K>::Raw raw[2];
+  wait_groups<NPS, kRing - 2>(ns - 1);
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 2; r++) PW4W::read(raw[r], wslot(0), lane, r);
+#pragma unroll
+  for (int r = 0; r < 2; r++) PW<GQ_Q4_K>::dequant(raw[r], s0, b[r]);
+  for (int s = 0; s < ns; s++) {
+    /* this wave's copies of step s + 1 have landed once only later steps'
+     * remain; the barrier extends that to every wave and frees the X slot
+     * of step s - 1 and the weight slot of step s (read in iteration s - 1)
+     * for step s + 2 */
+    if (s + 1 < ns) wait_groups<NPS, kRing - 3>(ns - 2 - s);
+    __syncthreads();
+    if (s + kRing - 1 < ns) issue(s + kRing - 1);
+    const GQ_LDS uint8_t *xc = smem + (s % kRing) * XB;
+    /* A operands one k-slice ahead of the MFMAs that use them */
+#pragma unroll
+    for (int i = 0; i < TT; i++) av[0][i] = lld<gq_bf16x8>(xc, aoff[0][i]);
+    const bool more = s + 1 < ns;
+    if (more) {
+#pragma unroll
+      for (int r = 0; r < 2; r++) PW4W::read(raw[r], wslot(s + 1), lane, r);
+    }
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+      if (kk < 3) {
+#pragma unroll
+        for (int i = 0; i < TT; i++) av[(kk + 1) & 1][i] = lld<gq_bf16x8>(xc, aoff[kk + 1][i]);
+      }
+#pragma unroll
+      for (int i = 0; i < TT; i++)
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+          acc[r][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[kk & 1][i], b[r][kk], acc[r][i], 0, 0, 0);
+    }
+    if (more) {
+#pragma unroll
+      for (int r = 0; r < 2; r++) PW<GQ_Q4_K>::dequant(raw[r], s0 + s + 1, b[r]);
+    }
+  }
+}
+
+/* Fused gate/up + SwiGLU over Q4_K weights on the wide tile.  Grid: x = 128
+ * gate rows (with the same 128 up rows), y = token tiles of 32 TT; 256
+ * threads.  Waves 0/1 take gate rows 0-63 / 64-127 of the tile, waves 2/3 the
+ * same up rows.  Each output is the same sum in the same order as
+ * pgemm_kernel's (MFMAs over the steps, k-slices in order), so the two agree
+ * bit for bit; the epilogue is pgemm_kernel's. */
+template <int TT>
+__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void pgemm_wide_swiglu_kernel(PgArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t pg_smem[];
+  GQ_LDS uint8_t *smem = (GQ_LDS uint8_t *)pg_smem;
+  const int lane = threadIdx.x & 63, rw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int t0 = blockIdx.y * 32 * TT;
+  const PgSeg &S = a.seg[rw >> 1];
+  const int r0 = blockIdx.x * 128 + 64 * (rw & 1);
+  const uint32_t rowbytes = (uint32_t)(a.K / 256) * 144u;
+  gq_f32x16 acc[2][TT];
+  tile_loop_wide<TT>(a, S.w + (size_t)r0 * rowbytes, rowbytes, t0, smem, acc);
+  __syncthreads(); /* the ring is free */
+  GQ_LDS float *xch = (GQ_LDS float *)smem;
+  if (rw >= 2) {
+#pragma unroll
+    for (int r = 0; r < 2; r++)
+#pragma unroll
+      for (int i = 0; i < TT; i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) xch[((((rw - 2) * 2 + r) * TT + i) * 16 + e) * 64 + lane] = acc[r][i][e];
+  }
+  __syncthreads();
+  if (rw < 2) {
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      const int n = r0 + 32 * r + (lane & 31);
+#pragma unroll
+      for (int i = 0; i < TT; i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const int t = t0 + tile_token(i, e, lane);
+          const float g = acc[r][i][e], u = xch[(((rw * 2 + r) * TT + i) * 16 + e) * 64 + lane];
+          const float sig = 1.0f / (1.0f + expf(0.0f - g));
+          const __bf16 v = (__bf16)((g * sig) * u);
+          if (t < a.T) gst<unsigned short>(a.act + (size_t)t * S.rows + n, __builtin_bit_cast(unsigned short, v));
+        }
+    }
+  }
+}
+static_assert(wide_ring_bytes<4>() >= 2 * 2 * 4 * 16 * 64 * 4 && 2 * wide_ring_bytes<4>() <= 160 * 1024,
+              "wide ring: the SwiGLU exchange fits, two workgroups per CU");
+
 /* y = (y +) ((part 0 + part 1) + ...) elementwise over T x rows_total
  * (n4 float4s per part), scattered back to the segments' outputs */
 __global__ void pg_parts_kernel(PgArgs a, size_t n4, int resid) {
@@ -718,6 +909,20 @@ int launch_mode(const PgArgs &a0, int row_tiles, hipStream_t s) {
   PgArgs a = a0;
   a.kparts = 1;
   if (a.kparts_out) *a.kparts_out = 1;
+  /* Q4_K gate/up whose 128-row tiles alone give every CU a workgroup: the
+   * wide tile */
+  if (MODE == MV_SWIGLU && a.seg[0].dtype == GQ_Q4_K && a.seg[0].rows % 128 == 0 &&
+      (a.seg[0].rows / 128) * ((a.T + 127) / 128) >= n_cus()) {
+    static bool attr = false;
+    if (!attr) {
+      (void)hipFuncSetAttribute((const void *)pgemm_wide_swiglu_kernel<4>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                wide_ring_bytes<4>());
+      attr = true;
+    }
+    hipLaunchKernelGGL(pgemm_wide_swiglu_kernel<4>, dim3(a.seg[0].rows / 128, (a.T + 127) / 128, 1), dim3(kPThreads),
+                       wide_ring_bytes<4>(), s, a);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+  }
   bool q4 = false, q6 = false, q6x = false, q8 = false;
   for (int i = 0; i < a.nseg; i++)
     q4 |= a.seg[i].dtype == GQ_Q4_K, q6 |= a.seg[i].dtype == GQ_Q6_K, q6x |= a.seg[i].dtype == GQ_Q6_KX,

@@ -208,6 +208,45 @@ def test_prefill_gate_up_swiglu(ctx, orc, dtype, T, N, K):
     H.lib.gq_hip_free(ctx.h, gd), H.lib.gq_hip_free(ctx.h, ud)
 
 
+@pytest.mark.parametrize("T,N,K", [(512, 14336, 4096), (300, 11008, 2048)])
+def test_prefill_gate_up_wide_tile(ctx, orc, T, N, K):
+    """The fused Q4_K gate/up launch on the wide tile (64 rows per wave),
+    which the launcher takes when the 128-row tiles alone fill the GPU
+    (config 5's 2 x 14336 x 4096; a ragged 300-token case).  Rows are
+    independent, so each half of the rows runs again as a launch of its own,
+    which on 256 CUs takes the 32-row tile without a K split (7168 rows at
+    512 tokens, 5504 at 300): the same sums in the same order, so the halves
+    must agree bit for bit with the wide launch.  Sampled rows are held to
+    the exact-input reference as test_prefill_gate_up_swiglu does."""
+    import guanaco_amd.hip as H
+    seed = 0x5EED ^ (T << 16) ^ N
+    print(f"prefill gate/up wide tile {T}x{N}x{K}", flush=True)
+    wg, wu = orc.synth_quant(S.Q4_K, seed, N, K), orc.synth_quant(S.Q4_K, seed + 1, N, K)
+    x = orc.synth_normal(seed + 2, T * K).reshape(T, K)
+    gd, ud, xd = ctx.upload_weight(wg), ctx.upload_weight(wu), ctx.upload(x)
+    half = N // 2
+    act, sub = ctx.alloc(2 * T * N), ctx.alloc(2 * T * half)
+    assert H.lib.gq_hip_prefill_gate_up_dev(ctx.h, S.Q4_K, gd, ud, N, K, xd.ptr, T, act.ptr) == 0
+    wide = act.download(np.uint16, count=T * N).reshape(T, N)
+    if ctx.info()[0] == 256:
+        rowbytes = K // 256 * 144
+        for r0 in (0, half):
+            assert H.lib.gq_hip_prefill_gate_up_dev(ctx.h, S.Q4_K, gd + r0 * rowbytes, ud + r0 * rowbytes, half, K,
+                                                    xd.ptr, T, sub.ptr) == 0
+            narrow = sub.download(np.uint16, count=T * half).reshape(T, half)
+            assert np.array_equal(wide[:, r0:r0 + half], narrow), r0
+    idx = np.unique(np.concatenate([[0, N - 1], np.random.default_rng(seed).choice(N, 254, replace=False)]))
+    n = idx.size
+    pick = lambda w: np.ascontiguousarray(w.reshape(N, -1)[idx]).reshape(-1)  # noqa: E731
+    xb = bf16_round(x).astype(np.float64)
+    g = xb @ bf16_round(q4k_dequant_kernel_order(pick(wg), n, K)).astype(np.float64).T
+    u = xb @ bf16_round(q4k_dequant_kernel_order(pick(wu), n, K)).astype(np.float64).T
+    got = (wide[:, idx].astype(np.uint32) << 16).view(np.float32)
+    assert rel_l2(got, bf16_round(silu_mul_f32(g, u))) < 1e-3
+    act.free(), sub.free(), xd.free()
+    H.lib.gq_hip_free(ctx.h, gd), H.lib.gq_hip_free(ctx.h, ud)
+
+
 @pytest.mark.parametrize("nh,nkv,hd,pre,T,ms", [
     (32, 8, 128, 0, 512, 640),     # config 5: a 512-token chunk from position 0
     (32, 8, 128, 300, 200, 640),   # after a cached prefix
