@@ -208,14 +208,15 @@ def test_prefill_gate_up_swiglu(ctx, orc, dtype, T, N, K):
     H.lib.gq_hip_free(ctx.h, gd), H.lib.gq_hip_free(ctx.h, ud)
 
 
-@pytest.mark.parametrize("T,N,K", [(512, 14336, 4096), (300, 11008, 2048)])
+@pytest.mark.parametrize("T,N,K", [(512, 14336, 4096), (300, 11008, 2048), (257, 11008, 1024)])
 def test_prefill_gate_up_wide_tile(ctx, orc, T, N, K):
     """The fused Q4_K gate/up launch on the wide tile (64 rows per wave),
     which the launcher takes when the 128-row tiles alone fill the GPU
-    (config 5's 2 x 14336 x 4096; a ragged 300-token case).  Rows are
+    (config 5's 2 x 14336 x 4096; ragged 300- and 257-token cases, the
+    last with one token in its last tile).  Rows are
     independent, so each half of the rows runs again as a launch of its own,
     which on 256 CUs takes the 32-row tile without a K split (7168 rows at
-    512 tokens, 5504 at 300): the same sums in the same order, so the halves
+    512 tokens, 5504 at 300 and 257): the same sums in the same order, so the halves
     must agree bit for bit with the wide launch.  Sampled rows are held to
     the exact-input reference as test_prefill_gate_up_swiglu does."""
     import guanaco_amd.hip as H
