@@ -100,6 +100,7 @@ struct MmPlan {
   int planes, pwb;  /* without AREG: LDS offset of the waves' digit planes, bytes per wave */
   int eb;           /* without AREG: LDS offset of the waves' block exponents (32 bytes each) */
   int park;         /* LDS offset of the finished outputs (16 floats per tile) */
+  int red;          /* NB: LDS offset of the tiles' per-wave row sums (16 x NW floats per tile) */
   int total;        /* output rows (MV_SWIGLU: gate rows) */
 };
 
@@ -343,9 +344,29 @@ struct MmTr<GQ_Q6_K> {
  * the tile-interleaved tensor, one contiguous range (16 * BB * cb bytes)
  * into ring slot `buf` in 1 KB instructions; for MV_RESID with c == 0 also
  * the tile's residual values into rbuf.  Returns their count. */
-template <int MODE, int NW, int BB>
+template <int MODE, int NW, int BB, bool NB>
 __device__ __forceinline__ int mm_issue(const MvArgs &a, const MvSegs &sv, const MmPlan &pl, int t, int c,
                                         GQ_LDS uint8_t *buf, GQ_LDS float *rbuf, int wave, int lane) {
+  if constexpr (NB) {
+    /* only the blocks this wave computes (wave + s NW of the stage), each 16
+     * rows x BB bytes contiguous, so no other wave reads what it copies */
+    constexpr int RB = 16 * BB, NI = (RB + 1023) / 1024;
+    const uint8_t *src = a.mm + ((size_t)t * pl.nb + (size_t)c * pl.cb) * RB;
+    const uint32_t base = (uint32_t)(uintptr_t)buf;
+    int cnt = 0;
+    for (int sb = 0; sb < pl.bpc; sb++) {
+      const int bl = wave + sb * NW;
+      if (bl >= pl.cb) break;
+#pragma unroll
+      for (int i = 0; i < NI; i++) {
+        const uint32_t o = (uint32_t)(bl * RB + i * 1024);
+        const uint32_t d = __builtin_amdgcn_readfirstlane(base + o);
+        if (i * 1024 + 16 * lane < RB) dma16(src + o + 16 * lane, d);
+        cnt++;
+      }
+    }
+    return cnt;
+  }
   const int sb = 16 * BB * pl.cb;
   copy_range(a.mm + ((size_t)t * pl.nb + (size_t)c * pl.cb) * (16 * BB), sb, buf, wave, lane, NW);
   int cnt = copy_count(sb, wave, NW);
@@ -364,7 +385,7 @@ __device__ __forceinline__ int mm_issue(const MvArgs &a, const MvSegs &sv, const
  * MAXB blocks, every chunk); otherwise the digit planes stay in LDS (up to
  * 8 blocks per wave) and each stage loads the A operands of its MAXB
  * blocks per wave, for rows longer than registers hold. */
-template <int DT, int MODE, int NW, int MAXB, int NS, bool AREG>
+template <int DT, int MODE, int NW, int MAXB, int NS, bool AREG, bool NB>
 __global__ __launch_bounds__(NW * GQ_WAVE) void mvm_kernel(MvArgs a, MmPlan pl) {
   using T = typename MmTr<DT>::type;
   static_assert(NS >= 3, "ring of NS stage slots, NS - 1 stages in flight");
@@ -382,7 +403,7 @@ __global__ __launch_bounds__(NW * GQ_WAVE) void mvm_kernel(MvArgs a, MmPlan pl) 
   const int nst = mytiles * pl.nch;
   auto issue = [&](int q) -> int { /* stage q into slot q % NS */
     const int tl = q / pl.nch;
-    return mm_issue<MODE, NW, T::BB>(a, sv, pl, bid + tl * nblk, q - tl * pl.nch, lds + (q % NS) * pl.stride,
+    return mm_issue<MODE, NW, T::BB, NB>(a, sv, pl, bid + tl * nblk, q - tl * pl.nch, lds + (q % NS) * pl.stride,
                                      lres + (tl % kRing) * 16, wave, lane);
   };
 
@@ -485,7 +506,9 @@ __global__ __launch_bounds__(NW * GQ_WAVE) void mvm_kernel(MvArgs a, MmPlan pl) 
       for (int j = 1; j < NS - 1; j++) pend += cnt[j];
       wait_vmcnt(pend);
     }
-    __syncthreads();
+    /* NB: only the first (x converted by every wave before stages land in its
+     * slots; the sums of squares): each wave reads only what it copied */
+    if (!NB || k == 0) __syncthreads();
     /* stages up to k + NS - 1 (the first iteration also those x held back),
      * into the slots of stages already computed; issued after this stage's
      * LDS reads and MFMAs, so that the wait for room in the memory pipeline
@@ -513,7 +536,7 @@ __global__ __launch_bounds__(NW * GQ_WAVE) void mvm_kernel(MvArgs a, MmPlan pl) 
       rscale = 1.0f / sqrtf(tot);
       have_rscale = true;
     }
-    if (k > 0 && c == 0 && lane < RPW) { /* rows of the tile completed at k-1 */
+    if (!NB && k > 0 && c == 0 && lane < RPW) { /* rows of the tile completed at k-1 */
       const int tl = (k - 1) / pl.nch, r = wave * RPW + lane;
       if (MODE != MV_SWIGLU || r < 8) {
         const int tp = MODE == MV_SWIGLU ? r + 8 : r ^ 1;
@@ -598,11 +621,35 @@ __global__ __launch_bounds__(NW * GQ_WAVE) void mvm_kernel(MvArgs a, MmPlan pl) 
       float v = acc;
       v += __shfl_xor(v, 16, 64);
       v += __shfl_xor(v, 32, 64);
-      if (lane < 16) sh.red[(k / pl.nch) & 1][lane][wave] = v;
+      if (lane < 16) {
+        if constexpr (NB)
+          lst<float>(lds, (uint32_t)pl.red + 4u * (uint32_t)(((k / pl.nch) * 16 + lane) * NW + wave), v);
+        else
+          sh.red[(k / pl.nch) & 1][lane][wave] = v;
+      }
       acc = 0.f;
     }
   }
   __syncthreads();
+  if constexpr (NB) {
+    /* plain stores only (the launcher takes NB for MV_STORE without RoPE):
+     * every wave's row sums of every tile are in; wave w finishes and stores
+     * tiles w, w + NW, ... (lane r: row r), the sums in the same order */
+    for (int tl = wave; tl < mytiles; tl += NW) {
+      const int t = bid + tl * nblk, r = lane;
+      int s = 0, lr = 0;
+      gq_mv_locate(sv, 16 * t, s, lr);
+      s = __builtin_amdgcn_readfirstlane(s);
+      lr = __builtin_amdgcn_readfirstlane(lr) + r;
+      if (r >= 16 || lr >= gq_mv_rows(sv, s)) continue;
+      float v = 0.f;
+#pragma unroll
+      for (int j = 0; j < NW; j++) v += lld<float>(lds, (uint32_t)pl.red + 4u * (uint32_t)((tl * 16 + r) * NW + j));
+      float *dst = rdest<MODE>(a, sv, s, lr, pos);
+      if (dst) gst<float>(dst, v * rscale);
+    }
+    return;
+  }
   /* the parked rows go out: wave w stores tiles w, w + NW, ..., so the
    * segment of a tile is uniform across the wave */
   const int prow = MODE == MV_SWIGLU ? 8 : 16;
@@ -633,11 +680,17 @@ constexpr int kMmWaves = 8; /* waves per workgroup (4 measured 18.4-19.0 us on g
 constexpr size_t kMmLds = 160 * 1024; /* LDS of a CU (gfx950) */
 constexpr int kMmNs = 3;    /* ring slots (4 and 6 measured slower: 16.5 and 20.0 us on gate/up) */
 constexpr int kMmStageCap = 40960; /* bytes of weights per stage at most */
+/* Plain-store workgroups (no RoPE, no residual) that run at least this many
+ * stages drop the per-stage barrier: each wave copies only the blocks it
+ * computes and the tiles are finished after the loop.  The LM head (64 stages a workgroup at the 8B shape)
+ * measured 88-89 -> 81-84 us; gate/up (7 stages) 14.8 -> 15.4 us, so it
+ * keeps the barrier. */
+constexpr int kMmNbStages = 16;
 
-template <int DT, int MODE, int NW, int MAXB, int NS, bool AREG = true>
+template <int DT, int MODE, int NW, int MAXB, int NS, bool AREG = true, bool NB = false>
 int launch_mm_as(const MvArgs &a, const MmPlan &pl, size_t lds, int grid, hipStream_t s) {
   static bool attr_set = false;
-  auto f = mvm_kernel<DT, MODE, NW, MAXB, NS, AREG>;
+  auto f = mvm_kernel<DT, MODE, NW, MAXB, NS, AREG, NB>;
   if (!attr_set) {
     (void)hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxDynLdsW);
     (void)hipGetLastError(); /* a refusal shows up as the launch's error instead */
@@ -648,9 +701,17 @@ int launch_mm_as(const MvArgs &a, const MmPlan &pl, size_t lds, int grid, hipStr
 }
 
 template <int DT, int MODE, int NW, int NS>
-int launch_mm_b(int maxb, bool areg, const MvArgs &a, const MmPlan &pl, size_t lds, int grid, hipStream_t s) {
+int launch_mm_b(int maxb, bool areg, bool nb, const MvArgs &a, const MmPlan &pl, size_t lds, int grid,
+                hipStream_t s) {
   if (!areg) return pl.bpc <= 1 ? launch_mm_as<DT, MODE, NW, 1, NS, false>(a, pl, lds, grid, s)
                                 : launch_mm_as<DT, MODE, NW, 2, NS, false>(a, pl, lds, grid, s);
+  if constexpr (MODE == MV_STORE) {
+    if (nb) {
+      if (maxb <= 1) return launch_mm_as<DT, MODE, NW, 1, NS, true, true>(a, pl, lds, grid, s);
+      if (maxb <= 2) return launch_mm_as<DT, MODE, NW, 2, NS, true, true>(a, pl, lds, grid, s);
+      return launch_mm_as<DT, MODE, NW, 4, NS, true, true>(a, pl, lds, grid, s);
+    }
+  }
   if (maxb <= 1) return launch_mm_as<DT, MODE, NW, 1, NS>(a, pl, lds, grid, s);
   if (maxb <= 2) return launch_mm_as<DT, MODE, NW, 2, NS>(a, pl, lds, grid, s);
   return launch_mm_as<DT, MODE, NW, 4, NS>(a, pl, lds, grid, s);
@@ -704,15 +765,21 @@ int launch_mm_w(const MvArgs &a, int total, hipStream_t s) {
   const size_t shb = sizeof(MmShared<NW>);
   int grid = 0;
   size_t lds = 0;
+  bool nb = false;
   for (int pc = 2; pc >= 1 && !grid; pc--) {
     const int gr = std::min(pl.ntiles, pc * g_n_cu);
-    const size_t l = (size_t)pl.park + 64 * (size_t)((pl.ntiles + gr - 1) / gr);
-    if (l <= kMaxDynLdsW && pc * (l + shb + 1024) <= kMmLds + 1024) grid = gr, lds = l;
+    const size_t tpw = (size_t)((pl.ntiles + gr - 1) / gr);
+    /* NB (no barrier per stage, the tiles finished after the loop) where a
+     * workgroup runs at least kMmNbStages stages; it needs 16 x NW floats of
+     * row sums per tile */
+    nb = MODE == MV_STORE && !a.rope.cs && areg && tpw * pl.nch >= (size_t)kMmNbStages;
+    const size_t l = (size_t)pl.park + 64 * tpw + (nb ? (size_t)64 * NW * tpw : 0);
+    if (l <= kMaxDynLdsW && pc * (l + shb + 1024) <= kMmLds + 1024) grid = gr, lds = l, pl.red = pl.park + 64 * (int)tpw;
   }
   if (!grid) return 1;
-  if (ns == 3) return launch_mm_b<DT, MODE, NW, 3>(maxb, areg, a, pl, lds, grid, s);
-  if (ns == 4) return launch_mm_b<DT, MODE, NW, 4>(maxb, areg, a, pl, lds, grid, s);
-  return launch_mm_b<DT, MODE, NW, 6>(maxb, areg, a, pl, lds, grid, s);
+  if (ns == 3) return launch_mm_b<DT, MODE, NW, 3>(maxb, areg, nb, a, pl, lds, grid, s);
+  if (ns == 4) return launch_mm_b<DT, MODE, NW, 4>(maxb, areg, nb, a, pl, lds, grid, s);
+  return launch_mm_b<DT, MODE, NW, 6>(maxb, areg, nb, a, pl, lds, grid, s);
 }
 
 template <int DT, int MODE>

@@ -66,6 +66,28 @@ def test_matvec_vs_oracle(ctx, orc, dt, rows, cols, path):
     __import__("guanaco_amd.hip").hip.lib.gq_hip_free(ctx.h, wd)
 
 
+@pytest.mark.parametrize("dt,rows,cols", [(Q6_K, 32776, 4096), (Q4_K, 32768, 8192)])
+def test_matvec_mfma_many_stages(ctx, orc, dt, rows, cols):
+    """Matrix-core launches whose workgroups run 16 or more stages (the
+    LM head's shape class) drop the per-stage barrier: each wave copies only
+    the blocks it computes, and the tiles are finished after the loop.  Q6_K
+    32776 x 4096 (two chunks a row, 8 tiles a workgroup, the last tile
+    half full) and Q4_K 32768 x 8192 (two chunks, 8 tiles) against the
+    oracle, every row."""
+    import guanaco_amd.hip as H
+    seed = 0x5A6E ^ (dt << 20) ^ rows
+    w = orc.synth_quant(dt, seed, rows, cols)
+    x = orc.synth_normal(seed + 1, cols)
+    wd = ctx.upload_weight(w)
+    with H.matvec_path("mfma"):
+        rc, y = ctx.matvec_host(dt, wd, rows, cols, x, byte_size=w.nbytes)
+    assert rc == 0
+    ref = orc.matvec(dt, w, rows, cols, x)
+    assert rel_l2(y, ref) < MV_TOL
+    assert np.abs(y - ref).max() / (np.abs(ref).max() + 1e-30) < 1e-5
+    H.lib.gq_hip_free(ctx.h, wd)
+
+
 # Rows of 32 .. 4096 columns: a 256-thread workgroup holds 32 .. 2 row groups
 # (8- to 128-lane groups; below 64 lanes a group is part of a wave), which
 # share x times the norm weights through LDS; Q8_0 rows of 9 and 1 units
