@@ -50,7 +50,7 @@ CLASS_KERNELS = {
     "o_proj": "mvx_kernel<Q4_K, RESID> (o + residual, x shared in LDS)",
     "gate_up": "mvm_kernel<Q4_K, SWIGLU> (int8 matrix cores, RMSNorm + SwiGLU fused)",
     "down": "mvx_kernel<Q6_K in the unit layout / Q4_K, RESID> (down + residual)",
-    "lm_head": "mvm_kernel<Q6_K, STORE> (int8 matrix cores, final RMSNorm fused)",
+    "lm_head": "mvm_kernel<Q6_K, STORE> (int8 matrix cores, final RMSNorm fused, no per-stage barrier)",
 }
 
 
