@@ -375,8 +375,12 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(AttnArgs a) {
   __shared__ float xm[3][64], xl[3][64], xo[3][ND * 4][64];
   const int lane = threadIdx.x & 63, c = lane & 15, j = lane >> 4;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  /* heavy (late) tiles first */
-  const int tile = gridDim.x - 1 - blockIdx.x, g = blockIdx.y;
+  /* One linear grid: workgroup L runs on XCD L mod 8, and takes KV head
+   * L mod n_kv, so a head's K/V stays in one XCD's L2 (n_kv = 8: one head
+   * per XCD; with tile-major ids every XCD read every head's K/V, 4 MB at
+   * 512 tokens: 49.3 -> 38.6 us per layer).  Heavy (late) tiles first. */
+  const int ntile = gridDim.x / a.n_kv;
+  const int g = blockIdx.x % a.n_kv, tile = ntile - 1 - blockIdx.x / a.n_kv;
   const int t0 = tile * TPT;
   const int last = min(t0 + TPT, a.ntok) - 1;
   const int pmax = a.pos + last; /* last key any row of the tile needs */
@@ -530,7 +534,7 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(AttnArgs a) {
 
 template <int HD, int G>
 int launch_flash(const AttnArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL((flash_prefill_kernel<HD, G>), dim3((a.ntok + 16 / G - 1) / (16 / G), a.n_kv), dim3(256), 0, s,
+  hipLaunchKernelGGL((flash_prefill_kernel<HD, G>), dim3((a.ntok + 16 / G - 1) / (16 / G) * a.n_kv), dim3(256), 0, s,
                      a);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
