@@ -38,8 +38,11 @@ constexpr int kThreads = 256;
 
 __global__ __launch_bounds__(kThreads) void rope_append_kernel(RopeArgs a) {
 #pragma clang fp contract(off)
-  /* token blockIdx.x of a chunk (0 for one token) */
-  const int tz = blockIdx.x;
+  /* token blockIdx.x / n_kv of a chunk (0 for one token), KV head
+   * g = blockIdx.x % n_kv and its G query heads: workgroup L runs on XCD
+   * L mod 8, so head g's K/V rows are written where the flash kernel, which
+   * takes head g on those workgroups, reads them */
+  const int tz = (int)blockIdx.x / a.n_kv, g = (int)blockIdx.x % a.n_kv, G = a.n_heads / a.n_kv;
   const int pos = (a.pos_dev ? *a.pos_dev : a.pos) + tz;
   /* the host rejects positions outside the cache; this keeps a stray
    * device-side position from indexing past the table or the slab */
@@ -49,7 +52,6 @@ __global__ __launch_bounds__(kThreads) void rope_append_kernel(RopeArgs a) {
   const float2 *cs = a.cs + (size_t)pos * half;
   float *q = a.q + (size_t)tz * a.q_stride;
   const float *kin = a.k + (size_t)tz * a.k_stride, *vin = a.v + (size_t)tz * a.v_stride;
-  const int nq = a.n_heads * half, nk = a.n_kv * half;
   /* element o of this token's q | k | v from the GEMM's parts, summed in
    * pg_parts_kernel's order */
   const int qd = a.n_heads * a.hd, kvd = a.n_kv * a.hd;
@@ -76,19 +78,20 @@ __global__ __launch_bounds__(kThreads) void rope_append_kernel(RopeArgs a) {
     }
     return v;
   };
-  for (int t = threadIdx.x; t < nq + nk; t += kThreads) {
-    const bool isq = t < nq;
-    const int u = isq ? t : t - nq;
-    const int h = u / half, i = u - h * half;
+  for (int t = threadIdx.x; t < (G + 1) * half; t += kThreads) {
+    const bool isq = t < G * half;
+    const int u = isq ? t : t - G * half;
+    const int hl = u / half, i = u - hl * half;
+    const int h = isq ? g * G + hl : g;
     const float2 c = cs[i];
     const float2 x = prow ? part2((isq ? 0 : qd) + h * a.hd + 2 * i)
                           : ld2((isq ? (const float *)q : kin) + (size_t)h * a.hd + 2 * i);
     const float2 y = make_float2(x.x * c.x - x.y * c.y, x.x * c.y + x.y * c.x);
     st2(isq ? q + (size_t)h * a.hd + 2 * i : a.kc + ((size_t)h * a.max_seq + p) * a.hd + 2 * i, y);
   }
-  for (int t = 2 * threadIdx.x; t < kvd; t += 2 * kThreads) {
-    const int h = t / a.hd, d = t - h * a.hd;
-    st2(a.vc + ((size_t)h * a.max_seq + p) * a.hd + d, prow ? part2(qd + kvd + t) : ld2(vin + t));
+  for (int d = 2 * threadIdx.x; d < a.hd; d += 2 * kThreads) {
+    const int t = g * a.hd + d;
+    st2(a.vc + ((size_t)g * a.max_seq + p) * a.hd + d, prow ? part2(qd + kvd + t) : ld2(vin + t));
   }
 }
 
@@ -556,7 +559,7 @@ int gq_launch_flash_prefill(const AttnArgs &a, hipStream_t s) {
 }
 
 int gq_launch_rope_append(const RopeArgs &a, hipStream_t s) {
-  if ((a.hd & 1) || a.n_kv <= 0 || a.ntok < 0 || (a.parts && a.kparts < 1)) return -1;
-  hipLaunchKernelGGL(rope_append_kernel, dim3(std::max(a.ntok, 1)), dim3(kThreads), 0, s, a);
+  if ((a.hd & 1) || a.n_kv <= 0 || a.n_heads % a.n_kv || a.ntok < 0 || (a.parts && a.kparts < 1)) return -1;
+  hipLaunchKernelGGL(rope_append_kernel, dim3(std::max(a.ntok, 1) * a.n_kv), dim3(kThreads), 0, s, a);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
